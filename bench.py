@@ -1,0 +1,299 @@
+"""Benchmark of the gated-delta recurrence on one MI355X.
+
+The headline (`value`) is the 48-layer, B=1 decode step with the conv front end: one
+gdn_run call over 48 independent layers, each with its own fp32 state (151 MB of state
+read and written per step). Reported as algorithmic GB/s:
+    313,420,800 B per step = 48 x (6,291,456 state r+w + 238,144 front end, gates, o).
+Secondary lines: B=32 decode (9,714,321,408 B per step), speculative verify (B=8, T=5,
+152,887,168 B), and chunked prefill T=4096 (tokens/s, intra-chunk MFMA FLOP rate).
+
+State sets are rotated so the working set exceeds the 256 MB last-level cache: every
+timed step streams its state from HBM. The CPU baseline runs the oracle's unfused,
+one-pass-per-op restatement of the same step on the host cores.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD spec
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+D = 128
+HK, HV = 16, 48
+C = 2 * HK * D + HV * D          # 10240 conv channels
+METRIC = "gated-delta decode state GB/s (% HBM peak) at B=1,32; prefill tok/s T=4096"
+
+
+def bytes_decode_layer(B: int, conv: bool) -> int:
+    """Algorithmic bytes of one layer's decode step (state r+w, inputs, outputs)."""
+    state = B * HV * D * D * 4 * 2
+    gates = B * HV * 2 * 2 + HV * 4 * 2          # a, b bf16; A_log, dt_bias fp32
+    o = B * HV * D * 2                            # bf16
+    if conv:
+        front = B * C * 2 + B * 3 * C * 2 * 2 + 4 * C * 2   # x, conv state r+w, conv w
+    else:
+        front = B * 2 * HK * D * 2 + B * HV * D * 2         # q, k, v bf16
+    return state + gates + o + front
+
+
+def bytes_verify(B: int, T: int) -> int:
+    state_read = B * HV * D * D * 4
+    states = B * HV * T * D * D * 4
+    x = B * T * C * 2
+    conv_state = B * 3 * C * 2
+    w = 4 * C * 2
+    ab = B * T * HV * 2 * 2
+    params = HV * 4 * 2
+    o = B * T * HV * D * 2
+    return state_read + states + x + conv_state + w + ab + params + o
+
+
+def make_layer_inputs(torch, dev, nl: int, B: int, T: int, conv: bool, seed: int):
+    """Synthetic inputs with the benchmark distributions (torch RNG on the device)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    n = lambda *s: torch.randn(s, device=dev, generator=g)  # noqa: E731
+
+    def unit_bf16(*s):
+        x = n(*s)
+        return (x / x.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+
+    q = unit_bf16(nl, B, T, HK, D)
+    k = unit_bf16(nl, B, T, HK, D)
+    v = n(nl, B, T, HV, D).to(torch.bfloat16)
+    inp = dict(
+        a=n(nl, B, T, HV).to(torch.bfloat16),
+        b=n(nl, B, T, HV).to(torch.bfloat16),
+        A_log=torch.rand((nl, HV), device=dev, generator=g) * 2 - 1,
+        dt_bias=n(nl, HV) * 0.1,
+    )
+    if conv:
+        inp["x"] = torch.cat([q.reshape(nl, B, T, HK * D), k.reshape(nl, B, T, HK * D),
+                              v.reshape(nl, B, T, HV * D)], dim=-1).contiguous()
+        inp["conv_weight"] = (n(nl, 4, C) * 0.1).to(torch.bfloat16)
+        inp["conv_state"] = n(nl, B, 3, C).to(torch.bfloat16)
+    else:
+        inp.update(q=q, k=k, v=v)
+    return inp
+
+
+class Timer:
+    """HIP events on torch's current stream (the stream the library launches on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time_calls(self, fn, steps: int, warmup: int):
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            evs[i][0].record()
+            fn(warmup + i)
+            evs[i][1].record()
+        t1.record()
+        torch.cuda.synchronize()
+        per = sorted(a.elapsed_time(b) for a, b in evs)
+        total = t0.elapsed_time(t1)
+        return dict(ms_per_step=total / steps, launch_ms_avg=sum(per) / len(per),
+                    launch_ms_p10=per[len(per) // 10], launch_ms_p50=per[len(per) // 2],
+                    launch_ms_p90=per[(9 * len(per)) // 10])
+
+
+def bench_decode(torch, gdn, dev, timer, B: int, conv: bool, steps: int, warmup: int,
+                 sets: int):
+    """48-layer decode step, rotating over `sets` independent state sets."""
+    NL = 48
+    inps = [make_layer_inputs(torch, dev, NL, B, 1, conv, seed=100 + s) for s in range(sets)]
+    states = []
+    for s in range(sets):
+        g = torch.Generator(device=dev)
+        g.manual_seed(900 + s)
+        states.append(torch.randn((NL, B, HV, D, D), device=dev, generator=g) * 0.02)
+    o = torch.empty((NL, B, 1, HV, D), dtype=torch.bfloat16, device=dev)
+    conv_out = ([torch.empty((NL, B, 3, C), dtype=torch.bfloat16, device=dev) for _ in range(sets)]
+                if conv else [None] * sets)
+    argsets = []
+    for s in range(sets):
+        i = inps[s]
+        argsets.append(gdn.layer_args(
+            B=B, T=1, n_layers=NL, q=i.get("q"), k=i.get("k"), v=i.get("v"), x=i.get("x"),
+            conv_weight=i.get("conv_weight"), conv_state_in=i.get("conv_state"),
+            conv_state_out=conv_out[s], a=i["a"], b=i["b"], A_log=i["A_log"],
+            dt_bias=i["dt_bias"], state_in=states[s], state_out=states[s], o=o))
+    fn = lambda it: gdn.call_run(argsets[it % sets])  # noqa: E731
+    r = timer.time_calls(fn, steps, warmup)
+    nbytes = NL * bytes_decode_layer(B, conv)
+    r["bytes_per_step"] = nbytes
+    r["GBps"] = nbytes / (r["ms_per_step"] * 1e-3) / 1e9
+    r["kernel_GBps"] = nbytes / (r["launch_ms_avg"] * 1e-3) / 1e9
+    r["state_sets"] = sets
+    r["working_set_MB"] = sets * NL * B * HV * D * D * 4 / 1e6
+    del states, inps
+    return r
+
+
+def bench_verify(torch, gdn, dev, timer, steps: int, warmup: int, sets: int):
+    B, T = 8, 5
+    inps = [make_layer_inputs(torch, dev, 1, B, T, True, seed=300 + s) for s in range(sets)]
+    states_in = [torch.randn((1, B, HV, D, D), device=dev) * 0.02 for _ in range(sets)]
+    outs = [torch.empty((1, B, HV, T, D, D), device=dev) for _ in range(sets)]
+    o = torch.empty((1, B, T, HV, D), dtype=torch.bfloat16, device=dev)
+    argsets = []
+    for s in range(sets):
+        i = inps[s]
+        argsets.append(gdn.layer_args(
+            B=B, T=T, x=i["x"], conv_weight=i["conv_weight"], conv_state_in=i["conv_state"],
+            a=i["a"], b=i["b"], A_log=i["A_log"], dt_bias=i["dt_bias"], state_in=states_in[s],
+            states=outs[s], o=o))
+    r = timer.time_calls(lambda it: gdn.call_run(argsets[it % sets]), steps, warmup)
+    nbytes = bytes_verify(B, T)
+    r["bytes_per_step"] = nbytes
+    r["GBps"] = nbytes / (r["ms_per_step"] * 1e-3) / 1e9
+    r["kernel_GBps"] = nbytes / (r["launch_ms_avg"] * 1e-3) / 1e9
+    return r
+
+
+def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
+    """Device-to-device copy of 604 MB: a practical streaming ceiling for comparison."""
+    n = 4 * 48 * HV * D * D // 2
+    src = [torch.empty(n, device=dev) for _ in range(2)]
+    dst = [torch.empty(n, device=dev) for _ in range(2)]
+    r = timer.time_calls(lambda it: dst[it % 2].copy_(src[it % 2]), steps, 5)
+    return dict(GBps=2 * n * 4 / (r["launch_ms_avg"] * 1e-3) / 1e9, bytes=2 * n * 4)
+
+
+def cpu_baseline(target_seconds: float = 12.0):
+    """The oracle's unfused op sequence for the 48-layer B=1 decode step with the conv
+    front end (one full pass per op over materialised temporaries), on the host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    threads = len(os.sched_getaffinity(0))
+    inps = [O.make_inputs(config=1, layer=l, B=1, L=1, conv=True) for l in range(48)]
+    O.reference_layer(inps[0], materialize=True, threads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for inp in inps:
+            O.reference_layer(inp, materialize=True, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_seconds or reps >= 200:
+            break
+    per_step = el / reps
+    nbytes = 48 * bytes_decode_layer(1, True)
+    return dict(value=nbytes / per_step / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{reps} full 48-layer B=1 decode steps with the conv front end "
+                       f"(oracle, one pass per op, fp32), {per_step * 1e3:.1f} ms per step")
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        return json.load(fh).get(name)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list: decode1,decode32,verify,prefill,copy")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only: the gated-delta path "
+                                   "needs no collectives; use --gpus 1"}))
+        return 2
+
+    import torch
+    import __graft_entry__
+    gdn = __graft_entry__.load_package()
+    if not torch.cuda.is_available() or not gdn.available():
+        print(json.dumps({"error": "no gfx950 GPU visible"}))
+        return 1
+    dev = torch.device("cuda:0")
+    timer = Timer(torch)
+    only = set(filter(None, args.only.split(",")))
+    want = lambda n: not only or n in only  # noqa: E731
+
+    sec = {}
+    head = None
+    if want("decode1"):
+        head = bench_decode(torch, gdn, dev, timer, B=1, conv=True, steps=args.steps,
+                            warmup=args.warmup, sets=4)
+        print(f"# decode B=1 x48 conv: {head['ms_per_step'] * 1e3:.1f} us/step, "
+              f"{head['GBps']:.0f} GB/s", flush=True)
+    if want("decode32"):
+        r = bench_decode(torch, gdn, dev, timer, B=32, conv=False,
+                         steps=max(10, args.steps // 10), warmup=3, sets=2)
+        sec["decode_b32_48_layers"] = dict(
+            GBps=round(r["GBps"], 1), frac_hbm=round(r["GBps"] / HBM_PEAK_GBPS, 4),
+            ms_per_step=round(r["ms_per_step"], 4), bytes_per_step=r["bytes_per_step"])
+        print(f"# decode B=32 x48: {r['ms_per_step']:.3f} ms/step, {r['GBps']:.0f} GB/s", flush=True)
+    if want("verify"):
+        r = bench_verify(torch, gdn, dev, timer, steps=args.steps, warmup=args.warmup, sets=4)
+        sec["verify_b8_t5"] = dict(GBps=round(r["GBps"], 1), frac_hbm=round(r["GBps"] / HBM_PEAK_GBPS, 4),
+                                   us_per_call=round(r["ms_per_step"] * 1e3, 2),
+                                   bytes_per_call=r["bytes_per_step"])
+        print(f"# verify B=8 T=5: {r['ms_per_step'] * 1e3:.1f} us, {r['GBps']:.0f} GB/s", flush=True)
+    if want("copy"):
+        cc = bench_copy_ceiling(torch, dev, timer)
+        sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)
+        print(f"# device copy ceiling: {cc['GBps']:.0f} GB/s", flush=True)
+
+    if head is None:
+        print(json.dumps({"secondary": sec}))
+        return 0
+    cpu = None if args.no_cpu else cpu_baseline()
+    if cpu:
+        print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads", flush=True)
+    achieved = head["kernel_GBps"]
+    line = {
+        "metric": METRIC,
+        "value": round(head["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "48-layer gated-delta decode step, B=1, conv front end + gates "
+                               "+ recurrence (Hk=16, Hv=48, Dk=Dv=128, fp32 state)",
+                   "layers": 48, "batch": 1, "seq_len": 1,
+                   "state_sets_rotated": head["state_sets"],
+                   "working_set_MB": round(head["working_set_MB"], 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": load_traffic("decode_b1_48_layers_conv"),
+                     "kernel_us_avg": round(head["launch_ms_avg"] * 1e3, 2),
+                     "kernel_us_p50": round(head["launch_ms_p50"] * 1e3, 2),
+                     "bytes_per_launch": head["bytes_per_step"]},
+        "cpu_baseline": cpu,
+        "secondary": sec,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

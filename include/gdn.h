@@ -1,0 +1,165 @@
+/*
+ * gdn.h -- C ABI of the MI355X (gfx950) gated-delta recurrence library, libgdn.so.
+ *
+ * One Gated-DeltaNet layer's recurrent core, per the reference's per-layer call:
+ *
+ *   gates   beta  = sigmoid(b),  alpha = exp(-exp(A_log) * softplus(a + dt_bias))
+ *   update  S_t   = alpha_t (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T
+ *   readout o_t   = S_t^T q_t            (taken after the update)
+ *
+ * with the fp32 state of each (batch, v-head) stored (Dv, Dk), Dk contiguous, and
+ * Dk = Dv = 128. q and k carry num_k_heads heads; v-head h reads k-head
+ * h / (num_v_heads / num_k_heads). An optional front end takes the 10240-channel
+ * in_proj_qkv output instead of q,k,v and applies the causal depthwise conv (4 taps),
+ * SiLU, l2norm (eps 1e-6) and the q scale 128^-0.5, with bf16 rounding after every op
+ * as the reference's bf16 MLX ops do.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   gdn_run             delta::run            cpp/src/delta.hpp:66-68 (delta.cpp:137-173),
+ *                       with the gate math of cpp/src/model.cpp:608-612 and, in the conv
+ *                       front end, model.cpp:585-606 and DepthwiseConv model.cpp:385-395;
+ *                       the call site it drops into is model.cpp:622-624.
+ *   gdn_prefill_chunked chunked_delta         python/qwen35.py:365-431
+ *   gdn_commit          DeltaCache::commit    cpp/src/model.cpp:439-457
+ *   gdn_available       delta::available      cpp/src/delta.hpp:51 (delta.cpp:133-135)
+ *
+ * Conventions
+ *   - Every pointer is device memory owned by the caller; the library allocates no
+ *     device memory on any entry point and keeps no per-call state.
+ *   - All tensors are dense, row-major, with a leading n_layers dimension: layer l of
+ *     a tensor of per-layer size N starts at element l*N. n_layers > 1 runs that many
+ *     independent layers in one launch (the layers of a model evaluated together, or
+ *     a benchmark); n_layers = 1 is the reference's per-layer call.
+ *   - Work is ordered on `stream` (a hipStream_t; NULL is the null stream). No entry
+ *     point synchronises the device. Entry points are thread-safe.
+ *   - Errors never cross the ABI as exceptions. A non-zero return names the class of
+ *     error; gdn_last_error() returns this thread's message for the last failure.
+ *     Shapes the kernels do not implement are errors, never a silent fallback.
+ */
+#ifndef GDN_H
+#define GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+#define GDN_HEAD_DIM 128 /* Dk = Dv */
+#define GDN_CONV_TAPS 4  /* conv kernel size; the conv state holds GDN_CONV_TAPS-1 rows */
+
+typedef enum gdn_status {
+  GDN_OK = 0,
+  GDN_EINVAL = 1,      /* bad argument: null, shape, overlap, alignment, enum value */
+  GDN_EUNSUPPORTED = 2, /* no gfx950 device */
+  GDN_EDEVICE = 3      /* a HIP call failed; the message carries the HIP error */
+} gdn_status;
+
+typedef enum gdn_dtype { GDN_DTYPE_BF16 = 0, GDN_DTYPE_F32 = 1 } gdn_dtype;
+
+typedef enum gdn_frontend {
+  GDN_FRONTEND_QKV = 0, /* q, k, v given (already normalised, as delta::run takes them) */
+  GDN_FRONTEND_CONV = 1 /* x = in_proj_qkv output; conv + SiLU + l2norm + q scale inside */
+} gdn_frontend;
+
+typedef enum gdn_gate_mode {
+  GDN_GATES_RAW = 0,        /* a, b logits with A_log, dt_bias: the gate math runs inside */
+  GDN_GATES_PRECOMPUTED = 1 /* alpha, beta given in fp32, as delta::run takes them */
+} gdn_gate_mode;
+
+typedef enum gdn_states_layout {
+  GDN_STATES_BHT = 0, /* (B, Hv, T, Dv, Dk): the reference's S_all order (delta.cpp:88) */
+  GDN_STATES_TBH = 1  /* (T, B, Hv, Dv, Dk): step t is one contiguous state, so a commit
+                         can adopt it by pointer */
+} gdn_states_layout;
+
+/* Shapes below omit the leading n_layers dimension. C = 2*Hk*128 + Hv*128. */
+typedef struct gdn_layer_args {
+  int n_layers;    /* >= 1 */
+  int batch;       /* B >= 0 */
+  int seq_len;     /* T >= 0 steps per sequence (decode: 1) */
+  int num_k_heads; /* Hk >= 1 */
+  int num_v_heads; /* Hv, a multiple of Hk */
+
+  int frontend; /* gdn_frontend */
+  /* GDN_FRONTEND_QKV */
+  const void* q; /* (B, T, Hk, 128), qkv_dtype */
+  const void* k; /* (B, T, Hk, 128), qkv_dtype */
+  const void* v; /* (B, T, Hv, 128), qkv_dtype */
+  int qkv_dtype; /* gdn_dtype */
+  /* GDN_FRONTEND_CONV */
+  const void* x;             /* (B, T, C) bf16, channels [q | k | v] */
+  const void* conv_weight;   /* (4, C) bf16, w[j, c] = conv1d.weight[c, 0, j] */
+  const void* conv_state_in; /* (B, 3, C) bf16 pre-conv rows, or NULL for zeros */
+  void* conv_state_out;      /* (B, 3, C) bf16 <- last 3 rows of [conv_state_in ; x], or
+                                NULL; must not overlap conv_state_in */
+
+  int gate_mode; /* gdn_gate_mode */
+  /* GDN_GATES_RAW */
+  const void* a;        /* (B, T, Hv) bf16 */
+  const void* b;        /* (B, T, Hv) bf16 */
+  const float* A_log;   /* (Hv) */
+  const float* dt_bias; /* (Hv) */
+  /* GDN_GATES_PRECOMPUTED */
+  const float* alpha; /* (B, T, Hv) */
+  const float* beta;  /* (B, T, Hv) */
+
+  const float* state_in; /* (B, Hv, 128, 128), or NULL for a zero state; 16-byte aligned */
+  float* state_out;      /* (B, Hv, 128, 128) final state, or NULL; may equal state_in
+                            (in place), must not otherwise overlap it; 16-byte aligned */
+  float* states;         /* per-step states (collect), or NULL; must not overlap state_in;
+                            16-byte aligned. gdn_run only. */
+  int states_layout;     /* gdn_states_layout */
+  void* o;               /* (B, T, Hv, 128), o_dtype; never NULL */
+  int o_dtype;           /* gdn_dtype */
+  void* stream;          /* hipStream_t */
+} gdn_layer_args;
+
+/* Recurrent form for any T (decode T = 1; speculative verify with `states`). The
+ * state is read once and written once per call; with `states` set, the state after
+ * every step is written too and state_out may be NULL (record mode: the input state
+ * is left untouched, model.cpp:630-633). */
+int gdn_run(const gdn_layer_args* args);
+
+/* Chunked form (chunk 64, WY/UT transform) for prefill; same arguments as gdn_run
+ * except that `states` must be NULL. Intra-chunk products run on bf16 MFMA with fp32
+ * accumulation; the state hand-off between chunks stays fp32. */
+int gdn_prefill_chunked(const gdn_layer_args* args);
+
+typedef struct gdn_commit_args {
+  int n_layers;    /* >= 1 */
+  int batch;       /* B */
+  int seq_len;     /* T of the recorded block */
+  int num_v_heads; /* Hv */
+  int conv_dim;    /* C; 0 skips the conv window */
+  int n;           /* accepted prefix, 0 <= n <= T */
+  const float* states;       /* as written by gdn_run */
+  int states_layout;         /* gdn_states_layout */
+  const float* state_prev;   /* (B, Hv, 128, 128): the state the block started from */
+  float* state_dst;          /* (B, Hv, 128, 128) <- n == 0 ? state_prev : states[n-1];
+                                may equal state_prev */
+  const void* conv_state_in; /* (B, 3, C) bf16 the block started from, or NULL (zeros) */
+  const void* x;             /* (B, T, C) bf16, the block's conv input */
+  void* conv_state_dst;      /* (B, 3, C) bf16 <- rows n..n+2 of [conv_state_in ; x]; may
+                                equal conv_state_in */
+  void* stream;              /* hipStream_t */
+} gdn_commit_args;
+
+/* DeltaCache::commit(n): accept the first n tokens of a recorded block. */
+int gdn_commit(const gdn_commit_args* args);
+
+/* 1 if the current HIP device is a gfx950 the kernels were built for, else 0. */
+int gdn_available(void);
+
+/* GDN_ABI_VERSION of the library. */
+int gdn_abi_version(void);
+
+/* This thread's message for the most recent failed call ("" if none). */
+const char* gdn_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GDN_H */

@@ -1,0 +1,114 @@
+// Device-side scalar math for the gated-delta front end and gates (gfx950).
+//
+// The front end rounds to bf16 after every op (the reference's bf16 MLX ops,
+// cpp/src/model.cpp:585-602, cpp/src/ops.cpp:20-30), so a one-ulp difference in an
+// fp32 intermediate can flip a bf16 rounding and move an output by 2^-8 relative.
+// To make those decisions reproducible, exp/log/log1p here are fixed algorithms built
+// only from correctly rounded IEEE operations (add, mul, fma, div, sqrt, rint):
+//   exp   Cody-Waite reduction x = n ln2 + r, |r| <= ln2/2; degree-7 Taylor polynomial
+//         of e^r by Horner with fma; 2^n applied in two halves.
+//   log   x = m 2^e, m in [sqrt(1/2), sqrt(2)), f = m - 1, s = f/(2+f):
+//         log(1+f) = f - (f^2/2 - s (f^2/2 + R(s^2))), R the atanh series through s^8.
+//   log1p Goldberg's correction log(w) * (x / (w - 1)), w = 1 + x.
+// The translation unit is compiled with -ffp-contract=off, so every operation below is
+// rounded exactly as written.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+__device__ __forceinline__ float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  uint32_t u = f_bits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf2f(uint16_t h) { return bits_f((uint32_t)h << 16); }
+// Round an fp32 value to the nearest bf16 value, kept in fp32.
+__device__ __forceinline__ float rbf(float x) { return bf2f(f2bf(x)); }
+
+__device__ __forceinline__ float d_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2, n2 = ni - n1;
+  p = p * bits_f((uint32_t)(n1 + 127) << 23);
+  return p * bits_f((uint32_t)(n2 + 127) << 23);
+}
+
+// log of a positive normal argument (the only arguments used here are in (1, 2]).
+__device__ __forceinline__ float d_logf(float x) {
+  uint32_t u = f_bits(x);
+  int e = (int)((u >> 23) & 0xffu) - 127;
+  float m = bits_f((u & 0x007fffffu) | 0x3f800000u);
+  if (m > 1.41421356237309504880f) {
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float f = m - 1.0f;
+  const float s = f / (2.0f + f);
+  const float z = s * s;
+  float R = 0.22222222222222222222f;
+  R = __builtin_fmaf(R, z, 0.28571428571428571429f);
+  R = __builtin_fmaf(R, z, 0.4f);
+  R = __builtin_fmaf(R, z, 0.66666666666666666667f);
+  R = R * z;
+  const float hfsq = 0.5f * f * f;
+  const float lm = f - (hfsq - s * (hfsq + R));
+  const float ef = (float)e;
+  return __builtin_fmaf(ef, 0.693145751953125f, __builtin_fmaf(ef, 1.428606765330187045e-06f, lm));
+}
+
+__device__ __forceinline__ float d_log1pf(float x) {
+  const float w = 1.0f + x;
+  if (w == 1.0f) return x;
+  if (w == __builtin_inff()) return w;
+  return d_logf(w) * (x / (w - 1.0f));
+}
+
+// sigmoid(x) = 1 / (1 + exp(-x)), as MLX's unary op.
+__device__ __forceinline__ float d_sigmoidf(float x) {
+  const float e = d_expf(-x);
+  const float d = 1.0f + e;
+  return 1.0f / d;
+}
+
+// softplus(x) = logaddexp(0, x) (cpp/src/ops.cpp:22-25).
+__device__ __forceinline__ float d_softplusf(float x) {
+  if (x != x) return x;
+  const float mx = x > 0.0f ? x : 0.0f;
+  const float mn = x > 0.0f ? 0.0f : x;
+  if (mn == -__builtin_inff() || mx == __builtin_inff()) return mx;
+  return mx + d_log1pf(d_expf(mn - mx));
+}
+
+// Gate math of cpp/src/model.cpp:608-612 for one (step, v-head).
+__device__ __forceinline__ void d_gates(float a_logit, float b_logit, float A_log, float dt_bias,
+                                        float& alpha, float& beta) {
+  beta = d_sigmoidf(b_logit);
+  const float t = a_logit + dt_bias;
+  const float sp = d_softplusf(t);
+  const float A = d_expf(A_log);
+  const float m = A * sp;
+  alpha = d_expf(-m);
+}
+
+}  // namespace gdn

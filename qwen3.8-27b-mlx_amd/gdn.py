@@ -1,0 +1,338 @@
+"""Python host side of libgdn.so: ctypes bindings over the C ABI (include/gdn.h) and a
+mirror of the reference's per-layer interface.
+
+Mirrors (paths relative to the reference tree):
+  run(...)              delta::run(q, k, v, alpha, beta, S, collect)   cpp/src/delta.hpp:66-68
+                        (python: delta_kernel.gated_delta_metal, python/delta_kernel.py:126-165)
+  layer(...)            the recurrent core of GatedDeltaNet::operator() from the conv input
+                        to o: cpp/src/model.cpp:585-624 (gates 608-612)
+  prefill_chunked(...)  chunked_delta, python/qwen35.py:365-431
+  DeltaCache            DeltaCache + commit, cpp/src/model.hpp:211-227, model.cpp:439-457
+
+Tensors are torch tensors on the GPU (torch supplies device memory and the stream;
+the computation is the HIP library's). Errors from the library raise GdnError with the
+library's message; nothing falls back to another implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libgdn.so")
+
+GDN_OK, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_EDEVICE = 0, 1, 2, 3
+DTYPE_BF16, DTYPE_F32 = 0, 1
+FRONTEND_QKV, FRONTEND_CONV = 0, 1
+GATES_RAW, GATES_PRECOMPUTED = 0, 1
+STATES_BHT, STATES_TBH = 0, 1
+HEAD_DIM = 128
+CONV_TAPS = 4
+
+EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_commit", "gdn_available", "gdn_abi_version",
+           "gdn_last_error")
+
+
+class GdnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[gdn error {code}] {msg}")
+        self.code = code
+
+
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+
+
+class LayerArgs(ctypes.Structure):
+    """struct gdn_layer_args (include/gdn.h)."""
+    _fields_ = [
+        ("n_layers", _int), ("batch", _int), ("seq_len", _int), ("num_k_heads", _int),
+        ("num_v_heads", _int),
+        ("frontend", _int),
+        ("q", _vp), ("k", _vp), ("v", _vp), ("qkv_dtype", _int),
+        ("x", _vp), ("conv_weight", _vp), ("conv_state_in", _vp), ("conv_state_out", _vp),
+        ("gate_mode", _int),
+        ("a", _vp), ("b", _vp), ("A_log", _vp), ("dt_bias", _vp),
+        ("alpha", _vp), ("beta", _vp),
+        ("state_in", _vp), ("state_out", _vp), ("states", _vp), ("states_layout", _int),
+        ("o", _vp), ("o_dtype", _int),
+        ("stream", _vp),
+    ]
+
+
+class CommitArgs(ctypes.Structure):
+    """struct gdn_commit_args (include/gdn.h)."""
+    _fields_ = [
+        ("n_layers", _int), ("batch", _int), ("seq_len", _int), ("num_v_heads", _int),
+        ("conv_dim", _int), ("n", _int),
+        ("states", _vp), ("states_layout", _int),
+        ("state_prev", _vp), ("state_dst", _vp),
+        ("conv_state_in", _vp), ("x", _vp), ("conv_state_dst", _vp),
+        ("stream", _vp),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libgdn.so from the package directory; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        L.gdn_run.argtypes = [ctypes.POINTER(LayerArgs)]
+        L.gdn_run.restype = _int
+        L.gdn_prefill_chunked.argtypes = [ctypes.POINTER(LayerArgs)]
+        L.gdn_prefill_chunked.restype = _int
+        L.gdn_commit.argtypes = [ctypes.POINTER(CommitArgs)]
+        L.gdn_commit.restype = _int
+        L.gdn_available.argtypes = []
+        L.gdn_available.restype = _int
+        L.gdn_abi_version.argtypes = []
+        L.gdn_abi_version.restype = _int
+        L.gdn_last_error.argtypes = []
+        L.gdn_last_error.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().gdn_last_error().decode()
+
+
+def available() -> bool:
+    """delta::available (cpp/src/delta.cpp:133-135): a gfx950 device is current."""
+    return bool(lib().gdn_available())
+
+
+def _check(rc: int) -> None:
+    if rc != GDN_OK:
+        raise GdnError(rc, last_error())
+
+
+def call_run(args: LayerArgs) -> None:
+    _check(lib().gdn_run(ctypes.byref(args)))
+
+
+def call_prefill(args: LayerArgs) -> None:
+    _check(lib().gdn_prefill_chunked(ctypes.byref(args)))
+
+
+def call_commit(args: CommitArgs) -> None:
+    _check(lib().gdn_commit(ctypes.byref(args)))
+
+
+# --------------------------------------------------------------------------
+# torch-facing helpers
+
+def _ptr(t) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise GdnError(GDN_EINVAL, "tensors passed to libgdn must be contiguous")
+    return t.data_ptr()
+
+
+def _dt(t) -> int:
+    import torch
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    raise GdnError(GDN_EINVAL, f"unsupported dtype {t.dtype}")
+
+
+def _stream(stream) -> Optional[int]:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+@dataclass
+class Result:
+    """delta::Result (cpp/src/delta.hpp:53-57)."""
+    o: object
+    s_out: object
+    states: List[object] = field(default_factory=list)
+
+
+def run(q, k, v, alpha, beta, S=None, collect: bool = False, *, o_dtype=None, stream=None,
+        in_place: bool = False) -> Result:
+    """delta::run: q, k (B,L,H,128) head-expanded; v (B,L,H,128); alpha, beta (B,L,H) fp32;
+    S (B,H,128,128) fp32 or None. Returns o (B,L,H,128), s_out, and with collect the L
+    per-step states as views of one (B,H,L,128,128) buffer (delta.cpp:155-171)."""
+    import torch
+    B, L, H, _ = q.shape
+    o_dtype = torch.float32 if o_dtype is None else o_dtype
+    o = torch.empty((B, L, H, HEAD_DIM), dtype=o_dtype, device=q.device)
+    if in_place:
+        if S is None:
+            raise GdnError(GDN_EINVAL, "in-place run needs a state")
+        s_out = S
+    else:
+        s_out = torch.empty((B, H, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device)
+    S_all = (torch.empty((B, H, L, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device)
+             if collect else None)
+    args = LayerArgs(
+        n_layers=1, batch=B, seq_len=L, num_k_heads=q.shape[2], num_v_heads=v.shape[2],
+        frontend=FRONTEND_QKV, q=_ptr(q), k=_ptr(k), v=_ptr(v), qkv_dtype=_dt(q),
+        gate_mode=GATES_PRECOMPUTED, alpha=_ptr(alpha), beta=_ptr(beta),
+        state_in=_ptr(S), state_out=_ptr(s_out), states=_ptr(S_all), states_layout=STATES_BHT,
+        o=_ptr(o), o_dtype=_dt(o), stream=_stream(stream))
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise GdnError(GDN_EINVAL, "q, k, v must share a dtype")
+    call_run(args)
+    states = [S_all[:, :, t] for t in range(L)] if collect else []
+    return Result(o, s_out, states)
+
+
+def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
+               q=None, k=None, v=None, x=None, conv_weight=None, conv_state_in=None,
+               conv_state_out=None, a=None, b=None, A_log=None, dt_bias=None, alpha=None,
+               beta=None, state_in=None, state_out=None, states=None,
+               states_layout: int = STATES_BHT, o=None, stream=None) -> LayerArgs:
+    """Fill gdn_layer_args from torch tensors (front end and gate mode inferred)."""
+    conv = x is not None
+    raw = a is not None
+    return LayerArgs(
+        n_layers=n_layers, batch=B, seq_len=T, num_k_heads=Hk, num_v_heads=Hv,
+        frontend=FRONTEND_CONV if conv else FRONTEND_QKV,
+        q=_ptr(q), k=_ptr(k), v=_ptr(v), qkv_dtype=_dt(q) if q is not None else DTYPE_BF16,
+        x=_ptr(x), conv_weight=_ptr(conv_weight), conv_state_in=_ptr(conv_state_in),
+        conv_state_out=_ptr(conv_state_out),
+        gate_mode=GATES_RAW if raw else GATES_PRECOMPUTED,
+        a=_ptr(a), b=_ptr(b), A_log=_ptr(A_log), dt_bias=_ptr(dt_bias),
+        alpha=_ptr(alpha), beta=_ptr(beta),
+        state_in=_ptr(state_in), state_out=_ptr(state_out), states=_ptr(states),
+        states_layout=states_layout,
+        o=_ptr(o), o_dtype=_dt(o) if o is not None else DTYPE_BF16,
+        stream=_stream(stream))
+
+
+def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
+          conv_weight=None, conv_state=None, collect: bool = False, in_place: bool = True,
+          o_dtype=None, Hk: int = 16, stream=None):
+    """The north-star per-layer call: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
+    (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
+    v (B,T,Hv,128). Returns dict(o, state, states, conv_state)."""
+    import torch
+    src = x if x is not None else q
+    B, T = src.shape[0], src.shape[1]
+    Hv = A_log.shape[-1]
+    dev = src.device
+    o = torch.empty((B, T, Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16, device=dev)
+    record = collect
+    if record:
+        state_out = None
+    elif in_place and state is not None:
+        state_out = state
+    else:
+        state_out = torch.empty((B, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
+    states = (torch.empty((B, Hv, T, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
+              if record else None)
+    conv_out = None
+    if x is not None and not record:
+        conv_out = torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
+    args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
+                      conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
+                      A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out,
+                      states=states, o=o, stream=stream)
+    call_run(args)
+    return dict(o=o, state=state_out, states=states, conv_state=conv_out)
+
+
+def prefill_chunked(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
+                    conv_weight=None, conv_state=None, o_dtype=None, Hk: int = 16, stream=None):
+    """chunked_delta with the conv front end and gates inside. Returns dict(o, state, conv_state)."""
+    import torch
+    src = x if x is not None else q
+    B, T = src.shape[0], src.shape[1]
+    Hv = A_log.shape[-1]
+    dev = src.device
+    o = torch.empty((B, T, Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16, device=dev)
+    state_out = torch.empty((B, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
+    conv_out = (torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
+                if x is not None else None)
+    args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
+                      conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
+                      A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out, o=o,
+                      stream=stream)
+    call_prefill(args)
+    return dict(o=o, state=state_out, conv_state=conv_out)
+
+
+def commit(*, n: int, T: int, states, state_prev, state_dst, x=None, conv_state_in=None,
+           conv_state_dst=None, states_layout: int = STATES_BHT, n_layers: int = 1,
+           stream=None) -> None:
+    """DeltaCache::commit(n) on the device (cpp/src/model.cpp:439-457)."""
+    B, Hv = state_dst.shape[-4], state_dst.shape[-3]
+    C = x.shape[-1] if x is not None else (conv_state_dst.shape[-1] if conv_state_dst is not None else 0)
+    args = CommitArgs(n_layers=n_layers, batch=B, seq_len=T, num_v_heads=Hv, conv_dim=C, n=n,
+                      states=_ptr(states), states_layout=states_layout,
+                      state_prev=_ptr(state_prev), state_dst=_ptr(state_dst),
+                      conv_state_in=_ptr(conv_state_in), x=_ptr(x),
+                      conv_state_dst=_ptr(conv_state_dst), stream=_stream(stream))
+    call_commit(args)
+
+
+class DeltaCache:
+    """DeltaCache (cpp/src/model.hpp:211-227) over device buffers: `record` mode keeps
+    the per-step states of a block instead of advancing; commit(n) adopts step n.
+
+    The conv state is kept in two buffers that swap roles each call (the library never
+    updates it in place: every workgroup must see the old rows)."""
+
+    def __init__(self, B: int, Hv: int = 48, Hk: int = 16, device="cuda"):
+        import torch
+        C = 2 * Hk * HEAD_DIM + Hv * HEAD_DIM
+        self.Hk, self.Hv, self.C = Hk, Hv, C
+        self.state = torch.zeros((B, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=device)
+        self.conv = torch.zeros((B, CONV_TAPS - 1, C), dtype=torch.bfloat16, device=device)
+        self._conv_spare = torch.empty_like(self.conv)
+        self.offset = 0
+        self.record = False
+        self.base_offset = 0
+        self.pending = None
+
+    def step(self, x, conv_weight, a, b, A_log, dt_bias, o_dtype=None, stream=None):
+        """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache."""
+        import torch
+        B, T = x.shape[0], x.shape[1]
+        o = torch.empty((B, T, self.Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16,
+                        device=x.device)
+        if self.record:
+            states = torch.empty((B, self.Hv, T, HEAD_DIM, HEAD_DIM), dtype=torch.float32,
+                                 device=x.device)
+            args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,
+                              conv_state_in=self.conv, a=a, b=b, A_log=A_log, dt_bias=dt_bias,
+                              state_in=self.state, states=states, o=o, stream=stream)
+            call_run(args)
+            self.base_offset = self.offset
+            self.pending = (x, states, T)
+        else:
+            args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,
+                              conv_state_in=self.conv, conv_state_out=self._conv_spare, a=a,
+                              b=b, A_log=A_log, dt_bias=dt_bias, state_in=self.state,
+                              state_out=self.state, o=o, stream=stream)
+            call_run(args)
+            self.conv, self._conv_spare = self._conv_spare, self.conv
+            self.offset += T
+        return o
+
+    def commit(self, n: int, stream=None) -> None:
+        """Accept the first n tokens of the recorded block (model.cpp:439-457)."""
+        if self.pending is None:
+            return
+        x, states, T = self.pending
+        if n < 0 or n > T:
+            raise GdnError(GDN_EINVAL, "DeltaCache::commit out of range")
+        commit(n=n, T=T, states=states, state_prev=self.state, state_dst=self.state, x=x,
+               conv_state_in=self.conv, conv_state_dst=self.conv, stream=stream)
+        self.offset = self.base_offset + n
+        self.pending = None
+        self.record = False

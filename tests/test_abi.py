@@ -1,0 +1,191 @@
+"""CPU tests of the C ABI (include/gdn.h): the library loads, exports every declared
+symbol, its ctypes mirror matches the C struct layout, and argument errors come back as
+GDN_EINVAL with a message before any device work -- no GPU is needed for any of it."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gdn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(gdn_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == sorted(
+        ["gdn_run", "gdn_prefill_chunked", "gdn_commit", "gdn_available", "gdn_abi_version",
+         "gdn_last_error"])
+
+
+def test_library_exports_every_declared_symbol(gdn):
+    L = gdn.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", gdn.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s+(gdn_\w+)", out))
+    assert set(declared_functions()) <= exported
+    assert L.gdn_abi_version() == 1
+    assert set(gdn.EXPORTS) == set(declared_functions())
+
+
+def _c_layout(struct: str, fields):
+    src = "#include <stdio.h>\n#include <stddef.h>\n#include \"gdn.h\"\nint main(void){\n"
+    src += f'printf("%zu\\n", sizeof({struct}));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof({struct}, {f}));\n'
+    src += "return 0;}\n"
+    tmp = os.path.join("/tmp", f"gdn_layout_{os.getpid()}_{struct}")
+    with open(tmp + ".c", "w") as fh:
+        fh.write(src)
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), tmp + ".c", "-o",
+                    tmp], check=True)
+    out = subprocess.run([tmp], capture_output=True, text=True, check=True).stdout.split()
+    os.remove(tmp)
+    os.remove(tmp + ".c")
+    return [int(x) for x in out]
+
+
+@pytest.mark.parametrize("cls,struct", [("LayerArgs", "gdn_layer_args"),
+                                        ("CommitArgs", "gdn_commit_args")])
+def test_ctypes_mirror_matches_c_layout(gdn, cls, struct):
+    C = getattr(gdn, cls)
+    names = [f for f, _ in C._fields_]
+    layout = _c_layout(struct, names)
+    assert layout[0] == ctypes.sizeof(C)
+    assert layout[1:] == [getattr(C, n).offset for n in names]
+
+
+def _no_gpu():
+    import torch
+    return not torch.cuda.is_available()
+
+
+def _args(gdn, **kw):
+    base = dict(n_layers=1, batch=1, seq_len=1, num_k_heads=16, num_v_heads=48,
+                frontend=gdn.FRONTEND_QKV, q=0x1000, k=0x2000, v=0x3000,
+                qkv_dtype=gdn.DTYPE_BF16, gate_mode=gdn.GATES_RAW, a=0x4000, b=0x5000,
+                A_log=0x6000, dt_bias=0x7000, state_in=0x100000, state_out=0x100000,
+                o=0x9000000, o_dtype=gdn.DTYPE_BF16)
+    base.update(kw)
+    return gdn.LayerArgs(**base)
+
+
+BAD_RUN = [
+    (dict(n_layers=0), "n_layers"),
+    (dict(batch=-1), "batch"),
+    (dict(seq_len=-2), "seq_len"),
+    (dict(num_k_heads=0), "head counts"),
+    (dict(num_v_heads=40), "multiple"),
+    (dict(frontend=7), "frontend"),
+    (dict(gate_mode=3), "gate_mode"),
+    (dict(o_dtype=9), "o_dtype"),
+    (dict(qkv_dtype=4), "qkv_dtype"),
+    (dict(states_layout=2), "states_layout"),
+    (dict(q=None), "q, k and v"),
+    (dict(a=None), "raw gates"),
+    (dict(gate_mode=1), "precomputed"),
+    (dict(o=None), "o is required"),
+    (dict(state_in=0x100004), "16-byte"),
+    (dict(state_out=0x100000 + 4096), "state_out must equal"),
+    (dict(states=0x100000 + 64), "states must not overlap state_in"),
+    (dict(o=0x100000 + 128), "o must not overlap"),
+    (dict(frontend=1, x=None, conv_weight=0x8000), "x is required"),
+    (dict(frontend=1, x=0xA000000, conv_weight=None), "conv_weight"),
+    (dict(frontend=1, x=0xA000000, conv_weight=0x8000, conv_state_in=0xB000000,
+          conv_state_out=0xB000000 + 2), "conv_state_out must not overlap conv_state_in"),
+    (dict(frontend=1, x=0xA000000, conv_weight=0x8000, conv_state_out=0xA000000),
+     "must not overlap x"),
+    (dict(n_layers=48, batch=1 << 20), "too large"),
+]
+
+
+@pytest.mark.parametrize("kw,msg", BAD_RUN)
+def test_run_rejects_bad_arguments(gdn, kw, msg):
+    L = gdn.lib()
+    rc = L.gdn_run(ctypes.byref(_args(gdn, **kw)))
+    assert rc == gdn.GDN_EINVAL
+    assert msg in gdn.last_error(), gdn.last_error()
+
+
+def test_null_args_and_prefill_states(gdn):
+    L = gdn.lib()
+    assert L.gdn_run(None) == gdn.GDN_EINVAL and "NULL" in gdn.last_error()
+    assert L.gdn_prefill_chunked(None) == gdn.GDN_EINVAL
+    assert L.gdn_commit(None) == gdn.GDN_EINVAL
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, states=0x9000000 * 4)))
+    assert rc == gdn.GDN_EINVAL and "per-step states" in gdn.last_error()
+
+
+def _commit(gdn, **kw):
+    base = dict(n_layers=1, batch=1, seq_len=5, num_v_heads=48, conv_dim=10240, n=2,
+                states=0x1000000, states_layout=gdn.STATES_BHT, state_prev=0x100000,
+                state_dst=0x100000, conv_state_in=0x2000, x=0x40000000, conv_state_dst=0x2000)
+    base.update(kw)
+    return gdn.CommitArgs(**base)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(n=6), "out of range"),
+    (dict(n=-1), "out of range"),
+    (dict(states_layout=5), "states_layout"),
+    (dict(n=0, state_prev=None), "state_prev"),
+    (dict(states=None), "states is required"),
+    (dict(state_dst=None), "state_dst"),
+    (dict(state_dst=0x1000000 + 4096), "overlaps states"),
+    (dict(conv_state_dst=0x40000000 + 64), "must not overlap x"),
+    (dict(x=None), "x is required"),
+])
+def test_commit_rejects_bad_arguments(gdn, kw, msg):
+    rc = gdn.lib().gdn_commit(ctypes.byref(_commit(gdn, **kw)))
+    assert rc == gdn.GDN_EINVAL
+    assert msg in gdn.last_error(), gdn.last_error()
+
+
+def test_empty_batch_is_a_no_op(gdn):
+    # B = 0 touches nothing and needs no device
+    assert gdn.lib().gdn_run(ctypes.byref(_args(gdn, batch=0))) == gdn.GDN_OK
+    assert gdn.last_error() == ""
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="checks the no-device path")
+def test_valid_call_without_device_reports_device_error(gdn):
+    assert gdn.lib().gdn_available() == 0
+    rc = gdn.lib().gdn_run(ctypes.byref(_args(gdn)))
+    assert rc in (gdn.GDN_EDEVICE, gdn.GDN_EUNSUPPORTED)
+    assert gdn.last_error()
+
+
+def test_error_message_is_per_thread(gdn):
+    import threading
+    L = gdn.lib()
+    L.gdn_run(ctypes.byref(_args(gdn, n_layers=0)))
+    seen = {}
+
+    def worker():
+        seen["before"] = gdn.last_error()
+        L.gdn_run(ctypes.byref(_args(gdn, batch=-1)))
+        seen["after"] = gdn.last_error()
+
+    th = threading.Thread(target=worker)
+    th.start()
+    th.join()
+    assert seen["before"] == "" and "batch" in seen["after"]
+    assert "n_layers" in gdn.last_error()
+
+
+def test_product_does_not_touch_the_oracle():
+    pkg = os.path.join(ROOT, "qwen3.8-27b-mlx_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h", ".hpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text.lower() and "gdno_" not in text, f

@@ -1,0 +1,373 @@
+"""GPU parity of the recurrent kernel (decode, batched decode, verify, commit) through
+the C ABI, against the oracle on the same seeded inputs.
+
+Tolerances (written here, from the task statement):
+  fp32 state:      max|a-b|/max|b| <= 1e-4 and max|a-b| <= 1e-4
+  outputs, fp32:   same as the state
+  outputs, bf16:   max|a-b| <= 2e-3 against the oracle's fp32 output, and every element
+                   within its own rounding bound |a-b| <= 2^-8 |b| + 1e-5 max|b| (bf16 unit
+                   roundoff plus fp32 summation noise). The reference's max|a-b|/max|b| is
+                   bounded by 2^-8 + 1e-4: bf16 has an 8-bit significand, so the output
+                   rounding alone can reach 2^-8 = 3.9e-3 relative and no bf16 output can
+                   promise 2e-3 in that measure.
+  reference kernel test shapes: 2e-5 (cpp/src/tests.cpp:227)
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from _util import log_case, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+STATE_TOL = 1e-4
+O_F32_TOL = 1e-4
+O_BF16_TOL = 2e-3
+REF_TOL = 2e-5
+D = 128
+
+
+def _stack(arrs):
+    return None if arrs[0] is None else np.ascontiguousarray(np.stack(arrs, axis=0))
+
+
+def run_layers(gdn, dev, inps, *, o_dtype="f32", collect=False, tbh=False, in_place=False,
+               conv_out=True, Hk=16):
+    """Runs len(inps) independent layers in one gdn_run call. Returns numpy outputs."""
+    import torch
+    nl = len(inps)
+    i0 = inps[0]
+    conv = i0.x is not None
+    B, T = (i0.x.shape[0], i0.x.shape[1]) if conv else (i0.q.shape[0], i0.q.shape[1])
+    Hv = i0.A_log.size
+    t = {}
+    for name in ("q", "k", "v", "x", "conv_w", "conv_state", "a", "b", "A_log", "dt_bias", "state"):
+        arr = _stack([getattr(i, name) for i in inps])
+        t[name] = None if arr is None else to_dev(arr, dev)
+    st_in = t["state"]
+    odt = torch.bfloat16 if o_dtype == "bf16" else torch.float32
+    o = torch.empty((nl, B, T, Hv, D), dtype=odt, device=dev)
+    if collect:
+        state_out = None
+    elif in_place and st_in is not None:
+        state_out = st_in
+    else:
+        state_out = torch.full((nl, B, Hv, D, D), float("nan"), device=dev)
+    states = None
+    if collect:
+        shape = (nl, T, B, Hv, D, D) if tbh else (nl, B, Hv, T, D, D)
+        states = torch.full(shape, float("nan"), device=dev)
+    cout = None
+    if conv and conv_out:
+        cout = torch.zeros((nl, B, 3, i0.x.shape[2]), dtype=torch.bfloat16, device=dev)
+    args = gdn.layer_args(
+        B=B, T=T, Hk=Hk, Hv=Hv, n_layers=nl, q=t["q"], k=t["k"], v=t["v"], x=t["x"],
+        conv_weight=t["conv_w"], conv_state_in=t["conv_state"], conv_state_out=cout,
+        a=t["a"], b=t["b"], A_log=t["A_log"], dt_bias=t["dt_bias"], state_in=st_in,
+        state_out=state_out, states=states,
+        states_layout=gdn.STATES_TBH if tbh else gdn.STATES_BHT, o=o)
+    gdn.call_run(args)
+    torch.cuda.synchronize()
+    out = dict(o=to_np(o).astype(np.float32) if o_dtype == "f32" else to_np(o),
+               state=None if state_out is None else to_np(state_out),
+               states=None if states is None else to_np(states),
+               conv=None if cout is None else to_np(cout),
+               state_in_after=None if st_in is None else to_np(st_in))
+    return out
+
+
+def check_state(O, got, ref, what):
+    r, m = O.rel_err(got, ref), O.max_abs(got, ref)
+    print(f"  {what}: rel {r:.2e} max-abs {m:.2e}", flush=True)
+    assert np.all(np.isfinite(got)), what
+    assert r <= STATE_TOL and m <= STATE_TOL, (what, r, m)
+
+
+def check_o(O, got, ref, dtype, what):
+    if dtype == "bf16":
+        from _util import bf16_to_f32
+        g = bf16_to_f32(got)
+        r, m = O.rel_err(g, ref), O.max_abs(g, ref)
+        bound = 2.0 ** -8 * np.abs(ref) + 1e-5 * np.abs(ref).max()
+        excess = float((np.abs(g.astype(np.float64) - ref) - bound).max())
+        print(f"  {what} (bf16): rel {r:.2e} max-abs {m:.2e} rounding-bound excess {excess:.1e}",
+              flush=True)
+        assert m <= O_BF16_TOL and excess <= 0 and r <= 2.0 ** -8 + 1e-4, (what, r, m, excess)
+    else:
+        r, m = O.rel_err(got, ref), O.max_abs(got, ref)
+        print(f"  {what} (f32): rel {r:.2e} max-abs {m:.2e}", flush=True)
+        assert r <= O_F32_TOL and m <= O_F32_TOL, (what, r, m)
+
+
+@pytest.mark.parametrize("o_dtype", ["f32", "bf16"])
+def test_decode_single_layer_qkv(O, gdn, dev, o_dtype):
+    """Single decode step, one layer, B=1, q,k,v given (bf16, l2-normalised)."""
+    log_case(f"decode 1 layer B=1 qkv o={o_dtype}")
+    inp = O.make_inputs(config=0, layer=0, B=1, L=1)
+    ref = O.reference_layer(inp)
+    out = run_layers(gdn, dev, [inp], o_dtype=o_dtype)
+    check_state(O, out["state"][0], ref["state"], "state")
+    check_o(O, out["o"][0], ref["o"], o_dtype, "o")
+    assert np.array_equal(out["state_in_after"][0], inp.state)  # out of place: input untouched
+
+
+def test_decode_48_layers_conv(O, gdn, dev):
+    """Full-model decode step, B=1: 48 independent layers with the conv front end."""
+    log_case("decode 48 layers B=1 conv")
+    inps = [O.make_inputs(config=1, layer=l, B=1, L=1, conv=True) for l in range(48)]
+    out = run_layers(gdn, dev, inps, o_dtype="bf16", in_place=True)
+    for l in (0, 1, 17, 47):
+        ref = O.reference_layer(inps[l])
+        check_state(O, out["state"][l], ref["state"], f"layer {l} state")
+        check_o(O, out["o"][l], ref["o"], "bf16", f"layer {l} o")
+        assert np.array_equal(out["conv"][l], ref["xp"][:, -3:]), "conv state hand-off"
+    worst = 0.0
+    for l in range(48):
+        ref = O.reference_layer(inps[l])
+        worst = max(worst, O.rel_err(out["state"][l], ref["state"]))
+    assert worst <= STATE_TOL
+
+
+def test_decode_frontend_is_bit_exact(O, gdn, dev):
+    """With a zero state and beta from the gates, o = beta v (k.q): the front end's bf16
+    q,k,v must round exactly as the oracle's (checked through a zero-state step)."""
+    log_case("front end bit-exactness via zero state")
+    inp = O.make_inputs(config=1, layer=3, B=2, L=1, conv=True, zero_state=True)
+    ref = O.reference_layer(inp)
+    out = run_layers(gdn, dev, [inp], o_dtype="f32")
+    # S' = beta v k^T exactly (one rounding of a product of bf16-valued fp32 numbers)
+    check_state(O, out["state"][0], ref["state"], "state")
+    assert O.max_abs(out["state"][0], ref["state"]) <= 1e-7
+
+
+def test_decode_batched_48_layers_sampled(O, gdn, dev):
+    """B=32 x 48 layers (4.8 GB of state) in one call; sampled (layer, batch) slices are
+    checked against the oracle (the slices are independent)."""
+    import torch
+    log_case("decode 48 layers B=32 qkv (sampled check)")
+    NL, B, Hk, Hv = 48, 32, 16, 48
+    g = torch.Generator(device=dev)
+    g.manual_seed(2024)
+    qk = torch.randn((2, NL, B, 1, Hk, D), device=dev, generator=g)
+    qk = (qk / qk.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+    q, k = qk[0].contiguous(), qk[1].contiguous()
+    v = torch.randn((NL, B, 1, Hv, D), device=dev, generator=g).to(torch.bfloat16)
+    a = torch.randn((NL, B, 1, Hv), device=dev, generator=g).to(torch.bfloat16)
+    b = torch.randn((NL, B, 1, Hv), device=dev, generator=g).to(torch.bfloat16)
+    A_log = torch.rand((NL, Hv), device=dev, generator=g) * 2 - 1
+    dt = torch.randn((NL, Hv), device=dev, generator=g) * 0.1
+    state = torch.randn((NL, B, Hv, D, D), device=dev, generator=g) * 0.02
+    samples = [(0, 0), (5, 31), (23, 7), (47, 16), (47, 31), (12, 0)]
+    saved = {s: to_np(state[s[0], s[1]]).copy() for s in samples}
+    o = torch.empty((NL, B, 1, Hv, D), dtype=torch.bfloat16, device=dev)
+    args = gdn.layer_args(B=B, T=1, Hk=Hk, Hv=Hv, n_layers=NL, q=q, k=k, v=v, a=a, b=b,
+                          A_log=A_log, dt_bias=dt, state_in=state, state_out=state, o=o)
+    gdn.call_run(args)
+    torch.cuda.synchronize()
+    for (l, bb) in samples:
+        inp = O.LayerInputs(q=to_np(q[l, bb:bb + 1]), k=to_np(k[l, bb:bb + 1]),
+                            v=to_np(v[l, bb:bb + 1]), x=None, conv_w=None, conv_state=None,
+                            a=to_np(a[l, bb:bb + 1]), b=to_np(b[l, bb:bb + 1]),
+                            A_log=to_np(A_log[l]), dt_bias=to_np(dt[l]),
+                            state=saved[(l, bb)][None])
+        ref = O.reference_layer(inp)
+        check_state(O, to_np(state[l, bb])[None], ref["state"], f"(layer {l}, b {bb}) state")
+        check_o(O, to_np(o[l, bb]), ref["o"][0], "bf16", f"(layer {l}, b {bb}) o")
+
+
+def test_decode_zero_state_closed_form_full_size(gdn, dev, O):
+    """Size-independent property at B=32 x 48 layers: from a zero state (state_in NULL),
+    S' = beta v k^T for every head, with beta from the gate math."""
+    import torch
+    log_case("closed form S'=beta v k^T at B=32 x 48 layers")
+    NL, B, Hk, Hv = 48, 32, 16, 48
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    q = torch.randn((NL, B, 1, Hk, D), device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn((NL, B, 1, Hk, D), device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn((NL, B, 1, Hv, D), device=dev, generator=g).to(torch.bfloat16)
+    alpha = torch.rand((NL, B, 1, Hv), device=dev, generator=g)
+    beta = torch.rand((NL, B, 1, Hv), device=dev, generator=g)
+    out = torch.empty((NL, B, Hv, D, D), device=dev)
+    o = torch.empty((NL, B, 1, Hv, D), device=dev)
+    args = gdn.layer_args(B=B, T=1, Hk=Hk, Hv=Hv, n_layers=NL, q=q, k=k, v=v, alpha=alpha,
+                          beta=beta, state_in=None, state_out=out, o=o)
+    gdn.call_run(args)
+    kf = k.float().repeat_interleave(3, dim=3)[:, :, 0]     # (NL,B,Hv,D)
+    vf = v.float()[:, :, 0]
+    want = beta[:, :, 0, :, None, None] * (vf[..., :, None] * kf[..., None, :])
+    err = (out - want).abs().max().item()
+    assert err <= 1e-6 * max(1.0, want.abs().max().item()), err
+    qf = q.float().repeat_interleave(3, dim=3)[:, :, 0].contiguous()
+    o_want = torch.matmul(out, qf.unsqueeze(-1).contiguous())[..., 0]
+    assert (o[:, :, 0] - o_want).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("tbh", [False, True])
+def test_verify_b8_t5_conv_with_commit(O, gdn, dev, tbh):
+    """Speculative verify: B=8, T=5, conv front end, all per-step states, input state
+    untouched; then DeltaCache::commit(n) for every n."""
+    import torch
+    log_case(f"verify B=8 T=5 conv collect tbh={tbh}")
+    inp = O.make_inputs(config=3, layer=0, B=8, L=5, conv=True)
+    ref = O.reference_layer(inp, collect=True)
+    out = run_layers(gdn, dev, [inp], o_dtype="bf16", collect=True, tbh=tbh, conv_out=False)
+    st = out["states"][0]
+    if tbh:
+        st = np.ascontiguousarray(np.transpose(st, (1, 2, 0, 3, 4)))  # -> (B,Hv,T,D,D)
+    for t in range(5):
+        check_state(O, st[:, :, t], ref["states"][:, :, t], f"step {t} state")
+    check_o(O, out["o"][0], ref["o"], "bf16", "o")
+    assert np.array_equal(out["state_in_after"][0], inp.state), "record mode touched the input state"
+    # commit every prefix length on the device, compare with the oracle's commit
+    states_dev = to_dev(out["states"], dev)
+    x = to_dev(inp.x, dev)
+    for n in range(6):
+        log_case(f"commit n={n} tbh={tbh}")
+        S = to_dev(inp.state, dev)
+        conv = to_dev(inp.conv_state, dev)
+        gdn.commit(n=n, T=5, states=states_dev, state_prev=S, state_dst=S, x=x,
+                   conv_state_in=conv, conv_state_dst=conv,
+                   states_layout=gdn.STATES_TBH if tbh else gdn.STATES_BHT)
+        torch.cuda.synchronize()
+        S_ref, conv_ref = O.commit(n, ref["states"], inp.state, ref["xp"])
+        if n == 0:
+            assert np.array_equal(to_np(S), inp.state)
+        else:
+            assert np.array_equal(to_np(S), st[:, :, n - 1])
+        check_state(O, to_np(S), S_ref, f"commit({n}) state")
+        assert np.array_equal(to_np(conv), conv_ref)
+
+
+@pytest.mark.parametrize("B,L,H", [(1, 1, 48), (1, 4, 48), (1, 9, 48), (2, 3, 16), (1, 64, 48),
+                                   (1, 384, 8)])
+def test_reference_kernel_test_shapes(O, gdn, dev, B, L, H):
+    """cpp/src/tests.cpp:206-243: delta::run vs run_reference on q=l2norm(N)*Dk^-0.5,
+    k=l2norm(N), v=N, alpha~U(0.85,1), beta~U(0,1), S0=0.1 N; fp32 in/out, collect too."""
+    import torch
+    log_case(f"reference test shape B={B} L={L} H={H}")
+    s = 5000 + 7 * L + H
+    qn = O.normal(s, (B, L, H, D))
+    kn = O.normal(s + 1, (B, L, H, D))
+    q = (qn / np.linalg.norm(qn, axis=-1, keepdims=True) / math.sqrt(D)).astype(np.float32)
+    k = (kn / np.linalg.norm(kn, axis=-1, keepdims=True)).astype(np.float32)
+    v = O.normal(s + 2, (B, L, H, D))
+    al = O.uniform(s + 3, (B, L, H), 0.85, 1.0)
+    bt = O.uniform(s + 4, (B, L, H), 0.0, 1.0)
+    S0 = O.normal(s + 5, (B, H, D, D), 0, 0.1)
+    ro, rS, rst = O.recurrent(q, k, v, al, bt, S0, collect=True)
+    T = lambda a: to_dev(a, dev)  # noqa: E731
+    res = gdn.run(T(q), T(k), T(v), T(al), T(bt), T(S0))
+    torch.cuda.synchronize()
+    eo, es = O.rel_err(to_np(res.o), ro), O.rel_err(to_np(res.s_out), rS)
+    print(f"  out {eo:.2e} state {es:.2e}", flush=True)
+    assert max(eo, es) < REF_TOL
+    rc = gdn.run(T(q), T(k), T(v), T(al), T(bt), T(S0), collect=True)
+    torch.cuda.synchronize()
+    assert len(rc.states) == L
+    worst = max(O.rel_err(to_np(rc.states[t]), rst[:, :, t]) for t in range(L))
+    assert worst < REF_TOL, worst
+
+
+@pytest.mark.parametrize("T", [2, 9, 17])
+def test_ragged_steps_conv_and_zero_inputs(O, gdn, dev, T):
+    """Step counts that straddle the in-kernel staging of 8 steps; zero conv state and
+    zero initial state (NULL pointers); conv state hand-off for T < 3 and T >= 3."""
+    log_case(f"ragged T={T} conv, NULL conv state and NULL state")
+    inp = O.make_inputs(config=9, layer=T, B=2, L=T, conv=True, conv_state=False,
+                        zero_state=True)
+    ref = O.reference_layer(inp)
+    out = run_layers(gdn, dev, [inp], o_dtype="f32")
+    check_state(O, out["state"][0], ref["state"], "state")
+    check_o(O, out["o"][0], ref["o"], "f32", "o")
+    assert np.array_equal(out["conv"][0], ref["xp"][:, -3:])
+    inp2 = O.make_inputs(config=9, layer=T + 100, B=2, L=T, conv=True)
+    ref2 = O.reference_layer(inp2)
+    out2 = run_layers(gdn, dev, [inp2], o_dtype="f32")
+    check_state(O, out2["state"][0], ref2["state"], "state (with conv state)")
+    assert np.array_equal(out2["conv"][0], ref2["xp"][:, -3:])
+
+
+def test_empty_block_copies_state_and_conv(O, gdn, dev):
+    import torch
+    log_case("T=0 block")
+    inp = O.make_inputs(config=9, layer=1, B=2, L=1, conv=True)
+    S = to_dev(inp.state, dev)
+    out = torch.zeros_like(S)
+    cs = to_dev(inp.conv_state, dev)
+    cout = torch.zeros_like(cs)
+    x = to_dev(np.zeros((2, 0, inp.x.shape[2]), np.uint16), dev)
+    o = torch.empty((2, 0, 48, D), dtype=torch.bfloat16, device=dev)
+    args = gdn.layer_args(B=2, T=0, x=x, conv_weight=to_dev(inp.conv_w, dev), conv_state_in=cs,
+                          conv_state_out=cout, a=None, b=None, alpha=None, beta=None,
+                          state_in=S, state_out=out, o=o)
+    gdn.call_run(args)
+    torch.cuda.synchronize()
+    assert torch.equal(out, S) and torch.equal(cout.view(torch.int16), cs.view(torch.int16))
+
+
+def test_in_place_equals_out_of_place_multi_layer(O, gdn, dev):
+    log_case("in place vs out of place, 3 layers qkv B=3")
+    inps = [O.make_inputs(config=5, layer=l, B=3, L=1) for l in range(3)]
+    a = run_layers(gdn, dev, inps, o_dtype="f32", in_place=False)
+    b = run_layers(gdn, dev, inps, o_dtype="f32", in_place=True)
+    assert np.array_equal(a["state"], b["state"]) and np.array_equal(a["o"], b["o"])
+    for l in range(3):
+        ref = O.reference_layer(inps[l])
+        check_state(O, a["state"][l], ref["state"], f"layer {l}")
+
+
+def test_deltacache_spec_equals_plain(O, gdn, dev):
+    """The verify contract (session.cpp:476-515): record a 5-token block, commit(j), then
+    decode on; the cache must equal one that decoded the j accepted tokens directly."""
+    import torch
+    log_case("DeltaCache record/commit == plain decode")
+    B = 2
+    inp = O.make_inputs(config=3, layer=4, B=B, L=6, conv=True)
+    w = to_dev(inp.conv_w, dev)
+    Al, dt = to_dev(inp.A_log, dev), to_dev(inp.dt_bias, dev)
+    x = to_dev(inp.x, dev)
+    a, b = to_dev(inp.a, dev), to_dev(inp.b, dev)
+    for j in (0, 2, 5):
+        spec = gdn.DeltaCache(B, device=dev)
+        plain = gdn.DeltaCache(B, device=dev)
+        for c in (spec, plain):
+            c.state.copy_(to_dev(inp.state, dev))
+            c.conv.copy_(to_dev(inp.conv_state, dev))
+        spec.record = True
+        spec.step(x[:, :5].contiguous(), w, a[:, :5].contiguous(), b[:, :5].contiguous(), Al, dt)
+        spec.commit(j)
+        for t in range(j):
+            plain.step(x[:, t:t + 1].contiguous(), w, a[:, t:t + 1].contiguous(),
+                       b[:, t:t + 1].contiguous(), Al, dt)
+        assert spec.offset == plain.offset == j
+        o1 = spec.step(x[:, 5:6].contiguous(), w, a[:, 5:6].contiguous(), b[:, 5:6].contiguous(), Al, dt)
+        o2 = plain.step(x[:, 5:6].contiguous(), w, a[:, 5:6].contiguous(), b[:, 5:6].contiguous(), Al, dt)
+        torch.cuda.synchronize()
+        assert torch.equal(spec.conv.view(torch.int16), plain.conv.view(torch.int16))
+        assert torch.equal(spec.state, plain.state), j
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+def test_gpu_rejects_bad_arguments_without_launching(gdn, dev):
+    import torch
+    log_case("argument errors on the GPU path")
+    S = torch.zeros((1, 48, D, D), device=dev)
+    q = torch.zeros((1, 1, 16, D), dtype=torch.bfloat16, device=dev)
+    v = torch.zeros((1, 1, 48, D), dtype=torch.bfloat16, device=dev)
+    ab = torch.zeros((1, 1, 48), device=dev)
+    o = torch.zeros((1, 1, 48, D), dtype=torch.bfloat16, device=dev)
+    args = gdn.layer_args(B=1, T=1, q=q, k=q, v=v, alpha=ab, beta=ab, state_in=S,
+                          state_out=S, o=o)
+    args.state_out = S.data_ptr() + 16  # partial overlap with state_in
+    with pytest.raises(gdn.GdnError, match="state_out must equal"):
+        gdn.call_run(args)
+    args.state_out = S.data_ptr()
+    args.num_v_heads = 47
+    with pytest.raises(gdn.GdnError, match="multiple"):
+        gdn.call_run(args)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(S).item() == 0
