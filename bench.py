@@ -86,12 +86,28 @@ def make_layer_inputs(torch, dev, nl: int, B: int, T: int, conv: bool, seed: int
 
 
 class Timer:
-    """HIP events on torch's current stream (the stream the library launches on)."""
+    """HIP events on torch's current stream (the stream the library launches on).
+
+    Before the timed launches are enqueued, the stream is held by a spin kernel long
+    enough for the host to enqueue all of them, so the event pairs bracket GPU work only
+    (host-side launch overhead would otherwise leave the GPU idle between short kernels).
+    """
 
     def __init__(self, torch):
         self.torch = torch
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize()
+        s.record()
+        torch.cuda._sleep(2_000_000)
+        e.record()
+        torch.cuda.synchronize()
+        self.cycles_per_ms = 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
-    def time_calls(self, fn, steps: int, warmup: int):
+    def hold(self, ms: float):
+        self.torch.cuda._sleep(int(self.cycles_per_ms * ms))
+
+    def time_calls(self, fn, steps: int, warmup: int, host_us_per_call: float = 60.0):
         torch = self.torch
         for i in range(warmup):
             fn(i)
@@ -100,6 +116,7 @@ class Timer:
                for _ in range(steps)]
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
+        self.hold(2.0 + steps * host_us_per_call * 1e-3)
         t0.record()
         for i in range(steps):
             evs[i][0].record()

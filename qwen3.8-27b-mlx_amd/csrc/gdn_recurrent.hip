@@ -2,33 +2,44 @@
 // (T steps, every per-step state written) and any other T.
 //
 // Work decomposition. One workgroup = 4 wave64s = one (layer, batch, v-head,
-// 64-row Dv tile). Each wave owns 16 state rows; inside a wave, each 16-lane row of
-// the wave (a DPP row) owns one state row at a time and the wave holds 4 rows per
-// lane group ("slots"), so a lane keeps 4 x 8 fp32 state elements in registers.
-// Lane j of a group holds elements [4j, 4j+4) and [64+4j, 64+4j+4) of its rows: one
-// float4 load instruction of the wave reads 4 rows x 256 contiguous bytes.
+// 64-row Dv tile): 32 KB of fp32 state, read once and written once per call whatever T
+// is. Each wave owns 16 state rows; inside a wave each 16-lane DPP row owns one state
+// row at a time and a lane holds 4 rows ("slots") x 8 fp32 elements: [4j, 4j+4) and
+// [64+4j, 64+4j+4) for lane j of the group, so one float4 load instruction of the wave
+// reads 4 rows x 256 contiguous bytes. State traffic is non-temporal: it is streamed
+// once per step and would only evict the small shared inputs from the caches.
 //
-// The state is read once and written once per call whatever T is: rows stay in
-// registers while the steps run. q, k, v and the gates of up to 8 steps are staged
-// in LDS by the workgroup (computed there from x in the conv front end), then every
-// wave applies the steps to its rows:
+// q, k, the tile's v rows and the gates of up to 8 steps are staged in LDS by the
+// workgroup (computed there from x in the conv front end: causal depthwise conv,
+// SiLU, l2norm, q scale, gate math), then every wave applies the steps to its rows:
 //   kS = k . s            (per-lane partial dot, then a 16-lane DPP butterfly)
 //   s  = a (s - b kS k) + b v_r k
 //   o_r = q . s           (partial dot + DPP butterfly)
 // Both reductions stay inside a DPP row: no LDS, no atomics.
 //
-// Reference semantics: cpp/src/delta.cpp:185-200 (step), 87-94 (collect), the gates
-// of cpp/src/model.cpp:608-612 and the front end of model.cpp:585-606 / 385-395.
+// Decode (T = 1) orders its memory traffic for latency: the front end's few loads are
+// issued first, then the tile's state loads, so the front-end arithmetic runs while the
+// state is in flight (loads retire in order, so the reverse order would make the front
+// end wait for the whole tile).
+//
+// Blocks are mapped XCD-aware: the 6 workgroups that share a k-head (3 v-heads x 2
+// tiles) run on one XCD, whose L2 then serves their shared q/k/x reads.
+//
+// Reference semantics: cpp/src/delta.cpp:185-200 (step), 87-94 (collect), the gates of
+// cpp/src/model.cpp:608-612 and the front end of model.cpp:585-606 / 385-395.
 #include "gdn_device_math.h"
 #include "gdn_internal.h"
 
 namespace gdn {
 namespace {
 
-constexpr int kTileRows = 64;   // Dv rows per workgroup
-constexpr int kThreads = 256;   // 4 waves
-constexpr int kSlots = 4;       // rows per 16-lane group
-constexpr int kTC = 8;          // steps staged in LDS per pass
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 64;                 // Dv rows per workgroup
+constexpr int kTilesPerHead = kD / kTileRows; // 2
+constexpr int kThreads = 256;                 // 4 waves
+constexpr int kSlots = 4;                     // rows per 16-lane group
+constexpr int kTC = 8;                        // steps staged in LDS per pass
 
 // Sum over the 16 lanes of a DPP row; every lane receives the same total.
 // quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror.
@@ -53,25 +64,13 @@ __device__ __forceinline__ float load_qkv(const void* base, size_t i, int bf16) 
   return bf16 ? bf2f(static_cast<const uint16_t*>(base)[i]) : static_cast<const float*>(base)[i];
 }
 
-// One conv channel at step t (model.cpp:385-395): taps in order j = 0..3, every
-// product and partial sum rounded to bf16; xp row r is conv_in[r] for r < 3 else x[r-3].
-__device__ __forceinline__ float conv_channel(const uint16_t* __restrict__ x_b,
-                                              const uint16_t* __restrict__ cin_b,
-                                              const uint16_t* __restrict__ w, int C, int c,
-                                              int t) {
-  float y = 0.0f;
+// Causal depthwise conv at one channel from its 4 xp rows and 4 taps
+// (model.cpp:385-395): taps in order j = 0..3, every product and partial sum rounded
+// to bf16.
+__device__ __forceinline__ float conv4(const float (&xv)[kTaps], const float (&wv)[kTaps]) {
+  float y = rbf(xv[0] * wv[0]);
 #pragma unroll
-  for (int j = 0; j < kTaps; ++j) {
-    const int r = t + j;
-    float xv;
-    if (r < kConvRows) {
-      xv = cin_b ? bf2f(cin_b[(size_t)r * C + c]) : 0.0f;
-    } else {
-      xv = bf2f(x_b[(size_t)(r - kConvRows) * C + c]);
-    }
-    const float prod = rbf(xv * bf2f(w[(size_t)j * C + c]));
-    y = (j == 0) ? prod : rbf(y + prod);
-  }
+  for (int j = 1; j < kTaps; ++j) y = rbf(y + rbf(xv[j] * wv[j]));
   return y;
 }
 
@@ -81,242 +80,460 @@ __device__ __forceinline__ float silu_bf(float y) {
   return rbf(y * sg);
 }
 
+// l2norm of a 128-vector held as (u0, u1) = elements (lane, lane+64) of a wave
+// (ops.cpp:27-30): x * rsqrt(sum(x*x) + eps), every op in bf16; q additionally gets the
+// 128^-0.5 scale (model.cpp:601).
+__device__ __forceinline__ void l2norm_pair(float u0, float u1, bool scale, float& y0, float& y1) {
+  const float scale_b = rbf(1.0f / sqrtf((float)kD));
+  const float eps_b = rbf(1e-6f);
+  const float pr = rbf(u0 * u0) + rbf(u1 * u1);
+  const float ssum = rbf(wave64_sum(pr));
+  const float den = rbf(ssum + eps_b);
+  const float rs = rbf(1.0f / sqrtf(den));
+  y0 = rbf(u0 * rs);
+  y1 = rbf(u1 * rs);
+  if (scale) {
+    y0 = rbf(y0 * scale_b);
+    y1 = rbf(y1 * scale_b);
+  }
+}
+
+struct Tile {
+  int layer, bb, h, g, r0, tile;
+  size_t lb, head;
+};
+
+__device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
+  int bid = blockIdx.x;
+  if (p.remap) {
+    const int per = p.nblocks >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  Tile t;
+  t.tile = bid % kTilesPerHead;
+  int rest = bid / kTilesPerHead;
+  t.h = rest % p.Hv;
+  rest /= p.Hv;
+  t.bb = rest % p.B;
+  t.layer = rest / p.B;
+  t.g = t.h / p.rep;
+  t.r0 = t.tile * kTileRows;
+  t.lb = (size_t)t.layer * p.B + t.bb;
+  t.head = t.lb * p.Hv + t.h;
+  return t;
+}
+
+__device__ __forceinline__ int row_of(int wave, int i, int grp) { return wave * 4 * kSlots + i * 4 + grp; }
+
+__device__ __forceinline__ void load_state(const RecurrentParams& p, const Tile& t, int wave,
+                                           int grp, int j16, f4v (&s)[kSlots][2]) {
+  if (p.state_in) {
+    const float* base = p.state_in + t.head * kD * kD;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int row = t.r0 + row_of(wave, i, grp);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        s[i][hf] = __builtin_nontemporal_load(
+            reinterpret_cast<const f4v*>(base + (size_t)row * kD + hf * 64 + j16 * 4));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+__device__ __forceinline__ void store_rows(float* base, const Tile& t, int wave, int grp, int j16,
+                                           const f4v (&s)[kSlots][2]) {
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int row = t.r0 + row_of(wave, i, grp);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      __builtin_nontemporal_store(s[i][hf],
+                                  reinterpret_cast<f4v*>(base + (size_t)row * kD + hf * 64 + j16 * 4));
+    }
+  }
+}
+
+// The conv state hand-off: rows T..T+2 of [conv_in ; x] for this tile's v channels,
+// plus the q (first tile) or k (second tile) channels of the k-head when h is its
+// k-head's first v-head. Every channel has exactly one writer.
+__device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const Tile& t,
+                                               const uint16_t* x_b, const uint16_t* cin_b) {
+  uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
+  const int vbase = 2 * p.Hk * kD + t.h * kD + t.r0;
+  const bool qk_writer = (t.h % p.rep) == 0;
+  const int qkbase = (t.tile == 0 ? 0 : p.Hk * kD) + t.g * kD;
+  const int nch = kTileRows + (qk_writer ? kD : 0);
+  for (int e = threadIdx.x; e < nch * kConvRows; e += kThreads) {
+    const int r = e / nch;
+    const int ci = e % nch;
+    const int c = ci < kTileRows ? vbase + ci : qkbase + (ci - kTileRows);
+    const int src = p.T + r;  // row of xp
+    uint16_t val;
+    if (src < kConvRows) {
+      val = cin_b ? cin_b[(size_t)src * p.C + c] : (uint16_t)0;
+    } else {
+      val = x_b[(size_t)(src - kConvRows) * p.C + c];
+    }
+    cout_b[(size_t)r * p.C + c] = val;
+  }
+}
+
+template <bool COLLECT>
+__device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
+                                           float al, float be, const float* kk, const float* qq,
+                                           const float* vv, int wave, int grp, int j16,
+                                           f4v (&s)[kSlots][2]) {
+  const f4v k0 = *reinterpret_cast<const f4v*>(kk + j16 * 4);
+  const f4v k1 = *reinterpret_cast<const f4v*>(kk + 64 + j16 * 4);
+  const f4v q0 = *reinterpret_cast<const f4v*>(qq + j16 * 4);
+  const f4v q1 = *reinterpret_cast<const f4v*>(qq + 64 + j16 * 4);
+  float ov[kSlots];
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const float vr = vv[row_of(wave, i, grp)];
+    f4v& a0 = s[i][0];
+    f4v& a1 = s[i][1];
+    float pk = k0.x * a0.x;
+    pk = __builtin_fmaf(k0.y, a0.y, pk);
+    pk = __builtin_fmaf(k0.z, a0.z, pk);
+    pk = __builtin_fmaf(k0.w, a0.w, pk);
+    pk = __builtin_fmaf(k1.x, a1.x, pk);
+    pk = __builtin_fmaf(k1.y, a1.y, pk);
+    pk = __builtin_fmaf(k1.z, a1.z, pk);
+    pk = __builtin_fmaf(k1.w, a1.w, pk);
+    const float kS = row16_sum(pk);
+    const float nbk = -(be * kS);
+    const float bv = be * vr;
+#define GDN_UPD(S, K) S = __builtin_fmaf(al, __builtin_fmaf(nbk, K, S), bv * K)
+    GDN_UPD(a0.x, k0.x); GDN_UPD(a0.y, k0.y); GDN_UPD(a0.z, k0.z); GDN_UPD(a0.w, k0.w);
+    GDN_UPD(a1.x, k1.x); GDN_UPD(a1.y, k1.y); GDN_UPD(a1.z, k1.z); GDN_UPD(a1.w, k1.w);
+#undef GDN_UPD
+    float po = q0.x * a0.x;
+    po = __builtin_fmaf(q0.y, a0.y, po);
+    po = __builtin_fmaf(q0.z, a0.z, po);
+    po = __builtin_fmaf(q0.w, a0.w, po);
+    po = __builtin_fmaf(q1.x, a1.x, po);
+    po = __builtin_fmaf(q1.y, a1.y, po);
+    po = __builtin_fmaf(q1.z, a1.z, po);
+    po = __builtin_fmaf(q1.w, a1.w, po);
+    ov[i] = row16_sum(po);
+  }
+  if (COLLECT) {
+    float* dst = p.states_tbh
+                     ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
+                     : p.states + (t.head * p.T + step) * kD * kD;
+    store_rows(dst, t, wave, grp, j16, s);
+  }
+  // lane j (< kSlots) of each group writes the output of slot j
+  if (j16 < kSlots) {
+    float val = ov[0];
+#pragma unroll
+    for (int i = 1; i < kSlots; ++i) val = (j16 == i) ? ov[i] : val;
+    const int row = t.r0 + row_of(wave, j16, grp);
+    const size_t oi = ((t.lb * p.T + step) * p.Hv + t.h) * kD + row;
+    if (p.o_bf16) {
+      static_cast<uint16_t*>(p.o)[oi] = f2bf(val);
+    } else {
+      static_cast<float*>(p.o)[oi] = val;
+    }
+  }
+}
+
+// Address of row r of the padded conv input xp = [conv_in ; x] at channel c. A row of a
+// missing (zero) conv state points at x instead -- a valid address -- and its value is
+// replaced by zero after the load (xp_value), so the loads carry no branches and can all
+// be in flight together.
+__device__ __forceinline__ const uint16_t* xp_addr(const uint16_t* __restrict__ x_b,
+                                                   const uint16_t* __restrict__ cin_b, int C,
+                                                   int c, int r) {
+  if (r >= kConvRows) return x_b + (size_t)(r - kConvRows) * C + c;
+  return cin_b ? cin_b + (size_t)r * C + c : x_b + c;
+}
+
+__device__ __forceinline__ float xp_value(uint32_t raw, const uint16_t* cin_b, int r) {
+  return (r < kConvRows && !cin_b) ? 0.0f : bf2f((uint16_t)raw);
+}
+
+// Raw gate inputs of one (step, v-head): (a, b, A_log, dt_bias) or (alpha, beta).
+struct GateRaw {
+  uint32_t g0 = 0, g1 = 0, g2 = 0, g3 = 0;
+};
+
+__device__ __forceinline__ GateRaw gate_load(const RecurrentParams& p, int layer, int h, size_t gi) {
+  GateRaw r;
+  if (p.gate_raw) {
+    r.g0 = p.a[gi];
+    r.g1 = p.b[gi];
+    r.g2 = f_bits(p.A_log[(size_t)layer * p.Hv + h]);
+    r.g3 = f_bits(p.dt_bias[(size_t)layer * p.Hv + h]);
+  } else {
+    r.g0 = f_bits(p.alpha[gi]);
+    r.g1 = f_bits(p.beta[gi]);
+  }
+  return r;
+}
+
+__device__ __forceinline__ void gate_math(const RecurrentParams& p, const GateRaw& r, float& al,
+                                          float& be) {
+  if (p.gate_raw) {
+    d_gates(bf2f((uint16_t)r.g0), bf2f((uint16_t)r.g1), bits_f(r.g2), bits_f(r.g3), al, be);
+  } else {
+    al = bits_f(r.g0);
+    be = bits_f(r.g1);
+  }
+}
+
+__device__ __forceinline__ uint32_t qkv_raw(const void* base, size_t i, int bf16) {
+  return bf16 ? (uint32_t) static_cast<const uint16_t*>(base)[i]
+              : static_cast<const uint32_t*>(base)[i];
+}
+
+__device__ __forceinline__ float qkv_value(uint32_t raw, int bf16) {
+  return bf16 ? bf2f((uint16_t)raw) : bits_f(raw);
+}
+
+// Front-end channel of a wave in the conv front end: wave 0 -> q channels (lane,
+// lane+64) of k-head g, wave 1 -> k channels, wave 2 -> the tile's v channels.
+__device__ __forceinline__ int fe_channel(const RecurrentParams& p, const Tile& t, int wave,
+                                          int lane) {
+  return wave == 0 ? t.g * kD + lane
+       : wave == 1 ? p.Hk * kD + t.g * kD + lane
+                   : 2 * p.Hk * kD + t.h * kD + t.r0 + lane;
+}
+
+// ---------------------------------------------------------------- decode, T = 1
+
+template <int FE>
+__global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
+  __shared__ float sm_q[kD];
+  __shared__ float sm_k[kD];
+  __shared__ float sm_v[kTileRows];
+  __shared__ float sm_ab[2];
+
+  const Tile t = decode_block(p);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4, j16 = lane & 15;
+  const size_t row0 = t.lb;  // (layer, b) at step 0
+
+  // 1. the front end's global loads, all in flight together
+  uint32_t xr[2][kTaps] = {}, wr[2][kTaps] = {};
+  uint32_t fe_raw = 0, v_raw = 0;
+  const uint16_t* x_b = nullptr;
+  const uint16_t* cin_b = nullptr;
+  int c0 = 0;
+  if (FE == 1) {
+    x_b = p.x + t.lb * (size_t)p.C;
+    cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
+    const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
+    // Every wave issues the same loads (no branch, so nothing waits on them early);
+    // waves 2 and 3 read their one channel twice, wave 3's values go unused.
+    c0 = fe_channel(p, t, wave < 3 ? wave : 2, lane);
+    const int c1 = wave < 2 ? c0 + 64 : c0;
+#pragma unroll
+    for (int j = 0; j < kTaps; ++j) {
+      xr[0][j] = *xp_addr(x_b, cin_b, p.C, c0, j);
+      wr[0][j] = w_l[(size_t)j * p.C + c0];
+      xr[1][j] = *xp_addr(x_b, cin_b, p.C, c1, j);
+      wr[1][j] = w_l[(size_t)j * p.C + c1];
+    }
+  } else {
+    // thread i stages q[i] (i < 128) or k[i - 128]; threads < 64 also the tile's v rows
+    fe_raw = qkv_raw(tid < kD ? p.q : p.k, (row0 * p.Hk + t.g) * kD + (tid & (kD - 1)), p.qkv_bf16);
+    if (tid < kTileRows) v_raw = qkv_raw(p.v, (row0 * p.Hv + t.h) * kD + t.r0 + tid, p.qkv_bf16);
+  }
+  // 2. the tile's state; then the gate inputs, which only wave 3 waits for
+  f4v s[kSlots][2];
+  load_state(p, t, wave, grp, j16, s);
+  GateRaw gr;
+  if (wave == 3) gr = gate_load(p, t.layer, t.h, row0 * p.Hv + t.h);
+  __builtin_amdgcn_sched_barrier(0);  // keep the front-end arithmetic below the loads
+
+  // 3. front-end arithmetic while the state is in flight
+  if (FE == 1) {
+    if (wave < 3) {
+      float u[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        float xv[kTaps], wv[kTaps];
+#pragma unroll
+        for (int j = 0; j < kTaps; ++j) {
+          xv[j] = xp_value(xr[m][j], cin_b, j);
+          wv[j] = bf2f((uint16_t)wr[m][j]);
+        }
+        u[m] = silu_bf(conv4(xv, wv));
+      }
+      if (wave < 2) {
+        float y0, y1;
+        l2norm_pair(u[0], u[1], wave == 0, y0, y1);
+        float* dst = wave == 0 ? sm_q : sm_k;
+        dst[lane] = y0;
+        dst[lane + 64] = y1;
+      } else {
+        sm_v[lane] = u[0];
+      }
+    }
+  } else {
+    const float val = qkv_value(fe_raw, p.qkv_bf16);
+    if (tid < kD) sm_q[tid] = val;
+    else sm_k[tid - kD] = val;
+    if (tid < kTileRows) sm_v[tid] = qkv_value(v_raw, p.qkv_bf16);
+  }
+  if (wave == 3) {
+    float al, be;
+    gate_math(p, gr, al, be);
+    if (lane == 0) {
+      sm_ab[0] = al;
+      sm_ab[1] = be;
+    }
+  }
+  __syncthreads();
+
+  // 4. the step, then the state goes back
+  apply_step<false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
+  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+
+  // 5. conv state hand-off from the rows already in registers: new rows 0..2 are xp
+  // rows 1..3. This tile's v channels; the q (tile 0) or k (tile 1) channels of the
+  // k-head when h is its k-head's first v-head -- every channel has one writer.
+  if (FE == 1 && p.conv_out) {
+    uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
+    const bool qk_writer = (t.h % p.rep) == 0 && wave == t.tile;
+    const int nm = wave == 2 ? 1 : (wave < 2 && qk_writer ? 2 : 0);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (m < nm) {
+#pragma unroll
+        for (int r = 0; r < kConvRows; ++r) {
+          const bool zero = (r + 1 < kConvRows) && !cin_b;
+          cout_b[(size_t)r * p.C + c0 + 64 * m] = zero ? (uint16_t)0 : (uint16_t)xr[m][r + 1];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- any T (verify, prefill-size L)
+
 template <int FE, bool COLLECT>
-__global__ __launch_bounds__(kThreads) void recurrent_kernel(RecurrentParams p) {
-  __shared__ float4 sm_q[kTC][kD / 4];
-  __shared__ float4 sm_k[kTC][kD / 4];
+__global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
+  __shared__ float sm_q[kTC][kD];
+  __shared__ float sm_k[kTC][kD];
   __shared__ float sm_v[kTC][kTileRows];
   __shared__ float sm_a[kTC];
   __shared__ float sm_b[kTC];
 
-  int bid = blockIdx.x;
-  if (p.remap) {
-    // Consecutive logical blocks (the 3 v-heads x 2 tiles that share a k-head) land on
-    // the same XCD, whose L2 then serves their shared q/k/x reads.
-    const int per = p.nblocks >> 3;
-    bid = (bid & 7) * per + (bid >> 3);
-  }
-  const int tile = bid & 1;
-  int rest = bid >> 1;
-  const int h = rest % p.Hv;
-  rest /= p.Hv;
-  const int bb = rest % p.B;
-  const int layer = rest / p.B;
-  const int g = h / p.rep;
-  const int r0 = tile * kTileRows;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int grp = lane >> 4;
-  const int j16 = lane & 15;
-
+  const Tile t = decode_block(p);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = lane >> 4, j16 = lane & 15;
   const int T = p.T;
-  const size_t lb = (size_t)layer * p.B + bb;         // (layer, b)
-  const size_t head = lb * p.Hv + h;                  // (layer, b, h)
-  const size_t DD = (size_t)kD * kD;
+  constexpr int kWin = kTC + kTaps - 1;  // xp rows feeding one chunk
 
-  // ---- issue the state loads first: they do not depend on the front end ----
-  float4 s[kSlots][2];
-  {
-    const float* sin = p.state_in ? p.state_in + head * DD : nullptr;
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int row = r0 + wave * 16 + i * 4 + grp;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        if (sin) {
-          s[i][hf] = *reinterpret_cast<const float4*>(sin + (size_t)row * kD + hf * 64 + j16 * 4);
-        } else {
-          s[i][hf] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-    }
-  }
-
-  // ---- conv state hand-off (conv front end): rows T..T+2 of [conv_in ; x] ----
   const uint16_t* x_b = nullptr;
   const uint16_t* cin_b = nullptr;
   const uint16_t* w_l = nullptr;
+  int c0 = 0;
+  float wv[2][kTaps] = {};
   if (FE == 1) {
-    x_b = p.x + lb * (size_t)T * p.C;
-    cin_b = p.conv_in ? p.conv_in + lb * (size_t)kConvRows * p.C : nullptr;
-    w_l = p.conv_w + (size_t)layer * kTaps * p.C;
-    if (p.conv_out) {
-      uint16_t* cout_b = p.conv_out + lb * (size_t)kConvRows * p.C;
-      // v channels of this tile; q (tile 0) or k (tile 1) channels of the k-head when
-      // this is the k-head's first v-head. Each channel has exactly one writer.
-      const int vbase = 2 * p.Hk * kD + h * kD + r0;
-      const bool qk_writer = (h % p.rep) == 0;
-      const int qkbase = (tile == 0 ? 0 : p.Hk * kD) + g * kD;
-      const int nch = kTileRows + (qk_writer ? kD : 0);
-      for (int e = tid; e < nch * kConvRows; e += kThreads) {
-        const int r = e / nch;
-        const int ci = e % nch;
-        const int c = ci < kTileRows ? vbase + ci : qkbase + (ci - kTileRows);
-        const int src = T + r;  // row of xp
-        uint16_t val;
-        if (src < kConvRows) {
-          val = cin_b ? cin_b[(size_t)src * p.C + c] : (uint16_t)0;
-        } else {
-          val = x_b[(size_t)(src - kConvRows) * p.C + c];
-        }
-        cout_b[(size_t)r * p.C + c] = val;
-      }
-    }
+    x_b = p.x + t.lb * (size_t)T * p.C;
+    cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
+    w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
+    c0 = fe_channel(p, t, wave, lane);
   }
+  const int nm = wave < 2 ? 2 : 1;  // conv channels per lane (waves 0..2)
 
-  const float scale_b = rbf(1.0f / sqrtf((float)kD));
-  const float eps_b = rbf(1e-6f);
-
+  f4v s[kSlots][2];
   for (int t0 = 0; t0 < T; t0 += kTC) {
     const int tc = min(kTC, T - t0);
     if (t0 > 0) __syncthreads();  // the previous pass is done reading LDS
 
-    // ---- front end for steps t0 .. t0+tc-1 into LDS ----
+    // front-end loads of the chunk (raw bits, all in flight together)
+    uint32_t xr[2][kWin] = {};
+    uint32_t wr[2][kTaps] = {};
+    if (FE == 1 && wave < 3) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        if (m < nm) {
+#pragma unroll
+          for (int r = 0; r < kWin; ++r) {
+            if (r < tc + kTaps - 1) xr[m][r] = *xp_addr(x_b, cin_b, p.C, c0 + 64 * m, t0 + r);
+          }
+          if (t0 == 0) {
+#pragma unroll
+            for (int j = 0; j < kTaps; ++j) wr[m][j] = w_l[(size_t)j * p.C + c0 + 64 * m];
+          }
+        }
+      }
+    }
+    GateRaw gr;
+    const int gt = tid - (kThreads - kTC);  // the last 8 threads: one step each
+    if (gt >= 0 && gt < tc) gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gt)) * p.Hv + t.h);
+
+    if (t0 == 0) load_state(p, t, wave, grp, j16, s);
+
     if (FE == 0) {
-      float* q_s = reinterpret_cast<float*>(sm_q);
-      float* k_s = reinterpret_cast<float*>(sm_k);
       const int per = 2 * kD + kTileRows;
       for (int e = tid; e < tc * per; e += kThreads) {
         const int tt = e / per;
         const int c = e % per;
-        const size_t row = lb * T + (t0 + tt);
+        const size_t row = t.lb * T + (t0 + tt);
         if (c < kD) {
-          q_s[tt * kD + c] = load_qkv(p.q, (row * p.Hk + g) * kD + c, p.qkv_bf16);
+          sm_q[tt][c] = load_qkv(p.q, (row * p.Hk + t.g) * kD + c, p.qkv_bf16);
         } else if (c < 2 * kD) {
-          k_s[tt * kD + c - kD] = load_qkv(p.k, (row * p.Hk + g) * kD + c - kD, p.qkv_bf16);
+          sm_k[tt][c - kD] = load_qkv(p.k, (row * p.Hk + t.g) * kD + c - kD, p.qkv_bf16);
         } else {
-          sm_v[tt][c - 2 * kD] = load_qkv(p.v, (row * p.Hv + h) * kD + r0 + c - 2 * kD, p.qkv_bf16);
+          sm_v[tt][c - 2 * kD] = load_qkv(p.v, (row * p.Hv + t.h) * kD + t.r0 + c - 2 * kD, p.qkv_bf16);
         }
       }
-    } else {
-      if (wave < 2) {
-        // wave 0: q of k-head g; wave 1: k. Lane l: channels l and l+64 of the head.
-        float* dst = reinterpret_cast<float*>(wave == 0 ? sm_q : sm_k);
-        const int cbase = (wave == 0 ? 0 : p.Hk * kD) + g * kD;
-        for (int tt = 0; tt < tc; ++tt) {
-          const int t = t0 + tt;
-          const float u0 = silu_bf(conv_channel(x_b, cin_b, w_l, p.C, cbase + lane, t));
-          const float u1 = silu_bf(conv_channel(x_b, cin_b, w_l, p.C, cbase + lane + 64, t));
-          // l2norm (ops.cpp:27-30): x * rsqrt(sum(x*x) + eps), every op in bf16
-          const float pr = rbf(u0 * u0) + rbf(u1 * u1);
-          const float ssum = rbf(wave64_sum(pr));
-          const float den = rbf(ssum + eps_b);
-          const float rs = rbf(1.0f / sqrtf(den));
-          float y0 = rbf(u0 * rs);
-          float y1 = rbf(u1 * rs);
-          if (wave == 0) {  // q *= 128^-0.5 (model.cpp:601)
-            y0 = rbf(y0 * scale_b);
-            y1 = rbf(y1 * scale_b);
+    } else if (wave < 3) {
+      if (t0 == 0) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+#pragma unroll
+          for (int j = 0; j < kTaps; ++j) wv[m][j] = bf2f((uint16_t)wr[m][j]);
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < kTC; ++tt) {
+        if (tt < tc) {
+          float u[2] = {0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            if (m < nm) {
+              float xv[kTaps];
+#pragma unroll
+              for (int j = 0; j < kTaps; ++j) xv[j] = xp_value(xr[m][tt + j], cin_b, t0 + tt + j);
+              u[m] = silu_bf(conv4(xv, wv[m]));
+            }
           }
-          dst[tt * kD + lane] = y0;
-          dst[tt * kD + lane + 64] = y1;
-        }
-      } else if (wave == 2) {
-        const int c = 2 * p.Hk * kD + h * kD + r0 + lane;
-        for (int tt = 0; tt < tc; ++tt) {
-          sm_v[tt][lane] = silu_bf(conv_channel(x_b, cin_b, w_l, p.C, c, t0 + tt));
+          if (wave < 2) {
+            float y0, y1;
+            l2norm_pair(u[0], u[1], wave == 0, y0, y1);
+            float* dst = wave == 0 ? sm_q[tt] : sm_k[tt];
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+          } else {
+            sm_v[tt][lane] = u[0];
+          }
         }
       }
     }
-    // gates: one thread per step
-    if (tid >= kThreads - kTC) {
-      const int tt = tid - (kThreads - kTC);
-      if (tt < tc) {
-        const size_t gi = (lb * T + (t0 + tt)) * p.Hv + h;
-        float al, be;
-        if (p.gate_raw) {
-          d_gates(bf2f(p.a[gi]), bf2f(p.b[gi]), p.A_log[(size_t)layer * p.Hv + h],
-                  p.dt_bias[(size_t)layer * p.Hv + h], al, be);
-        } else {
-          al = p.alpha[gi];
-          be = p.beta[gi];
-        }
-        sm_a[tt] = al;
-        sm_b[tt] = be;
-      }
-    }
+    if (gt >= 0 && gt < tc) gate_math(p, gr, sm_a[gt], sm_b[gt]);
     __syncthreads();
 
-    // ---- apply the steps to this wave's rows ----
     for (int tt = 0; tt < tc; ++tt) {
-      const int t = t0 + tt;
-      const float al = sm_a[tt];
-      const float be = sm_b[tt];
-      const float4 k0 = sm_k[tt][j16];
-      const float4 k1 = sm_k[tt][16 + j16];
-      const float4 q0 = sm_q[tt][j16];
-      const float4 q1 = sm_q[tt][16 + j16];
-      float ov[kSlots];
-#pragma unroll
-      for (int i = 0; i < kSlots; ++i) {
-        const int rl = wave * 16 + i * 4 + grp;  // row within the tile
-        const float vr = sm_v[tt][rl];
-        float4& a0 = s[i][0];
-        float4& a1 = s[i][1];
-        float pk = k0.x * a0.x;
-        pk = __builtin_fmaf(k0.y, a0.y, pk);
-        pk = __builtin_fmaf(k0.z, a0.z, pk);
-        pk = __builtin_fmaf(k0.w, a0.w, pk);
-        pk = __builtin_fmaf(k1.x, a1.x, pk);
-        pk = __builtin_fmaf(k1.y, a1.y, pk);
-        pk = __builtin_fmaf(k1.z, a1.z, pk);
-        pk = __builtin_fmaf(k1.w, a1.w, pk);
-        const float kS = row16_sum(pk);
-        const float nbk = -(be * kS);
-        const float bv = be * vr;
-#define GDN_UPD(S, K) S = __builtin_fmaf(al, __builtin_fmaf(nbk, K, S), bv * K)
-        GDN_UPD(a0.x, k0.x); GDN_UPD(a0.y, k0.y); GDN_UPD(a0.z, k0.z); GDN_UPD(a0.w, k0.w);
-        GDN_UPD(a1.x, k1.x); GDN_UPD(a1.y, k1.y); GDN_UPD(a1.z, k1.z); GDN_UPD(a1.w, k1.w);
-#undef GDN_UPD
-        float po = q0.x * a0.x;
-        po = __builtin_fmaf(q0.y, a0.y, po);
-        po = __builtin_fmaf(q0.z, a0.z, po);
-        po = __builtin_fmaf(q0.w, a0.w, po);
-        po = __builtin_fmaf(q1.x, a1.x, po);
-        po = __builtin_fmaf(q1.y, a1.y, po);
-        po = __builtin_fmaf(q1.z, a1.z, po);
-        po = __builtin_fmaf(q1.w, a1.w, po);
-        ov[i] = row16_sum(po);
-      }
-      if (COLLECT) {
-        float* dst = p.states_tbh
-                         ? p.states + ((((size_t)layer * T + t) * p.B + bb) * p.Hv + h) * DD
-                         : p.states + (head * T + t) * DD;
-#pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          const int row = r0 + wave * 16 + i * 4 + grp;
-          *reinterpret_cast<float4*>(dst + (size_t)row * kD + j16 * 4) = s[i][0];
-          *reinterpret_cast<float4*>(dst + (size_t)row * kD + 64 + j16 * 4) = s[i][1];
-        }
-      }
-      // lane j (< 4) of each group writes the output of slot j
-      if (j16 < kSlots) {
-        float val = ov[0];
-        if (j16 == 1) val = ov[1];
-        if (j16 == 2) val = ov[2];
-        if (j16 == 3) val = ov[3];
-        const int row = r0 + wave * 16 + j16 * 4 + grp;
-        const size_t oi = ((lb * T + t) * p.Hv + h) * kD + row;
-        if (p.o_bf16) {
-          static_cast<uint16_t*>(p.o)[oi] = f2bf(val);
-        } else {
-          static_cast<float*>(p.o)[oi] = val;
-        }
-      }
+      apply_step<COLLECT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave,
+                          grp, j16, s);
     }
   }
 
-  if (p.state_out) {
-    float* sout = p.state_out + head * DD;
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int row = r0 + wave * 16 + i * 4 + grp;
-      *reinterpret_cast<float4*>(sout + (size_t)row * kD + j16 * 4) = s[i][0];
-      *reinterpret_cast<float4*>(sout + (size_t)row * kD + 64 + j16 * 4) = s[i][1];
-    }
-  }
+  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+  if (FE == 1 && p.conv_out) write_conv_out(p, t, x_b, cin_b);
 }
 
 __global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t n) {
@@ -339,17 +556,23 @@ __global__ void copy_u16_kernel(uint16_t* __restrict__ dst, const uint16_t* __re
 hipError_t launch_recurrent(const RecurrentParams& p, int frontend, bool collect,
                             hipStream_t stream) {
   const dim3 grid(p.nblocks), block(kThreads);
-  if (frontend == 0) {
-    if (collect) {
-      hipLaunchKernelGGL((recurrent_kernel<0, true>), grid, block, 0, stream, p);
+  if (p.T == 1 && !collect) {
+    if (frontend == 0) {
+      hipLaunchKernelGGL((decode_kernel<0>), grid, block, 0, stream, p);
     } else {
-      hipLaunchKernelGGL((recurrent_kernel<0, false>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((decode_kernel<1>), grid, block, 0, stream, p);
+    }
+  } else if (frontend == 0) {
+    if (collect) {
+      hipLaunchKernelGGL((steps_kernel<0, true>), grid, block, 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((steps_kernel<0, false>), grid, block, 0, stream, p);
     }
   } else {
     if (collect) {
-      hipLaunchKernelGGL((recurrent_kernel<1, true>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((steps_kernel<1, true>), grid, block, 0, stream, p);
     } else {
-      hipLaunchKernelGGL((recurrent_kernel<1, false>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((steps_kernel<1, false>), grid, block, 0, stream, p);
     }
   }
   return hipGetLastError();
