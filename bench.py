@@ -185,6 +185,38 @@ def bench_verify(torch, gdn, dev, timer, steps: int, warmup: int, sets: int):
     return r
 
 
+# Chunked prefill, T=4096, chunk 64: normative FLOP counts of the intra-chunk products
+# (Gram K K^T and scores Q K^T per k-head; W = T(beta g K), U = T(beta V) and the intra
+# output (Q K^T . Gamma) V' per v-head) and of the inter-chunk state products.
+def prefill_flops(T: int, C: int = 64):
+    nC = T // C
+    intra = nC * (HK * 2 * 2 * C * C * D + HV * 3 * 2 * C * C * D)
+    inter = nC * HV * 3 * 2 * C * D * D
+    return intra, inter
+
+
+def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096):
+    i = make_layer_inputs(torch, dev, 1, 1, T, True, seed=500)
+    x = i["x"][0].contiguous()
+    o = torch.empty((1, T, HV, D), dtype=torch.bfloat16, device=dev)
+    state_out = torch.empty((1, HV, D, D), device=dev)
+    conv_out = torch.empty((1, 3, C), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(gdn.prefill_workspace_size(1, T), dtype=torch.uint8, device=dev)
+    args = gdn.layer_args(B=1, T=T, x=x, conv_weight=i["conv_weight"][0].contiguous(),
+                          conv_state_in=None, conv_state_out=conv_out, a=i["a"][0].contiguous(),
+                          b=i["b"][0].contiguous(), A_log=i["A_log"][0].contiguous(),
+                          dt_bias=i["dt_bias"][0].contiguous(), state_in=None,
+                          state_out=state_out, o=o, workspace=ws)
+    r = timer.time_calls(lambda it: gdn.call_prefill(args), steps, warmup, host_us_per_call=80.0)
+    intra, inter = prefill_flops(T)
+    sec = r["launch_ms_avg"] * 1e-3
+    return dict(tokens_per_s=T / sec, us_per_call=r["launch_ms_avg"] * 1e3,
+                intra_TFLOPs=intra / sec / 1e12,
+                intra_frac_mfma=intra / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
+                all_products_frac_mfma=(intra + inter) / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
+                intra_flop=intra, inter_flop=inter)
+
+
 def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
     """Device-to-device copy of 604 MB: a practical streaming ceiling for comparison."""
     n = 4 * 48 * HV * D * D // 2
@@ -269,6 +301,11 @@ def main() -> int:
                                    us_per_call=round(r["ms_per_step"] * 1e3, 2),
                                    bytes_per_call=r["bytes_per_step"])
         print(f"# verify B=8 T=5: {r['ms_per_step'] * 1e3:.1f} us, {r['GBps']:.0f} GB/s", flush=True)
+    if want("prefill"):
+        r = bench_prefill(torch, gdn, dev, timer, steps=max(5, args.steps // 10), warmup=3)
+        sec["prefill_t4096"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        print(f"# prefill T=4096: {r['us_per_call']:.1f} us, {r['tokens_per_s'] / 1e6:.2f} M tok/s, "
+              f"intra MFMA frac {r['intra_frac_mfma']:.4f}", flush=True)
     if want("copy"):
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)

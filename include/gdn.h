@@ -114,6 +114,9 @@ typedef struct gdn_layer_args {
   int states_layout;     /* gdn_states_layout */
   void* o;               /* (B, T, Hv, 128), o_dtype; never NULL */
   int o_dtype;           /* gdn_dtype */
+  void* workspace;       /* gdn_prefill_chunked only: caller device memory of at least
+                            gdn_prefill_workspace_size() bytes, 256-byte aligned */
+  size_t workspace_bytes;
   void* stream;          /* hipStream_t */
 } gdn_layer_args;
 
@@ -124,9 +127,15 @@ typedef struct gdn_layer_args {
 int gdn_run(const gdn_layer_args* args);
 
 /* Chunked form (chunk 64, WY/UT transform) for prefill; same arguments as gdn_run
- * except that `states` must be NULL. Intra-chunk products run on bf16 MFMA with fp32
- * accumulation; the state hand-off between chunks stays fp32. */
+ * except that `states` must be NULL, a workspace is required and the qkv front end takes
+ * bf16 q, k, v only. Intra-chunk products run on bf16 MFMA with fp32 accumulation; the
+ * state hand-off between chunks stays fp32. The workspace contents are scratch: they need
+ * no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);
+
+/* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len and head
+ * counts (the other fields are not read). */
+int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {
   int n_layers;    /* >= 1 */

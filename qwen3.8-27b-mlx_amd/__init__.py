@@ -5,5 +5,5 @@ from .gdn import (  # noqa: F401
     GATES_RAW, GDN_EDEVICE, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_OK, HEAD_DIM, LIB_PATH,
     STATES_BHT, STATES_TBH, CommitArgs, DeltaCache, GdnError, LayerArgs, Result, available,
     call_commit, call_prefill, call_run, commit, last_error, layer, layer_args, lib,
-    prefill_chunked, run,
+    prefill_chunked, prefill_workspace_size, run,
 )

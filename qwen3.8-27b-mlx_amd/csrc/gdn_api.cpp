@@ -16,7 +16,8 @@
 
 namespace gdn {
 int recurrent_tile_rows();
-hipError_t launch_chunked_prefill(const gdn_layer_args& a, hipStream_t stream);
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv);
+hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream);
 }  // namespace gdn
 
 namespace {
@@ -258,15 +259,35 @@ int gdn_run(const gdn_layer_args* a) {
   return ok();
 }
 
+int gdn_prefill_workspace_size(const gdn_layer_args* a, size_t* bytes) {
+  if (!a || !bytes) return fail(GDN_EINVAL, "gdn_prefill_workspace_size: NULL argument");
+  if (a->batch < 0 || a->seq_len < 0 || a->num_k_heads < 1 || a->num_v_heads < 1)
+    return fail(GDN_EINVAL, "gdn_prefill_workspace_size: bad shape");
+  *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
+  return ok();
+}
+
 int gdn_prefill_chunked(const gdn_layer_args* a) {
   int rc = validate_layer(a, "gdn_prefill_chunked", false);
   if (rc != GDN_OK) return rc;
   if (a->batch == 0) return ok();
+  if (a->frontend == GDN_FRONTEND_QKV && a->qkv_dtype != GDN_DTYPE_BF16)
+    return fail(GDN_EINVAL, "gdn_prefill_chunked: the qkv front end takes bf16 q, k, v");
+  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
+  if (a->seq_len > 0) {
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace of %zu bytes required (got %zu)", need,
+                  a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256))
+      return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace must be 256-byte aligned");
+    const int64_t L = a->n_layers;
+    if (L != 1) return fail(GDN_EINVAL, "gdn_prefill_chunked: one layer per call (n_layers = 1)");
+  }
   rc = check_device();
   if (rc != GDN_OK) return rc;
   hipStream_t stream = static_cast<hipStream_t>(a->stream);
   if (a->seq_len == 0) return run_empty(a, stream);
-  hipError_t e = gdn::launch_chunked_prefill(*a, stream);
+  hipError_t e = gdn::launch_chunked_prefill(*a, a->workspace, stream);
   if (e != hipSuccess) return hip_fail(e, "gdn_prefill_chunked launch");
   return ok();
 }

@@ -31,8 +31,8 @@ STATES_BHT, STATES_TBH = 0, 1
 HEAD_DIM = 128
 CONV_TAPS = 4
 
-EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_commit", "gdn_available", "gdn_abi_version",
-           "gdn_last_error")
+EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
+           "gdn_available", "gdn_abi_version", "gdn_last_error")
 
 
 class GdnError(RuntimeError):
@@ -58,6 +58,7 @@ class LayerArgs(ctypes.Structure):
         ("alpha", _vp), ("beta", _vp),
         ("state_in", _vp), ("state_out", _vp), ("states", _vp), ("states_layout", _int),
         ("o", _vp), ("o_dtype", _int),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("stream", _vp),
     ]
 
@@ -88,6 +89,8 @@ def lib() -> ctypes.CDLL:
         L.gdn_run.restype = _int
         L.gdn_prefill_chunked.argtypes = [ctypes.POINTER(LayerArgs)]
         L.gdn_prefill_chunked.restype = _int
+        L.gdn_prefill_workspace_size.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(ctypes.c_size_t)]
+        L.gdn_prefill_workspace_size.restype = _int
         L.gdn_commit.argtypes = [ctypes.POINTER(CommitArgs)]
         L.gdn_commit.restype = _int
         L.gdn_available.argtypes = []
@@ -124,6 +127,13 @@ def call_prefill(args: LayerArgs) -> None:
 
 def call_commit(args: CommitArgs) -> None:
     _check(lib().gdn_commit(ctypes.byref(args)))
+
+
+def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48) -> int:
+    args = LayerArgs(n_layers=1, batch=B, seq_len=T, num_k_heads=Hk, num_v_heads=Hv)
+    out = ctypes.c_size_t(0)
+    _check(lib().gdn_prefill_workspace_size(ctypes.byref(args), ctypes.byref(out)))
+    return out.value
 
 
 # --------------------------------------------------------------------------
@@ -195,7 +205,8 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
                q=None, k=None, v=None, x=None, conv_weight=None, conv_state_in=None,
                conv_state_out=None, a=None, b=None, A_log=None, dt_bias=None, alpha=None,
                beta=None, state_in=None, state_out=None, states=None,
-               states_layout: int = STATES_BHT, o=None, stream=None) -> LayerArgs:
+               states_layout: int = STATES_BHT, o=None, workspace=None,
+               stream=None) -> LayerArgs:
     """Fill gdn_layer_args from torch tensors (front end and gate mode inferred)."""
     conv = x is not None
     raw = a is not None
@@ -211,6 +222,8 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
         state_in=_ptr(state_in), state_out=_ptr(state_out), states=_ptr(states),
         states_layout=states_layout,
         o=_ptr(o), o_dtype=_dt(o) if o is not None else DTYPE_BF16,
+        workspace=_ptr(workspace),
+        workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
         stream=_stream(stream))
 
 
@@ -246,22 +259,26 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     return dict(o=o, state=state_out, states=states, conv_state=conv_out)
 
 
-def prefill_chunked(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
-                    conv_weight=None, conv_state=None, o_dtype=None, Hk: int = 16, stream=None):
-    """chunked_delta with the conv front end and gates inside. Returns dict(o, state, conv_state)."""
+def prefill_chunked(*, x=None, q=None, k=None, v=None, a=None, b=None, A_log=None,
+                    dt_bias=None, alpha=None, beta=None, state=None, conv_weight=None,
+                    conv_state=None, o_dtype=None, Hk: int = 16, Hv: int = 48, workspace=None,
+                    stream=None):
+    """chunked_delta (python/qwen35.py:365-431) with the conv front end and gates inside.
+    Returns dict(o, state, conv_state). The workspace is allocated here unless given."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
-    Hv = A_log.shape[-1]
     dev = src.device
     o = torch.empty((B, T, Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16, device=dev)
     state_out = torch.empty((B, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
     conv_out = (torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
                 if x is not None else None)
+    if workspace is None and T > 0:
+        workspace = torch.empty(prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device=dev)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
-                      A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out, o=o,
-                      stream=stream)
+                      A_log=A_log, dt_bias=dt_bias, alpha=alpha, beta=beta, state_in=state,
+                      state_out=state_out, o=o, workspace=workspace, stream=stream)
     call_prefill(args)
     return dict(o=o, state=state_out, conv_state=conv_out)
 

@@ -16,13 +16,13 @@ HEADER = os.path.join(ROOT, "include", "gdn.h")
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(gdn_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(gdn_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(
-        ["gdn_run", "gdn_prefill_chunked", "gdn_commit", "gdn_available", "gdn_abi_version",
-         "gdn_last_error"])
+        ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
+         "gdn_available", "gdn_abi_version", "gdn_last_error"])
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -114,6 +114,20 @@ def test_run_rejects_bad_arguments(gdn, kw, msg):
     rc = L.gdn_run(ctypes.byref(_args(gdn, **kw)))
     assert rc == gdn.GDN_EINVAL
     assert msg in gdn.last_error(), gdn.last_error()
+
+
+def test_prefill_workspace_size_and_checks(gdn):
+    # 3 q/k planes + 2 (T', M) planes + gate scalars, 256-byte aligned pieces
+    n = gdn.prefill_workspace_size(1, 4096)
+    assert n == 3 * 16 * 64 * 64 * 128 * 2 + 2 * 48 * 64 * 2 * 64 * 64 * 2 + 48 * 64 * 132 * 4
+    L = gdn.lib()
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100)))
+    assert rc == gdn.GDN_EINVAL and "workspace" in gdn.last_error()
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, qkv_dtype=gdn.DTYPE_F32)))
+    assert rc == gdn.GDN_EINVAL and "bf16" in gdn.last_error()
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, workspace=0x10000010,
+                                                  workspace_bytes=1 << 40)))
+    assert rc == gdn.GDN_EINVAL and "256-byte" in gdn.last_error()
 
 
 def test_null_args_and_prefill_states(gdn):
