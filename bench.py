@@ -250,11 +250,13 @@ def cpu_baseline(target_seconds: float = 12.0):
 
 
 def load_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 counter runs (profiles/)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
-        return json.load(fh).get(name)
+        entry = json.load(fh).get(name)
+    return None if entry is None else entry["bytes"]
 
 
 def main() -> int:

@@ -1,0 +1,200 @@
+// gdn.hpp -- header-only C++ host layer over the C ABI of libgdn.so (gdn.h).
+//
+// Mirrors the reference's per-layer C++ interface so a DeltaNet layer can call it where
+// it called the Metal kernel (paths relative to the reference tree):
+//   gdn::run            delta::run(q, k, v, alpha, beta, S, collect)   cpp/src/delta.hpp:66-68
+//   gdn::Layer::step    the recurrent core of GatedDeltaNet::operator(),
+//                       front end + gates + delta::run + cache advance  cpp/src/model.cpp:585-638
+//   gdn::DeltaCache     DeltaCache with record / commit(n)             cpp/src/model.hpp:211-227,
+//                                                                       cpp/src/model.cpp:439-457
+// Errors are C++ exceptions on this side of the ABI (the reference's fail() /
+// std::runtime_error convention); the ABI itself never throws.
+//
+// Device memory: buffers owned here are allocated once, when a DeltaCache is created,
+// never on a step. Every call is ordered on the given stream and does not synchronise.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <stdexcept>
+#include <string>
+#include <utility>
+
+#include "gdn.h"
+
+namespace gdn {
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& msg) : std::runtime_error(msg), code(c) {}
+};
+
+inline void check(int rc) {
+  if (rc != GDN_OK) throw Error(rc, gdn_last_error());
+}
+
+inline void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(GDN_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline bool available() { return gdn_available() != 0; }
+
+// delta::run (delta.hpp:66-68) on device buffers: q, k (B,L,H,128), v (B,L,H,128), alpha,
+// beta (B,L,H), all fp32, head-expanded as the reference passes them; S (B,H,128,128) or
+// nullptr for zeros. Writes o (B,L,H,128) fp32, s_out and, when states != nullptr, the
+// per-step states (B,H,L,128,128) -- the reference's S_all (delta.cpp:155-171).
+inline void run(int B, int L, int H, const float* q, const float* k, const float* v,
+                const float* alpha, const float* beta, const float* S, float* o, float* s_out,
+                float* states = nullptr, hipStream_t stream = nullptr) {
+  gdn_layer_args a{};
+  a.n_layers = 1;
+  a.batch = B;
+  a.seq_len = L;
+  a.num_k_heads = H;
+  a.num_v_heads = H;
+  a.frontend = GDN_FRONTEND_QKV;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.qkv_dtype = GDN_DTYPE_F32;
+  a.gate_mode = GDN_GATES_PRECOMPUTED;
+  a.alpha = alpha;
+  a.beta = beta;
+  a.state_in = S;
+  a.state_out = s_out;
+  a.states = states;
+  a.states_layout = GDN_STATES_BHT;
+  a.o = o;
+  a.o_dtype = GDN_DTYPE_F32;
+  a.stream = stream;
+  check(gdn_run(&a));
+}
+
+// One Gated-DeltaNet layer's fixed parameters (device pointers, loaded elsewhere):
+// conv1d.weight transposed to (4, C) bf16, A_log and dt_bias (Hv) fp32.
+struct LayerParams {
+  const void* conv_weight = nullptr;
+  const float* A_log = nullptr;
+  const float* dt_bias = nullptr;
+  int num_k_heads = 16;
+  int num_v_heads = 48;
+  int conv_dim() const { return 2 * num_k_heads * GDN_HEAD_DIM + num_v_heads * GDN_HEAD_DIM; }
+};
+
+// DeltaCache (model.hpp:211-227): the layer's fp32 state and the 3 pre-conv rows, with
+// record mode for speculative blocks. The conv rows live in two buffers that swap roles
+// every step (the kernel never updates them in place).
+class DeltaCache {
+ public:
+  DeltaCache(const LayerParams& p, int batch, int max_record_steps)
+      : p_(p), B_(batch), max_T_(max_record_steps) {
+    const size_t D = GDN_HEAD_DIM;
+    state_bytes_ = (size_t)B_ * p_.num_v_heads * D * D * sizeof(float);
+    conv_bytes_ = (size_t)B_ * (GDN_CONV_TAPS - 1) * p_.conv_dim() * 2;
+    check_hip(hipMalloc(&state_, state_bytes_), "hipMalloc state");
+    check_hip(hipMalloc(&conv_, conv_bytes_), "hipMalloc conv");
+    check_hip(hipMalloc(&conv_spare_, conv_bytes_), "hipMalloc conv");
+    if (max_T_ > 0) check_hip(hipMalloc(&states_, state_bytes_ * max_T_), "hipMalloc states");
+    check_hip(hipMemset(state_, 0, state_bytes_), "hipMemset");
+    check_hip(hipMemset(conv_, 0, conv_bytes_), "hipMemset");
+  }
+  DeltaCache(const DeltaCache&) = delete;
+  DeltaCache& operator=(const DeltaCache&) = delete;
+  ~DeltaCache() {
+    (void)hipFree(state_);
+    (void)hipFree(conv_);
+    (void)hipFree(conv_spare_);
+    if (states_) (void)hipFree(states_);
+  }
+
+  int offset = 0;
+  bool record = false;
+
+  float* state() const { return state_; }
+  void* conv() const { return conv_; }
+  size_t state_bytes() const { return state_bytes_; }
+  size_t conv_bytes() const { return conv_bytes_; }
+
+  // GatedDeltaNet::operator() from the in_proj outputs to o (model.cpp:585-638):
+  // x (B,T,C) bf16 = in_proj_qkv(x), a, b (B,T,Hv) bf16 = in_proj_a/b(x); o (B,T,Hv,128)
+  // bf16. In record mode the state is not advanced and every per-step state is kept for
+  // commit(); x must then stay valid until commit().
+  void step(const void* x, const void* a, const void* b, int T, void* o, hipStream_t stream) {
+    gdn_layer_args g{};
+    g.n_layers = 1;
+    g.batch = B_;
+    g.seq_len = T;
+    g.num_k_heads = p_.num_k_heads;
+    g.num_v_heads = p_.num_v_heads;
+    g.frontend = GDN_FRONTEND_CONV;
+    g.x = x;
+    g.conv_weight = p_.conv_weight;
+    g.conv_state_in = conv_;
+    g.gate_mode = GDN_GATES_RAW;
+    g.a = a;
+    g.b = b;
+    g.A_log = p_.A_log;
+    g.dt_bias = p_.dt_bias;
+    g.state_in = state_;
+    g.states_layout = GDN_STATES_TBH;
+    g.o = o;
+    g.o_dtype = GDN_DTYPE_BF16;
+    g.stream = stream;
+    if (record) {
+      if (T > max_T_) throw Error(GDN_EINVAL, "DeltaCache: record block longer than max_record_steps");
+      g.states = states_;
+      check(gdn_run(&g));
+      base_offset_ = offset;
+      pending_x_ = x;
+      pending_T_ = T;
+    } else {
+      g.conv_state_out = conv_spare_;
+      g.state_out = state_;
+      check(gdn_run(&g));
+      std::swap(conv_, conv_spare_);
+      offset += T;
+    }
+  }
+
+  // Accept the first n tokens of the recorded block (model.cpp:439-457).
+  void commit(int n, hipStream_t stream) {
+    if (pending_T_ < 0) return;
+    if (n < 0 || n > pending_T_) throw Error(GDN_EINVAL, "DeltaCache::commit out of range");
+    gdn_commit_args c{};
+    c.n_layers = 1;
+    c.batch = B_;
+    c.seq_len = pending_T_;
+    c.num_v_heads = p_.num_v_heads;
+    c.conv_dim = p_.conv_dim();
+    c.n = n;
+    c.states = states_;
+    c.states_layout = GDN_STATES_TBH;
+    c.state_prev = state_;
+    c.state_dst = state_;
+    c.conv_state_in = conv_;
+    c.x = pending_x_;
+    c.conv_state_dst = conv_;
+    c.stream = stream;
+    check(gdn_commit(&c));
+    offset = base_offset_ + n;
+    pending_T_ = -1;
+    pending_x_ = nullptr;
+    record = false;
+  }
+
+ private:
+  LayerParams p_;
+  int B_;
+  int max_T_;
+  size_t state_bytes_ = 0, conv_bytes_ = 0;
+  float* state_ = nullptr;
+  void* conv_ = nullptr;
+  void* conv_spare_ = nullptr;
+  float* states_ = nullptr;
+  int base_offset_ = 0;
+  const void* pending_x_ = nullptr;
+  int pending_T_ = -1;
+};
+
+}  // namespace gdn

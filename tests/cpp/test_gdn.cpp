@@ -1,0 +1,203 @@
+// C++ host-side test of libgdn.so through include/gdn.hpp, in the style of the
+// reference's self-test (cpp/src/tests.cpp:36-56 rel_err/check, 196-243 test_delta):
+// gdn::run vs the oracle's run_reference restatement on the reference's shapes and input
+// distributions, with and without collect, bound 2e-5; then DeltaCache record/commit
+// against plain decoding. The oracle (oracle/gdn_oracle.h) is the checker only.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gdn.hpp"
+#include "gdn_oracle.h"
+
+namespace {
+
+int g_pass = 0, g_fail = 0;
+
+void check(bool ok, const std::string& what) {
+  printf("  [%s] %s\n", ok ? "ok" : "FAIL", what.c_str());
+  (ok ? g_pass : g_fail)++;
+}
+
+// max|a-b| / max|b| (tests.cpp:38-45)
+float rel_err(const std::vector<float>& a, const std::vector<float>& b) {
+  float num = 0.f, den = 0.f;
+  for (size_t i = 0; i < a.size(); ++i) {
+    num = std::max(num, std::fabs(a[i] - b[i]));
+    den = std::max(den, std::fabs(b[i]));
+  }
+  return num / (den > 0 ? den : 1.0f);
+}
+
+template <class T>
+T* to_dev(const std::vector<T>& h) {
+  T* d = nullptr;
+  gdn::check_hip(hipMalloc(&d, h.size() * sizeof(T)), "hipMalloc");
+  gdn::check_hip(hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice), "copy");
+  return d;
+}
+
+template <class T>
+std::vector<T> to_host(const T* d, size_t n) {
+  std::vector<T> h(n);
+  gdn::check_hip(hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost), "copy");
+  return h;
+}
+
+std::vector<float> normal(uint64_t seed, size_t n, float std = 1.0f) {
+  std::vector<float> v(n);
+  gdno_fill_normal(seed, 0.0f, std, v.data(), (int64_t)n);
+  return v;
+}
+
+void l2norm_rows(std::vector<float>& x, float scale) {
+  for (size_t r = 0; r < x.size() / 128; ++r) {
+    double s = 0;
+    for (int d = 0; d < 128; ++d) s += (double)x[r * 128 + d] * x[r * 128 + d];
+    const double inv = scale / std::sqrt(s);
+    for (int d = 0; d < 128; ++d) x[r * 128 + d] = (float)(x[r * 128 + d] * inv);
+  }
+}
+
+void test_delta() {
+  printf("\ndelta kernel (gfx950 available: %s)\n", gdn::available() ? "yes" : "no");
+  struct Case {
+    int B, L, H;
+  };
+  for (const Case& c : {Case{1, 1, 48}, Case{1, 4, 48}, Case{1, 9, 48}, Case{2, 3, 16},
+                        Case{1, 64, 48}, Case{1, 384, 8}}) {
+    const size_t nq = (size_t)c.B * c.L * c.H * 128, ng = (size_t)c.B * c.L * c.H,
+                 ns = (size_t)c.B * c.H * 128 * 128;
+    const uint64_t s = 9000 + 7 * c.L + c.H;
+    auto q = normal(s, nq), k = normal(s + 1, nq), v = normal(s + 2, nq), S0 = normal(s + 5, ns, 0.1f);
+    l2norm_rows(q, 1.0f / std::sqrt(128.0f));
+    l2norm_rows(k, 1.0f);
+    std::vector<float> al(ng), bt(ng);
+    gdno_fill_uniform(s + 3, 0.85f, 1.0f, al.data(), (int64_t)ng);
+    gdno_fill_uniform(s + 4, 0.0f, 1.0f, bt.data(), (int64_t)ng);
+
+    std::vector<float> ro(nq), rS(ns), rst(ns * c.L);
+    gdno_recurrent_f32(c.B, c.L, c.H, c.H, q.data(), k.data(), v.data(), al.data(), bt.data(),
+                       S0.data(), rS.data(), ro.data(), rst.data(), 0, 0);
+
+    float *dq = to_dev(q), *dk = to_dev(k), *dv = to_dev(v), *da = to_dev(al), *db = to_dev(bt),
+          *dS = to_dev(S0), *dO, *dSo, *dSt;
+    gdn::check_hip(hipMalloc(&dO, nq * 4), "hipMalloc");
+    gdn::check_hip(hipMalloc(&dSo, ns * 4), "hipMalloc");
+    gdn::check_hip(hipMalloc(&dSt, ns * c.L * 4), "hipMalloc");
+    gdn::run(c.B, c.L, c.H, dq, dk, dv, da, db, dS, dO, dSo);
+    gdn::check_hip(hipDeviceSynchronize(), "sync");
+    const float eo = rel_err(to_host(dO, nq), ro), es = rel_err(to_host(dSo, ns), rS);
+    char buf[160];
+    snprintf(buf, sizeof(buf), "B=%d L=%3d H=%2d  out %.2e  state %.2e", c.B, c.L, c.H, eo, es);
+    check(std::max(eo, es) < 2e-5f, buf);
+
+    gdn::run(c.B, c.L, c.H, dq, dk, dv, da, db, dS, dO, nullptr, dSt);
+    gdn::check_hip(hipDeviceSynchronize(), "sync");
+    const float ec = rel_err(to_host(dSt, ns * c.L), rst);
+    snprintf(buf, sizeof(buf), "  collect: %d states, max rel err %.2e", c.L, ec);
+    check(ec < 2e-5f, buf);
+    for (float* p : {dq, dk, dv, da, db, dS, dO, dSo, dSt}) (void)hipFree(p);
+  }
+}
+
+// DeltaCache record/commit against plain decoding of the accepted prefix
+// (session.cpp:476-515 contract), and step() against the oracle's layer sequence.
+void test_cache() {
+  printf("\nDeltaCache (record / commit)\n");
+  const int B = 2, Hk = 16, Hv = 48, C = 2 * Hk * 128 + Hv * 128, T = 5;
+  std::vector<uint16_t> w(4 * C), x((size_t)B * (T + 1) * C), a((size_t)B * (T + 1) * Hv),
+      b((size_t)B * (T + 1) * Hv);
+  gdno_round_bf16(normal(11, w.size(), 0.1f).data(), w.data(), (int64_t)w.size());
+  gdno_round_bf16(normal(12, x.size()).data(), x.data(), (int64_t)x.size());
+  gdno_round_bf16(normal(13, a.size()).data(), a.data(), (int64_t)a.size());
+  gdno_round_bf16(normal(14, b.size()).data(), b.data(), (int64_t)b.size());
+  std::vector<float> A_log(Hv), dt = normal(16, Hv, 0.1f);
+  gdno_fill_uniform(15, -1.0f, 1.0f, A_log.data(), Hv);
+  uint16_t *dw = to_dev(w), *dx = to_dev(x), *da = to_dev(a), *db = to_dev(b);
+  float *dA = to_dev(A_log), *ddt = to_dev(dt);
+  gdn::LayerParams p;
+  p.conv_weight = dw;
+  p.A_log = dA;
+  p.dt_bias = ddt;
+  uint16_t* o;
+  gdn::check_hip(hipMalloc(&o, (size_t)B * T * Hv * 128 * 2), "hipMalloc");
+
+  // per-token slices of x, a, b: (B, 1, .) rows of a (B, T+1, .) buffer are not
+  // contiguous for B > 1, so copy each token to its own buffer
+  auto token = [&](const std::vector<uint16_t>& src, int t, int width) {
+    std::vector<uint16_t> h((size_t)B * width);
+    for (int bb = 0; bb < B; ++bb)
+      memcpy(&h[(size_t)bb * width], &src[((size_t)bb * (T + 1) + t) * width], width * 2);
+    return to_dev(h);
+  };
+  auto block = [&](const std::vector<uint16_t>& src, int t0, int n, int width) {
+    std::vector<uint16_t> h((size_t)B * n * width);
+    for (int bb = 0; bb < B; ++bb)
+      memcpy(&h[(size_t)bb * n * width], &src[((size_t)bb * (T + 1) + t0) * width], (size_t)n * width * 2);
+    return to_dev(h);
+  };
+  for (int j : {0, 2, 5}) {
+    gdn::DeltaCache spec(p, B, T), plain(p, B, 0);
+    uint16_t* xb = block(x, 0, T, C);
+    uint16_t* ab = block(a, 0, T, Hv);
+    uint16_t* bb_ = block(b, 0, T, Hv);
+    spec.record = true;
+    spec.step(xb, ab, bb_, T, o, nullptr);
+    spec.commit(j, nullptr);
+    for (int t = 0; t < j; ++t) {
+      uint16_t *xt = token(x, t, C), *at = token(a, t, Hv), *bt = token(b, t, Hv);
+      plain.step(xt, at, bt, 1, o, nullptr);
+      gdn::check_hip(hipDeviceSynchronize(), "sync");
+      (void)hipFree(xt); (void)hipFree(at); (void)hipFree(bt);
+    }
+    uint16_t *xt = token(x, T, C), *at = token(a, T, Hv), *bt = token(b, T, Hv);
+    spec.step(xt, at, bt, 1, o, nullptr);
+    plain.step(xt, at, bt, 1, o, nullptr);
+    gdn::check_hip(hipDeviceSynchronize(), "sync");
+    const auto s1 = to_host(spec.state(), spec.state_bytes() / 4);
+    const auto s2 = to_host(plain.state(), plain.state_bytes() / 4);
+    const auto c1 = to_host((const uint16_t*)spec.conv(), spec.conv_bytes() / 2);
+    const auto c2 = to_host((const uint16_t*)plain.conv(), plain.conv_bytes() / 2);
+    char buf[160];
+    snprintf(buf, sizeof(buf), "commit(%d) then one step == plain decoding of %d tokens (offset %d)", j, j,
+             spec.offset);
+    check(s1 == s2 && c1 == c2 && spec.offset == plain.offset && spec.offset == j + 1, buf);
+    for (uint16_t* ptr : {xb, ab, bb_, xt, at, bt}) (void)hipFree(ptr);
+  }
+  bool threw = false;
+  try {
+    gdn::DeltaCache c(p, B, T);
+    uint16_t* xb = block(x, 0, T, C);
+    uint16_t* ab = block(a, 0, T, Hv);
+    uint16_t* bb_ = block(b, 0, T, Hv);
+    c.record = true;
+    c.step(xb, ab, bb_, T, o, nullptr);
+    c.commit(T + 1, nullptr);
+  } catch (const gdn::Error&) {
+    threw = true;
+  }
+  check(threw, "commit out of range throws (model.cpp:443)");
+}
+
+}  // namespace
+
+int main() {
+  if (!gdn::available()) {
+    printf("[skip] no gfx950 device\n");
+    return 0;
+  }
+  try {
+    test_delta();
+    test_cache();
+  } catch (const std::exception& e) {
+    printf("  [FAIL] exception: %s\n", e.what());
+    ++g_fail;
+  }
+  printf("\n%d passed, %d failed\n", g_pass, g_fail);
+  return g_fail == 0 ? 0 : 1;
+}
