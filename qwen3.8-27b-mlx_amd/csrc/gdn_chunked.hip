@@ -111,6 +111,19 @@ __device__ __forceinline__ uint16_t xp_row(const PrefillParams& p, int b, int po
   return p.x[((size_t)b * p.T + pos) * p.C + c];
 }
 
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// Eight consecutive channels of padded conv input row `pos` (16-byte aligned: C and the
+// channel offset are multiples of 8, x and the conv state 16-byte aligned).
+__device__ __forceinline__ u16x8 xp_vec8(const PrefillParams& p, int b, int pos, int c) {
+  if (pos >= p.T) return u16x8{};
+  if (pos < 0) {
+    if (!p.conv_in) return u16x8{};
+    return *reinterpret_cast<const u16x8*>(p.conv_in + ((size_t)b * kConvRows + (kConvRows + pos)) * p.C + c);
+  }
+  return *reinterpret_cast<const u16x8*>(p.x + ((size_t)b * p.T + pos) * p.C + c);
+}
+
 // ============================================================================ intra
 
 struct IntraSmem {
@@ -172,11 +185,27 @@ __global__ __launch_bounds__(kThreads) void prefill_intra_kernel(PrefillParams p
 
   // ---- q, k of the chunk into LDS (bf16) ----
   if (FE == 1) {
-    // stage rows t0-3 .. t0+63 of the q and k channels of k-head g
-    for (int e = tid; e < (kC + kConvRows) * 2 * kD; e += kThreads) {
-      const int r = e / (2 * kD), cc = e % (2 * kD);
-      const int ch = (cc < kD ? 0 : p.Hk * kD - kD) + g * kD + cc;
-      s.u.xs[r][cc] = xp_row(p, b, t0 - kConvRows + r, ch);
+    // stage rows t0-3 .. t0+63 of the q and k channels of k-head g: 16-byte loads, all
+    // issued before any is used
+    {
+      constexpr int kVec = (kC + kConvRows) * 2 * kD / 8;  // 16-byte pieces
+      constexpr int kIter = (kVec + kThreads - 1) / kThreads;
+      u16x8 vals[kIter];
+#pragma unroll
+      for (int it = 0; it < kIter; ++it) {
+        const int e = tid + it * kThreads;
+        const int r = e / (2 * kD / 8), cc = (e % (2 * kD / 8)) * 8;
+        const int ch = (cc < kD ? 0 : p.Hk * kD - kD) + g * kD + cc;
+        vals[it] = e < kVec ? xp_vec8(p, b, t0 - kConvRows + r, ch) : u16x8{};
+      }
+#pragma unroll
+      for (int it = 0; it < kIter; ++it) {
+        const int e = tid + it * kThreads;
+        if (e < kVec) {
+          const int r = e / (2 * kD / 8), cc = (e % (2 * kD / 8)) * 8;
+          *reinterpret_cast<u16x8*>(&s.u.xs[r][cc]) = vals[it];
+        }
+      }
     }
     __syncthreads();
     // wave 0/1: q of positions 0..31 / 32..63; wave 2/3: k. Lane: channels l, l+64.
@@ -382,8 +411,8 @@ struct ScanSmem {
   float v[kC][kDt + 1];
   float eg[kC];
   float egr[kC];
+  uint16_t xs[kC + kConvRows][kDt];  // 64-byte rows, 16-byte aligned
   float gam;
-  uint16_t xs[kC + kConvRows][kDt];
 };
 
 template <int FE>
@@ -426,34 +455,76 @@ __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p)
     const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
     const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
 
-    // ---- stage the chunk ----
-    for (int e = tid; e < kC * kD / 8; e += kThreads) {
-      const int pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      *reinterpret_cast<bf8*>(&s.q[pos][d8]) = *reinterpret_cast<const bf8*>(p.ws_q + gc * kC * kD + pos * kD + d8);
-      *reinterpret_cast<bf8*>(&s.k[pos][d8]) = *reinterpret_cast<const bf8*>(p.ws_k + gc * kC * kD + pos * kD + d8);
-      const int dk = e / (kC / 8), p8 = (e % (kC / 8)) * 8;
-      *reinterpret_cast<bf8*>(&s.kt[dk][p8]) = *reinterpret_cast<const bf8*>(p.ws_kt + gc * kC * kD + dk * kC + p8);
-    }
-    for (int e = tid; e < kC * kC / 8; e += kThreads) {
-      const int i = e / (kC / 8), j8 = (e % (kC / 8)) * 8;
+    // ---- stage the chunk: every 16-byte load issued before any is stored ----
+    {
+      constexpr int kQK = kC * kD / 8 / kThreads;  // 4 pieces per thread per matrix
+      constexpr int kTM = kC * kC / 8 / kThreads;  // 2
+      bf8 vq[kQK], vk[kQK], vkt[kQK], vth[kTM], vtl[kTM], vmh[kTM], vml[kTM];
+      const __bf16* wq = p.ws_q + gc * kC * kD;
+      const __bf16* wk = p.ws_k + gc * kC * kD;
+      const __bf16* wkt = p.ws_kt + gc * kC * kD;
       const __bf16* wt = p.ws_T + hc * 2 * kC * kC;
       const __bf16* wm = p.ws_M + hc * 2 * kC * kC;
-      *reinterpret_cast<bf8*>(&s.th[i][j8]) = *reinterpret_cast<const bf8*>(wt + i * kC + j8);
-      *reinterpret_cast<bf8*>(&s.tl[i][j8]) = *reinterpret_cast<const bf8*>(wt + kC * kC + i * kC + j8);
-      *reinterpret_cast<bf8*>(&s.mh[i][j8]) = *reinterpret_cast<const bf8*>(wm + i * kC + j8);
-      *reinterpret_cast<bf8*>(&s.ml[i][j8]) = *reinterpret_cast<const bf8*>(wm + kC * kC + i * kC + j8);
-    }
-    if (tid < kC) {
+#pragma unroll
+      for (int it = 0; it < kQK; ++it) {
+        const int e = tid + it * kThreads;
+        vq[it] = *reinterpret_cast<const bf8*>(wq + e * 8);
+        vk[it] = *reinterpret_cast<const bf8*>(wk + e * 8);
+        vkt[it] = *reinterpret_cast<const bf8*>(wkt + e * 8);
+      }
+#pragma unroll
+      for (int it = 0; it < kTM; ++it) {
+        const int e = tid + it * kThreads;
+        vth[it] = *reinterpret_cast<const bf8*>(wt + e * 8);
+        vtl[it] = *reinterpret_cast<const bf8*>(wt + kC * kC + e * 8);
+        vmh[it] = *reinterpret_cast<const bf8*>(wm + e * 8);
+        vml[it] = *reinterpret_cast<const bf8*>(wm + kC * kC + e * 8);
+      }
+      float gv = 0.f, grv = 0.f, gam = 0.f;
       const float* wg = p.ws_g + hc * kGStride;
-      s.eg[tid] = wg[tid];
-      s.egr[tid] = wg[64 + tid];
-      if (tid == 0) s.gam = wg[128];
+      if (tid < kC) {
+        gv = wg[tid];
+        grv = wg[64 + tid];
+        gam = wg[128];
+      }
+      u16x8 xv[2] = {};
+      constexpr int kXV = (kC + kConvRows) * kDt / 8;  // 268 pieces
+      if (FE == 1) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          const int e = tid + it * kThreads;
+          if (e < kXV) xv[it] = xp_vec8(p, b, t0 - kConvRows + e / (kDt / 8), vch0 + (e % (kDt / 8)) * 8);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < kQK; ++it) {
+        const int e = tid + it * kThreads;
+        *reinterpret_cast<bf8*>(&s.q[e / (kD / 8)][(e % (kD / 8)) * 8]) = vq[it];
+        *reinterpret_cast<bf8*>(&s.k[e / (kD / 8)][(e % (kD / 8)) * 8]) = vk[it];
+        *reinterpret_cast<bf8*>(&s.kt[e / (kC / 8)][(e % (kC / 8)) * 8]) = vkt[it];
+      }
+#pragma unroll
+      for (int it = 0; it < kTM; ++it) {
+        const int e = tid + it * kThreads, i = e / (kC / 8), j8 = (e % (kC / 8)) * 8;
+        *reinterpret_cast<bf8*>(&s.th[i][j8]) = vth[it];
+        *reinterpret_cast<bf8*>(&s.tl[i][j8]) = vtl[it];
+        *reinterpret_cast<bf8*>(&s.mh[i][j8]) = vmh[it];
+        *reinterpret_cast<bf8*>(&s.ml[i][j8]) = vml[it];
+      }
+      if (tid < kC) {
+        s.eg[tid] = gv;
+        s.egr[tid] = grv;
+        if (tid == 0) s.gam = gam;
+      }
+      if (FE == 1) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          const int e = tid + it * kThreads;
+          if (e < kXV) *reinterpret_cast<u16x8*>(&s.xs[e / (kDt / 8)][(e % (kDt / 8)) * 8]) = xv[it];
+        }
+      }
     }
     if (FE == 1) {
-      for (int e = tid; e < (kC + kConvRows) * kDt; e += kThreads) {
-        const int r = e / kDt, dt = e % kDt;
-        s.xs[r][dt] = xp_row(p, b, t0 - kConvRows + r, vch0 + dt);
-      }
     } else {
       for (int e = tid; e < kC * kDt; e += kThreads) {
         const int pos = e / kDt, dt = e % kDt;

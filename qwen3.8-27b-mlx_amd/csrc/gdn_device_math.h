@@ -22,13 +22,11 @@ namespace gdn {
 __device__ __forceinline__ float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __device__ __forceinline__ uint32_t f_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
-__device__ __forceinline__ uint16_t f2bf(float x) {
-  uint32_t u = f_bits(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16 bits, round to nearest even, NaN quieted: one v_cvt_pk_bf16_f32. On
+// gfx950 this instruction equals the integer rounding (u + 0x7fff + ((u >> 16) & 1)) >> 16,
+// with NaN -> (u >> 16) | 0x40, for every one of the 2^32 fp32 inputs (checked
+// exhaustively on the device).
+__device__ __forceinline__ uint16_t f2bf(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 __device__ __forceinline__ float bf2f(uint16_t h) { return bits_f((uint32_t)h << 16); }
 // Round an fp32 value to the nearest bf16 value, kept in fp32.
 __device__ __forceinline__ float rbf(float x) { return bf2f(f2bf(x)); }
