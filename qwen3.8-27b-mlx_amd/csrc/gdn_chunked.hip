@@ -4,26 +4,32 @@
 //   G_i   = sum_{m<=i} log clip(alpha_m, 1e-6, 1)        (within-chunk log decay)
 //   A_ij  = beta_i exp(G_i - G_j) (K K^T)_ij, j < i      T' = (I + A)^-1 diag(beta)
 //   M_ij  = exp(G_i - G_j) (Q K^T)_ij, j <= i
+//   U     = T' V        W = T' diag(e^G) K               (depend on the chunk only)
 // and, with the state S as (Dk x Dv) (the transpose of the stored (Dv, Dk) layout):
-//   V' = T' (V - e^G . K S)                              (= U0 - Kt S of the reference)
+//   V' = U - W S                                         (= U0 - Kt S of the reference)
 //   y  = e^G . (Q S) + M V'                              (= MU0 + Qeff S)
 //   S  = e^{G_63} S + K^T (e^{G_63 - G} . V')
 //
 // Two kernels:
-//   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel: the
-//                  conv front end for q and k (or the given q, k), Q K^T and K K^T on bf16
-//                  MFMA, and for each of the k-head's v-heads the gates, T' (blocked
-//                  forward substitution in fp32) and M. Results go to the workspace.
+//   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
+//                  per CU: the conv front end for q, k, v (or the given q, k, v), K K^T and
+//                  K Q^T on bf16 MFMA, and for the k-head's v-heads the gates, A and M,
+//                  T = (I + A)^-1 (one wave per v-head, fp32), U and W (bf16 MFMA, T'
+//                  split into bf16 hi + lo for U). Results go to the workspace, already in
+//                  the register order of the MFMA operands that read them.
 //   prefill_scan   one workgroup per (batch, v-head, 32-column Dv tile), serial over the
-//                  chunks; the fp32 state tile lives in MFMA accumulators. K S, Q S and
-//                  K^T V' use bf16 operands; T' R and M V' split both operands into bf16
-//                  hi + lo parts (three MFMAs), which keeps those two products -- the ones
-//                  the output is most sensitive to -- at about fp32 accuracy.
+//                  chunks; the fp32 state tile lives in MFMA accumulators. Each chunk's
+//                  operands go from the workspace straight into registers, one chunk
+//                  ahead of their use; LDS holds only the operands all four waves share
+//                  (S^T and V'). W S, Q S and K^T V'' use bf16 operands; M V' splits both
+//                  operands into bf16 hi + lo (three MFMAs).
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
 // are read as 16-byte rows ([row][k] for A, [col][k] for B), padded by 8 bf16 per row to
-// keep the 16 rows of a fragment on distinct banks.
+// keep the 16 rows of a fragment on distinct banks. A matrix stored in "fragment order"
+// is a sequence of 16 x 32 blocks (row block major, then k block), each block being the
+// 64 lanes' 16-byte A fragments in lane order: one 1 KB coalesced load per fragment.
 #include "../../include/gdn.h"
 #include "gdn_device_math.h"
 #include "gdn_internal.h"
@@ -32,16 +38,18 @@ namespace gdn {
 namespace {
 
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kC = 64;           // chunk
-constexpr int kPadB = 8;         // bf16 padding per LDS row
-constexpr int kDt = 32;          // Dv columns per scan workgroup
+constexpr int kC = 64;             // chunk
+constexpr int kPadB = 8;           // bf16 padding per LDS row
+constexpr int kDt = 32;            // Dv columns per scan workgroup
 constexpr int kThreads = 256;
-constexpr int kGStride = 132;    // floats per (v-head, chunk) in the gate workspace
-
-__device__ __forceinline__ __bf16 to_bf(float x) { return __builtin_bit_cast(__bf16, f2bf(x)); }
-__device__ __forceinline__ float from_bf(__bf16 x) { return bf2f(__builtin_bit_cast(uint16_t, x)); }
+constexpr int kGroup = 3;          // v-heads inverted together (one wave each)
+constexpr int kGStride = 132;      // floats per (v-head, chunk) in the gate workspace
+constexpr int kFrag = 512;         // bf16 elements of one 16 x 32 fragment block
+constexpr int kChunkElems = 8192;  // elements of one chunk's 64 x 128 (or 2 x 64 x 64) matrix
 
 __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -50,6 +58,18 @@ __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
 template <int LD>
 __device__ __forceinline__ bf8 frag(const __bf16 (*m)[LD], int row, int k) {
   return *reinterpret_cast<const bf8*>(&m[row][k]);
+}
+
+__device__ __forceinline__ bf4 to_bf4(f4 v) { return __builtin_convertvector(v, bf4); }
+__device__ __forceinline__ f4 from_bf4(bf4 v) { return __builtin_convertvector(v, f4); }
+
+// e^x for x <= 0 from the hardware 2^x (the decay factors inside a chunk).
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// Offset, in a matrix of `kb` 32-column blocks stored in fragment order, of element
+// (row, col); col % 4 == 0 addresses 4 consecutive elements (8 bytes).
+__device__ __forceinline__ int frag_off(int row, int col, int kb) {
+  return ((row >> 4) * kb + (col >> 5)) * kFrag + ((row & 15) + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
 }
 
 struct PrefillParams {
@@ -71,22 +91,16 @@ struct PrefillParams {
   const float* state_in;
   float* state_out;
   void* o;
-  // workspace
-  __bf16* ws_q;   // (B, Hk, nC, 64, 128)
-  __bf16* ws_k;   // (B, Hk, nC, 64, 128)
-  __bf16* ws_kt;  // (B, Hk, nC, 128, 64)
-  __bf16* ws_T;   // (B, Hv, nC, 2, 64, 64)  T' hi, lo
-  __bf16* ws_M;   // (B, Hv, nC, 2, 64, 64)  M hi, lo
+  // workspace, per chunk
+  __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128) in fragment order
+  __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64) in fragment order
+  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128) in fragment order
+  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64) in fragment order, hi and lo blocks interleaved
+  float* ws_u;    // (B, Hv, nC): U   (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]
   float* ws_g;    // (B, Hv, nC, kGStride): e^G [64], e^(G63-G) [64], e^G63
 };
 
-// silu on a bf16 value: x * sigmoid(x), both ops rounded (ops.cpp:20).
-__device__ __forceinline__ float silu_bf(float y) {
-  const float sg = rbf(d_sigmoidf(y));
-  return rbf(y * sg);
-}
-
-// Causal depthwise conv from 4 staged rows (model.cpp:385-395), bf16 after every op.
+// Causal depthwise conv from 4 rows (model.cpp:385-395), bf16 after every op.
 __device__ __forceinline__ float conv4_rows(float x0, float x1, float x2, float x3, const float (&w)[kTaps]) {
   float y = rbf(x0 * w[0]);
   y = rbf(y + rbf(x1 * w[1]));
@@ -95,158 +109,182 @@ __device__ __forceinline__ float conv4_rows(float x0, float x1, float x2, float 
   return y;
 }
 
-__device__ __forceinline__ float wave64_sum(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = x + __shfl_xor(x, m, 64);
-  return x;
+// Padded conv input rows (absolute position `pos`; negative rows come from the conv
+// state, rows past the end are zero). Rows without data read a valid row and are zeroed
+// after the load, and the row base is a uniform select, so the loads carry no branches
+// and a thread's loads are all in flight together.
+__device__ __forceinline__ const uint16_t* xp_base(const PrefillParams& p, int b, int pos) {
+  const uint16_t* xr = p.x + ((size_t)b * p.T + min(max(pos, 0), p.T - 1)) * p.C;
+  const uint16_t* cr = p.conv_in + ((size_t)b * kConvRows + (kConvRows + pos)) * p.C;
+  return (pos < 0 && p.conv_in) ? cr : xr;
+}
+__device__ __forceinline__ bool xp_valid(const PrefillParams& p, int pos) {
+  return pos < p.T && (pos >= 0 || p.conv_in != nullptr);
 }
 
-// Padded conv input row `pos` (absolute position; negative rows come from the conv
-// state) at channel c; 0 past the end of the sequence.
 __device__ __forceinline__ uint16_t xp_row(const PrefillParams& p, int b, int pos, int c) {
-  if (pos >= p.T) return 0;
-  if (pos < 0) {
-    return p.conv_in ? p.conv_in[((size_t)b * kConvRows + (kConvRows + pos)) * p.C + c] : (uint16_t)0;
-  }
-  return p.x[((size_t)b * p.T + pos) * p.C + c];
+  const uint16_t v = xp_base(p, b, pos)[c];
+  return xp_valid(p, pos) ? v : (uint16_t)0;
 }
 
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-
-// Eight consecutive channels of padded conv input row `pos` (16-byte aligned: C and the
-// channel offset are multiples of 8, x and the conv state 16-byte aligned).
-__device__ __forceinline__ u16x8 xp_vec8(const PrefillParams& p, int b, int pos, int c) {
-  if (pos >= p.T) return u16x8{};
-  if (pos < 0) {
-    if (!p.conv_in) return u16x8{};
-    return *reinterpret_cast<const u16x8*>(p.conv_in + ((size_t)b * kConvRows + (kConvRows + pos)) * p.C + c);
-  }
-  return *reinterpret_cast<const u16x8*>(p.x + ((size_t)b * p.T + pos) * p.C + c);
+// Four consecutive channels of the same row (8-byte aligned: C and c are multiples of
+// 4, x and the conv state 16-byte aligned).
+__device__ __forceinline__ u16x4 xp_vec4(const PrefillParams& p, int b, int pos, int c) {
+  const u16x4 v = *reinterpret_cast<const u16x4*>(xp_base(p, b, pos) + c);
+  return xp_valid(p, pos) ? v : u16x4{};
 }
 
 // ============================================================================ intra
 
 struct IntraSmem {
-  __bf16 q[kC][kD + kPadB];
-  __bf16 k[kC][kD + kPadB];
-  float gram[kC][kC + 4];
-  float qk[kC][kC + 4];
+  __bf16 kt[kD][kC + kPadB];  // K^T [dk][pos]
+  float G[kGroup][kC];
+  float beta[kGroup][kC];
   union {
-    uint16_t xs[kC + kConvRows][2 * kD];  // staged conv input rows (front end only)
     struct {
-      float a[kC][kC + 4];
-      float t[kC][kC + 4];
-    } m;
+      __bf16 q[kC][kD + kPadB];
+      __bf16 k[kC][kD + kPadB];
+    } fe;
+    float nat[kGroup][kC][kC + 4];  // -A^T per v-head: [j][i] = -A_ij
+    struct {
+      __bf16 th[kC][kC + kPadB];  // T' hi
+      __bf16 tl[kC][kC + kPadB];  // T' lo
+      __bf16 te[kC][kC + kPadB];  // T' diag(e^G)
+      __bf16 vt[kD][kC + kPadB];  // V^T [dv][pos]
+    } pr;
   } u;
-  float tmp[4][16][17];
-  float G[kC];
-  float beta[kC];
 };
 
-// One off-diagonal 16x16 block of T = (I + A)^-1 (block rows i > j), by one wave:
-// X_ij = -X_ii sum_{m=j}^{i-1} A_im X_mj. Lane l computes rows 4(l/16)..+3, column l%16.
-__device__ __forceinline__ void inverse_offdiag(IntraSmem& s, int bi, int bj, int wave, int lane) {
-  const int col = lane & 15, r0 = (lane >> 4) * 4;
-  float y[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int bm = bj; bm < bi; ++bm) {
-    for (int m = 0; m < 16; ++m) {
-      const float xv = s.u.m.t[16 * bm + m][16 * bj + col];
+// q (waves 0, 1) or k (waves 2, 3) of k-head g into LDS: conv + SiLU + l2norm, bf16
+// after every op (model.cpp:585-602). Lane l: positions 32 (wave & 1) + 8 (l / 16) .. +7,
+// channels {4m .. 4m+3} and {64+4m .. 64+4m+3}, m = l % 16. The l2norm sum keeps the
+// butterfly order of a wave that holds channels (L, L+64) in lane L: lane m adds its
+// four pairs as ((p0 + p1) + (p2 + p3)) (the first two butterfly steps), then the DPP
+// row sum does the remaining four.
+__device__ __forceinline__ void qk_frontend(const PrefillParams& p, IntraSmem& s, int b, int g, int t0, int n,
+                                            int wave, int lane) {
+  const int part = wave >> 1;
+  const int m = lane & 15;
+  const int p0 = (wave & 1) * 32 + 8 * (lane >> 4);
+  const int c0 = part * p.Hk * kD + g * kD + 4 * m;
+  const int c1 = c0 + 64;
+  float w0[4][kTaps], w1[4][kTaps];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) y[r] = __builtin_fmaf(s.u.m.a[16 * bi + r0 + r][16 * bm + m], xv, y[r]);
+  for (int j = 0; j < kTaps; ++j) {
+    const u16x4 a0 = *reinterpret_cast<const u16x4*>(p.conv_w + (size_t)j * p.C + c0);
+    const u16x4 a1 = *reinterpret_cast<const u16x4*>(p.conv_w + (size_t)j * p.C + c1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w0[e][j] = bf2f(a0[e]);
+      w1[e][j] = bf2f(a1[e]);
     }
   }
-  float(*tmp)[17] = s.tmp[wave];
+  u16x4 r0[8 + kConvRows], r1[8 + kConvRows];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) tmp[r0 + r][col] = y[r];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float z[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int m = 0; m < 16; ++m) {
-    const float yv = tmp[m][col];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) z[r] = __builtin_fmaf(s.u.m.t[16 * bi + r0 + r][16 * bi + m], yv, z[r]);
+  for (int i = 0; i < 8 + kConvRows; ++i) {
+    r0[i] = xp_vec4(p, b, t0 + p0 - kConvRows + i, c0);
+    r1[i] = xp_vec4(p, b, t0 + p0 - kConvRows + i, c1);
   }
+  __bf16(*dst)[kD + kPadB] = part == 0 ? s.u.fe.q : s.u.fe.k;
+  const float scale_b = rbf(1.0f / sqrtf((float)kD));
+  const float eps_b = rbf(1e-6f);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) s.u.m.t[16 * bi + r0 + r][16 * bj + col] = -z[r];
+  for (int t = 0; t < 8; ++t) {
+    float u0[4], u1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      u0[e] = silu_bf(conv4_rows(bf2f(r0[t][e]), bf2f(r0[t + 1][e]), bf2f(r0[t + 2][e]), bf2f(r0[t + 3][e]), w0[e]));
+      u1[e] = silu_bf(conv4_rows(bf2f(r1[t][e]), bf2f(r1[t + 1][e]), bf2f(r1[t + 2][e]), bf2f(r1[t + 3][e]), w1[e]));
+    }
+    float pr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pr[e] = rbf(u0[e] * u0[e]) + rbf(u1[e] * u1[e]);
+    const float ssum = rbf(row16_sum((pr[0] + pr[1]) + (pr[2] + pr[3])));
+    const float den = rbf(ssum + eps_b);
+    const float rs = rbf(1.0f / sqrtf(den));
+    f4 y0, y1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y0[e] = rbf(u0[e] * rs);
+      y1[e] = rbf(u1[e] * rs);
+      if (part == 0) {
+        y0[e] = rbf(y0[e] * scale_b);
+        y1[e] = rbf(y1[e] * scale_b);
+      }
+    }
+    const int pos = p0 + t;
+    if (pos >= n) {
+      y0 = f4{0.f, 0.f, 0.f, 0.f};
+      y1 = y0;
+    }
+    *reinterpret_cast<bf4*>(&dst[pos][4 * m]) = to_bf4(y0);
+    *reinterpret_cast<bf4*>(&dst[pos][64 + 4 * m]) = to_bf4(y1);
+  }
 }
 
-template <int FE>
-__global__ __launch_bounds__(kThreads) void prefill_intra_kernel(PrefillParams p) {
+// v of v-head h into LDS as V^T [dv][pos]: conv + SiLU (model.cpp:585-595). Thread t:
+// channel t % 128, positions 32 (t / 128) .. +31.
+__device__ __forceinline__ void v_frontend(const PrefillParams& p, IntraSmem& s, int b, int h, int t0, int n,
+                                           int tid) {
+  const int dv = tid & (kD - 1), ph = (tid >> 7) * 32;
+  const int ch = 2 * p.Hk * kD + h * kD + dv;
+  float w[kTaps];
+#pragma unroll
+  for (int j = 0; j < kTaps; ++j) w[j] = bf2f(p.conv_w[(size_t)j * p.C + ch]);
+  uint16_t xr[32 + kConvRows];
+#pragma unroll
+  for (int i = 0; i < 32 + kConvRows; ++i) xr[i] = xp_row(p, b, t0 + ph - kConvRows + i, ch);
+#pragma unroll
+  for (int q8 = 0; q8 < 4; ++q8) {
+    bf8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = 8 * q8 + e;
+      const float y = silu_bf(conv4_rows(bf2f(xr[t]), bf2f(xr[t + 1]), bf2f(xr[t + 2]), bf2f(xr[t + 3]), w));
+      v[e] = (__bf16)(ph + t < n ? y : 0.0f);
+    }
+    *reinterpret_cast<bf8*>(&s.u.pr.vt[dv][ph + 8 * q8]) = v;
+  }
+}
+
+// Column j (this lane) of T = (I + A)^-1 by forward substitution, right-looking: once x_m
+// is final, x_i += (-A_im) x_m for every later row i. All lanes read the same LDS words.
+__device__ __forceinline__ void invert_column(const float (*nat)[kC + 4], int j, float (&x)[kC]) {
+#pragma unroll
+  for (int i = 0; i < kC; ++i) x[i] = i == j ? 1.0f : 0.0f;
+#pragma unroll
+  for (int m = 0; m < kC - 1; ++m) {
+#pragma unroll
+    for (int i4 = (m + 1) & ~3; i4 < kC; i4 += 4) {
+      const f4 a = *reinterpret_cast<const f4*>(&nat[m][i4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (i4 + e > m) x[i4 + e] = __builtin_fmaf(a[e], x[m], x[i4 + e]);
+      }
+    }
+  }
+}
+
+// FE: 1 conv front end, 0 given q, k, v. ONE_GROUP: the k-head has at most kGroup v-heads
+// (the K K^T / Q K^T registers are then dead after the first group).
+template <int FE, bool ONE_GROUP>
+__global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) IntraSmem s;
   const int c = blockIdx.x % p.nC;
-  int rest = blockIdx.x / p.nC;
+  const int rest = blockIdx.x / p.nC;
   const int g = rest % p.Hk;
   const int b = rest / p.Hk;
   const int t0 = c * kC;
   const int n = min(kC, p.T - t0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fk = (lane >> 4) * 8, lg = lane >> 4;
+  const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
 
   // ---- q, k of the chunk into LDS (bf16) ----
   if (FE == 1) {
-    // stage rows t0-3 .. t0+63 of the q and k channels of k-head g: 16-byte loads, all
-    // issued before any is used
-    {
-      constexpr int kVec = (kC + kConvRows) * 2 * kD / 8;  // 16-byte pieces
-      constexpr int kIter = (kVec + kThreads - 1) / kThreads;
-      u16x8 vals[kIter];
-#pragma unroll
-      for (int it = 0; it < kIter; ++it) {
-        const int e = tid + it * kThreads;
-        const int r = e / (2 * kD / 8), cc = (e % (2 * kD / 8)) * 8;
-        const int ch = (cc < kD ? 0 : p.Hk * kD - kD) + g * kD + cc;
-        vals[it] = e < kVec ? xp_vec8(p, b, t0 - kConvRows + r, ch) : u16x8{};
-      }
-#pragma unroll
-      for (int it = 0; it < kIter; ++it) {
-        const int e = tid + it * kThreads;
-        if (e < kVec) {
-          const int r = e / (2 * kD / 8), cc = (e % (2 * kD / 8)) * 8;
-          *reinterpret_cast<u16x8*>(&s.u.xs[r][cc]) = vals[it];
-        }
-      }
-    }
-    __syncthreads();
-    // wave 0/1: q of positions 0..31 / 32..63; wave 2/3: k. Lane: channels l, l+64.
-    const int part = wave >> 1;
-    const int pbase = (wave & 1) * 32;
-    const uint16_t* w_l = p.conv_w;
-    float w0[kTaps], w1[kTaps];
-    const int ch0 = part * p.Hk * kD + g * kD + lane;
-#pragma unroll
-    for (int j = 0; j < kTaps; ++j) {
-      w0[j] = bf2f(w_l[(size_t)j * p.C + ch0]);
-      w1[j] = bf2f(w_l[(size_t)j * p.C + ch0 + 64]);
-    }
-    __bf16(*dst)[kD + kPadB] = part == 0 ? s.q : s.k;
-    const int col = part * kD + lane;
-    for (int pp = 0; pp < 32; ++pp) {
-      const int pos = pbase + pp;
-      float y0 = 0.f, y1 = 0.f;
-      if (pos < n) {
-        const float u0 = silu_bf(conv4_rows(bf2f(s.u.xs[pos][col]), bf2f(s.u.xs[pos + 1][col]),
-                                            bf2f(s.u.xs[pos + 2][col]), bf2f(s.u.xs[pos + 3][col]), w0));
-        const float u1 = silu_bf(conv4_rows(bf2f(s.u.xs[pos][col + 64]), bf2f(s.u.xs[pos + 1][col + 64]),
-                                            bf2f(s.u.xs[pos + 2][col + 64]), bf2f(s.u.xs[pos + 3][col + 64]), w1));
-        // l2norm (ops.cpp:27-30) with the butterfly sum order of the decode path
-        const float scale_b = rbf(1.0f / sqrtf((float)kD));
-        const float eps_b = rbf(1e-6f);
-        const float pr = rbf(u0 * u0) + rbf(u1 * u1);
-        const float ssum = rbf(wave64_sum(pr));
-        const float den = rbf(ssum + eps_b);
-        const float rs = rbf(1.0f / sqrtf(den));
-        y0 = rbf(u0 * rs);
-        y1 = rbf(u1 * rs);
-        if (part == 0) {
-          y0 = rbf(y0 * scale_b);
-          y1 = rbf(y1 * scale_b);
-        }
-      }
-      dst[pos][lane] = to_bf(y0);
-      dst[pos][lane + 64] = to_bf(y1);
-    }
-    // the conv state hand-off: rows T..T+2 of [conv_in ; x], written by the last
+    qk_frontend(p, s, b, g, t0, n, wave, lane);
+    // the conv state hand-off: rows T-3..T-1 of [conv_in ; x], written by the last
     // chunk's workgroup of each k-head for its q, k and v channels
     if (p.conv_out && c == p.nC - 1) {
       const int nch = 2 * kD + p.rep * kD;
@@ -259,60 +297,69 @@ __global__ __launch_bounds__(kThreads) void prefill_intra_kernel(PrefillParams p
       }
     }
   } else {
-    for (int e = tid; e < kC * kD; e += kThreads) {
-      const int pos = e / kD, d = e % kD;
-      __bf16 qv = to_bf(0.f), kv = to_bf(0.f);
-      if (pos < n) {
-        const size_t gi = (((size_t)b * p.T + t0 + pos) * p.Hk + g) * kD + d;
-        qv = p.q[gi];
-        kv = p.k[gi];
-      }
-      s.q[pos][d] = qv;
-      s.k[pos][d] = kv;
-    }
-  }
-  __syncthreads();
-
-  // ---- q, k, k^T to the workspace ----
-  {
-    const size_t base = (((size_t)b * p.Hk + g) * p.nC + c) * kC * kD;
     for (int e = tid; e < kC * kD / 8; e += kThreads) {
       const int pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      *reinterpret_cast<bf8*>(p.ws_q + base + pos * kD + d8) = frag(s.q, pos, d8);
-      *reinterpret_cast<bf8*>(p.ws_k + base + pos * kD + d8) = frag(s.k, pos, d8);
-    }
-    for (int e = tid; e < kC * kD; e += kThreads) {
-      const int d = e / kC, pos = e % kC;
-      p.ws_kt[base + (size_t)d * kC + pos] = s.k[pos][d];
-    }
-  }
-
-  // ---- K K^T and Q K^T (64 x 64) on MFMA: wave w takes row tile w ----
-  {
-    const int fr = lane & 15, fk = (lane >> 4) * 8;
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      f4 ag = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kD / 32; ++ks) {
-        const bf8 bk = frag(s.k, 16 * ct + fr, 32 * ks + fk);
-        ag = mfma(frag(s.k, 16 * wave + fr, 32 * ks + fk), bk, ag);
-        aq = mfma(frag(s.q, 16 * wave + fr, 32 * ks + fk), bk, aq);
+      bf8 qv = {}, kv = {};
+      if (pos < n) {
+        const size_t gi = (((size_t)b * p.T + t0 + pos) * p.Hk + g) * kD + d8;
+        qv = *reinterpret_cast<const bf8*>(p.q + gi);
+        kv = *reinterpret_cast<const bf8*>(p.k + gi);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s.gram[16 * wave + (lane >> 4) * 4 + i][16 * ct + fr] = ag[i];
-        s.qk[16 * wave + (lane >> 4) * 4 + i][16 * ct + fr] = aq[i];
-      }
+      *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = qv;
+      *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = kv;
     }
   }
   __syncthreads();
 
-  // ---- per v-head: gates, T', M ----
-  for (int r = 0; r < p.rep; ++r) {
-    const int h = g * p.rep + r;
-    const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-    if (wave == 0) {
+  // ---- K K^T and K Q^T on MFMA (wave w: rows j = 16w..; kept in registers), Q to the
+  // workspace, K^T into LDS ----
+  f4 gr[4], kq[4];  // lane: (j = 16 wave + 4 lg + e, i = 16 ct + fr): (K K^T)_ji, (Q K^T)_ij
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    gr[ct] = f4{0.f, 0.f, 0.f, 0.f};
+    kq[ct] = gr[ct];
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) {
+      const bf8 ak = frag(s.u.fe.k, 16 * wave + fr, 32 * ks + fk);
+      gr[ct] = mfma(ak, frag(s.u.fe.k, 16 * ct + fr, 32 * ks + fk), gr[ct]);
+      kq[ct] = mfma(ak, frag(s.u.fe.q, 16 * ct + fr, 32 * ks + fk), kq[ct]);
+    }
+  }
+  {
+    __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) {
+      *reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag) = frag(s.u.fe.q, 16 * wave + fr, 32 * ks + fk);
+    }
+    const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
+#pragma unroll
+    for (int q8 = 0; q8 < 4; ++q8) {
+      bf8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = s.u.fe.k[ph + 8 * q8 + e][dk];
+      *reinterpret_cast<bf8*>(&s.kt[dk][ph + 8 * q8]) = v;
+    }
+  }
+  __syncthreads();
+  {
+    __bf16* wkt = p.ws_kt + gc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int a2 = 0; a2 < 2; ++a2)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int a = 2 * wave + a2;
+        *reinterpret_cast<bf8*>(wkt + (a * 2 + ks) * kFrag) = frag(s.kt, 16 * a + fr, 32 * ks + fk);
+      }
+  }
+
+  // ---- the k-head's v-heads, in groups of up to three ----
+  const int rep_end = ONE_GROUP ? 1 : p.rep;
+  for (int r0 = 0; r0 < rep_end; r0 += kGroup) {
+    const int gs = min(kGroup, p.rep - r0);
+    // gates and the in-chunk log decay (wave r: v-head r0 + r, lane = position)
+    if (wave < gs) {
+      const int h = g * p.rep + r0 + wave;
+      const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
       float al = 1.0f, be = 0.0f;  // padded steps: alpha 1, beta 0 (exact no-ops)
       if (lane < n) {
         const size_t gi = ((size_t)b * p.T + t0 + lane) * p.Hv + h;
@@ -325,14 +372,13 @@ __global__ __launch_bounds__(kThreads) void prefill_intra_kernel(PrefillParams p
       }
       const float ac = al < 1e-6f ? 1e-6f : (al > 1.0f ? 1.0f : al);
       float G = ac == 1.0f ? 0.0f : d_logf(ac);
-      // inclusive prefix sum over the 64 lanes (positions)
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float up = __shfl_up(G, off, 64);
         if (lane >= off) G = G + up;
       }
-      s.G[lane] = G;
-      s.beta[lane] = be;
+      s.G[wave][lane] = G;
+      s.beta[wave][lane] = be;
       const float Gl = __shfl(G, 63, 64);
       float* wg = p.ws_g + hc * kGStride;
       wg[lane] = d_expf(G);
@@ -340,311 +386,264 @@ __global__ __launch_bounds__(kThreads) void prefill_intra_kernel(PrefillParams p
       if (lane == 0) wg[128] = d_expf(Gl);
     }
     __syncthreads();
-    // A (strictly lower) and M (lower incl. diagonal)
-    __bf16* wm = p.ws_M + hc * 2 * kC * kC;
-    for (int e = tid; e < kC * kC; e += kThreads) {
-      const int i = e / kC, j = e % kC;
-      float av = 0.f, mv = 0.f;
-      if (j <= i) {
-        const float dr = d_expf(s.G[i] - s.G[j]);
-        mv = dr * s.qk[i][j];
-        if (j < i) av = s.beta[i] * dr * s.gram[i][j];
+
+    // A (into LDS as -A^T) and M (hi, lo to the workspace) from the registers
+    for (int r = 0; r < gs; ++r) {
+      const size_t hc = ((size_t)b * p.Hv + g * p.rep + r0 + r) * p.nC + c;
+      __bf16* wm = p.ws_m + hc * kChunkElems;
+      const int j0 = 16 * wave + 4 * lg;
+      const f4 Gj = *reinterpret_cast<const f4*>(&s.G[r][j0]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int i = 16 * ct + fr;
+        const float Gi = s.G[r][i], bi = s.beta[r][i];
+        f4 mv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + e;
+          const float dr = j <= i ? fast_exp(Gi - Gj[e]) : 0.0f;
+          mv[e] = dr * kq[ct][e];
+          s.u.nat[r][j][i] = j < i ? -((bi * dr) * gr[ct][e]) : 0.0f;
+        }
+        const bf4 hi = to_bf4(mv);
+        const bf4 lo = to_bf4(mv - from_bf4(hi));
+        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks interleaved
+        const int blk = ((i >> 4) * 2 + (j0 >> 5)) * 2;
+        const int within = ((i & 15) + 16 * ((j0 & 31) >> 3)) * 8 + (j0 & 7);
+        *reinterpret_cast<bf4*>(wm + blk * kFrag + within) = hi;
+        *reinterpret_cast<bf4*>(wm + (blk + 1) * kFrag + within) = lo;
       }
-      s.u.m.a[i][j] = av;
-      s.u.m.t[i][j] = 0.f;
-      const __bf16 hi = to_bf(mv);
-      wm[e] = hi;
-      wm[kC * kC + e] = to_bf(mv - from_bf(hi));
     }
     __syncthreads();
-    // T = (I + A)^-1: diagonal 16x16 blocks by forward substitution (wave w, block w;
-    // lane = column), then the off-diagonal blocks by block distance
-    if (lane < 16) {
-      const int o = 16 * wave;
-      float xcol[16];
+
+    // T = (I + A)^-1: wave r inverts v-head r0 + r, lane j = column j
+    float x[kC];
+    if (wave < gs) invert_column(s.u.nat[wave], lane, x);
+    __syncthreads();
+
+    for (int r = 0; r < gs; ++r) {
+      const int h = g * p.rep + r0 + r;
+      const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
+      if (FE == 1) {
+        v_frontend(p, s, b, h, t0, n, tid);
+      } else {
+        const int dv = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = (i == lane) ? 1.0f : 0.0f;
+        for (int q8 = 0; q8 < 4; ++q8) {
+          bf8 v;
 #pragma unroll
-        for (int m = 0; m < i; ++m) v = __builtin_fmaf(-s.u.m.a[o + i][o + m], xcol[m], v);
-        xcol[i] = v;
+          for (int e = 0; e < 8; ++e) {
+            const int pos = ph + 8 * q8 + e;
+            const __bf16 val = p.v[(((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hv + h) * kD + dv];
+            v[e] = pos < n ? val : (__bf16)0.0f;
+          }
+          *reinterpret_cast<bf8*>(&s.u.pr.vt[dv][ph + 8 * q8]) = v;
+        }
       }
+      if (wave == r) {
+        // T' = T diag(beta) (hi + lo) and T' diag(e^G), column j = lane
+        const float bj = s.beta[r][lane];
+        const float ej = d_expf(s.G[r][lane]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s.u.m.t[o + i][o + lane] = xcol[i];
+        for (int i = 0; i < kC; ++i) {
+          const float tv = x[i] * bj;
+          const __bf16 hi = (__bf16)tv;
+          s.u.pr.th[i][lane] = hi;
+          s.u.pr.tl[i][lane] = (__bf16)(tv - (float)hi);
+          s.u.pr.te[i][lane] = (__bf16)(tv * ej);
+        }
+      }
+      __syncthreads();
+      // U = T' V: wave w takes position tile w, all eight dv tiles
+      {
+        const bf8 ah0 = frag(s.u.pr.th, 16 * wave + fr, fk), ah1 = frag(s.u.pr.th, 16 * wave + fr, 32 + fk);
+        const bf8 al0 = frag(s.u.pr.tl, 16 * wave + fr, fk), al1 = frag(s.u.pr.tl, 16 * wave + fr, 32 + fk);
+        float* wu = p.ws_u + hc * kChunkElems + lane * 4;
+#pragma unroll
+        for (int d = 0; d < kD / 16; ++d) {
+          const bf8 b0 = frag(s.u.pr.vt, 16 * d + fr, fk), b1 = frag(s.u.pr.vt, 16 * d + fr, 32 + fk);
+          f4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma(ah0, b0, acc);
+          acc = mfma(al0, b0, acc);
+          acc = mfma(ah1, b1, acc);
+          acc = mfma(al1, b1, acc);
+          *reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256) = acc;
+        }
+      }
+      // W^T = K^T (T' e^G)^T: wave w takes dk tiles 2w, 2w+1, all position tiles; lane
+      // gets W[i = 16 bt + fr][dk = 16 a + 4 lg .. +3]
+      {
+        __bf16* ww = p.ws_w + hc * kChunkElems;
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2) {
+          const int a = 2 * wave + a2;
+          const bf8 k0 = frag(s.kt, 16 * a + fr, fk), k1 = frag(s.kt, 16 * a + fr, 32 + fk);
+#pragma unroll
+          for (int bt = 0; bt < 4; ++bt) {
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = mfma(k0, frag(s.u.pr.te, 16 * bt + fr, fk), acc);
+            acc = mfma(k1, frag(s.u.pr.te, 16 * bt + fr, 32 + fk), acc);
+            *reinterpret_cast<bf4*>(ww + frag_off(16 * bt + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
+          }
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    if (wave < 3) inverse_offdiag(s, wave + 1, wave, wave, lane);
-    __syncthreads();
-    if (wave < 2) inverse_offdiag(s, wave + 2, wave, wave, lane);
-    __syncthreads();
-    if (wave == 0) inverse_offdiag(s, 3, 0, wave, lane);
-    __syncthreads();
-    // T' = T diag(beta), split into bf16 hi + lo
-    __bf16* wt = p.ws_T + hc * 2 * kC * kC;
-    for (int e = tid; e < kC * kC; e += kThreads) {
-      const int i = e / kC, j = e % kC;
-      const float tv = s.u.m.t[i][j] * s.beta[j];
-      const __bf16 hi = to_bf(tv);
-      wt[e] = hi;
-      wt[kC * kC + e] = to_bf(tv - from_bf(hi));
-    }
-    __syncthreads();
   }
 }
 
 // ============================================================================ scan
 
 struct ScanSmem {
-  __bf16 q[kC][kD + kPadB];
-  __bf16 k[kC][kD + kPadB];
-  __bf16 kt[kD][kC + kPadB];
-  __bf16 th[kC][kC + kPadB];
-  __bf16 tl[kC][kC + kPadB];
-  __bf16 mh[kC][kC + kPadB];
-  __bf16 ml[kC][kC + kPadB];
-  __bf16 st[kDt][kD + kPadB];    // S^T (bf16): [dt][dk]
-  __bf16 rh[kDt][kC + kPadB];    // R: [dt][pos]
-  __bf16 rl[kDt][kC + kPadB];
-  __bf16 vph[kDt][kC + kPadB];   // V'
-  __bf16 vpl[kDt][kC + kPadB];
-  __bf16 vpp[kDt][kC + kPadB];   // e^(G63-G) V'
-  float v[kC][kDt + 1];
-  float eg[kC];
-  float egr[kC];
-  uint16_t xs[kC + kConvRows][kDt];  // 64-byte rows, 16-byte aligned
-  float gam;
+  __bf16 st[kDt][kD + kPadB];  // S^T (bf16): [dt][dk]
+  __bf16 vh[kDt][kC + kPadB];  // V' hi: [dt][pos]
+  __bf16 vl[kDt][kC + kPadB];  // V' lo
+  __bf16 vp[kDt][kC + kPadB];  // e^(G63-G) V'
 };
 
-template <int FE>
+// One chunk's operands of one wave, in registers.
+struct ChunkIn {
+  bf8 q[4];       // Q rows 16w.., k = dk
+  bf8 w[4];       // W rows 16w.., k = dk
+  bf8 kt[2][2];   // K^T rows 32w + 16rt.., k = pos
+  bf8 m[2][2];    // M rows 16w.., k = pos; [ks][hi, lo]
+  f4 u[2];        // U (pos 16w + 4lg + e, dv 32jt + 16ct + fr)
+  f4 eg, egr;     // e^G, e^(G63-G) at pos 16w + 4lg + e
+  float gam;      // e^G63
+};
+
+__device__ __forceinline__ void load_chunk(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
+                                           int lane, ChunkIn& in) {
+  const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
+  const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
+  const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
+  const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
+  const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
+  const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    in.q[ks] = *reinterpret_cast<const bf8*>(q + (wave * 4 + ks) * kFrag);
+    in.w[ks] = *reinterpret_cast<const bf8*>(w + (wave * 4 + ks) * kFrag);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      in.kt[i][j] = *reinterpret_cast<const bf8*>(kt + ((2 * wave + i) * 2 + j) * kFrag);
+      in.m[i][j] = *reinterpret_cast<const bf8*>(m + ((wave * 2 + i) * 2 + j) * kFrag);
+    }
+  const float* u = p.ws_u + hc * kChunkElems + lane * 4;
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) in.u[ct] = *reinterpret_cast<const f4*>(u + ((2 * jt + ct) * 4 + wave) * 256);
+  const float* gg = p.ws_g + hc * kGStride + 16 * wave + 4 * (lane >> 4);
+  in.eg = *reinterpret_cast<const f4*>(gg);
+  in.egr = *reinterpret_cast<const f4*>(gg + 64);
+  in.gam = p.ws_g[hc * kGStride + 128];
+}
+
+// One chunk: uses `in`, loads chunk c + 1 (the last chunk again at the end) into `nx`.
+__device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, f4 (&S)[2][2], const ChunkIn& in,
+                                           ChunkIn& nx, int b, int g, int h, int jt, int c, int wave, int lane) {
+  const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
+  // S^T in bf16 for the W S and Q S products
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+      *reinterpret_cast<bf4*>(&s.st[16 * ct + fr][32 * wave + 16 * rt + fq]) = to_bf4(S[rt][ct]);
+  __syncthreads();
+  load_chunk(p, b, g, h, jt, min(c + 1, p.nC - 1), wave, lane, nx);
+
+  // P = W S, QS = Q S (wave w: positions 16w..); V' = U - P
+  f4 QS[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    f4 P = {0.f, 0.f, 0.f, 0.f};
+    QS[ct] = P;
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) {
+      const bf8 bs = frag(s.st, 16 * ct + fr, 32 * ks + fk);
+      P = mfma(in.w[ks], bs, P);
+      QS[ct] = mfma(in.q[ks], bs, QS[ct]);
+    }
+    const f4 vpr = in.u[ct] - P;
+    const bf4 hi = to_bf4(vpr);
+    *reinterpret_cast<bf4*>(&s.vh[16 * ct + fr][16 * wave + fq]) = hi;
+    *reinterpret_cast<bf4*>(&s.vl[16 * ct + fr][16 * wave + fq]) = to_bf4(vpr - from_bf4(hi));
+    *reinterpret_cast<bf4*>(&s.vp[16 * ct + fr][16 * wave + fq]) = to_bf4(in.egr * vpr);
+  }
+  __syncthreads();
+
+  // y = e^G . QS + M V' (split operands)
+  const int t0 = c * kC;
+  const int n = min(kC, p.T - t0);
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kC / 32; ++ks) {
+      const bf8 bh = frag(s.vh, 16 * ct + fr, 32 * ks + fk);
+      const bf8 bl = frag(s.vl, 16 * ct + fr, 32 * ks + fk);
+      acc = mfma(in.m[ks][0], bh, acc);
+      acc = mfma(in.m[ks][1], bh, acc);
+      acc = mfma(in.m[ks][0], bl, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int pos = 16 * wave + fq + e;
+      if (pos < n) {
+        const float y = in.eg[e] * QS[ct][e] + acc[e];
+        const size_t oi = (((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + 16 * ct + fr;
+        if (p.o_bf16) {
+          static_cast<uint16_t*>(p.o)[oi] = f2bf(y);
+        } else {
+          static_cast<float*>(p.o)[oi] = y;
+        }
+      }
+    }
+  }
+
+  // S = e^G63 S + K^T (e^(G63-G) V')
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      f4 acc = S[rt][ct] * in.gam;
+#pragma unroll
+      for (int ks = 0; ks < kC / 32; ++ks) acc = mfma(in.kt[rt][ks], frag(s.vp, 16 * ct + fr, 32 * ks + fk), acc);
+      S[rt][ct] = acc;
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) ScanSmem s;
   const int jt = blockIdx.x % (kD / kDt);
-  int rest = blockIdx.x / (kD / kDt);
+  const int rest = blockIdx.x / (kD / kDt);
   const int h = rest % p.Hv;
   const int b = rest / p.Hv;
   const int g = h / p.rep;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
-  const int vch0 = 2 * p.Hk * kD + h * kD + jt * kDt;  // first v channel of the tile
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int fr = lane & 15, fq = (lane >> 4) * 4;
 
-  // S tile (Dk x 32) in accumulators: wave w holds dk rows 32w + 16rt + fq + i, dt 16ct + fr
+  // S tile (Dk x 32) in accumulators: wave w holds dk rows 32w + 16rt + fq + e, dt 16ct + fr
   f4 S[2][2];
-  {
-    const float* sin = p.state_in ? p.state_in + ((size_t)b * p.Hv + h) * kD * kD : nullptr;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int dk = 32 * wave + 16 * rt + fq + i, dt = 16 * ct + fr;
-          S[rt][ct][i] = sin ? sin[(size_t)(jt * kDt + dt) * kD + dk] : 0.0f;
-        }
-  }
-  float wv[kTaps] = {};
-  if (FE == 1) {
-    const int dt = tid & (kDt - 1);
-#pragma unroll
-    for (int j = 0; j < kTaps; ++j) wv[j] = bf2f(p.conv_w[(size_t)j * p.C + vch0 + dt]);
-  }
-
-  for (int c = 0; c < p.nC; ++c) {
-    const int t0 = c * kC;
-    const int n = min(kC, p.T - t0);
-    const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
-    const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-
-    // ---- stage the chunk: every 16-byte load issued before any is stored ----
-    {
-      constexpr int kQK = kC * kD / 8 / kThreads;  // 4 pieces per thread per matrix
-      constexpr int kTM = kC * kC / 8 / kThreads;  // 2
-      bf8 vq[kQK], vk[kQK], vkt[kQK], vth[kTM], vtl[kTM], vmh[kTM], vml[kTM];
-      const __bf16* wq = p.ws_q + gc * kC * kD;
-      const __bf16* wk = p.ws_k + gc * kC * kD;
-      const __bf16* wkt = p.ws_kt + gc * kC * kD;
-      const __bf16* wt = p.ws_T + hc * 2 * kC * kC;
-      const __bf16* wm = p.ws_M + hc * 2 * kC * kC;
-#pragma unroll
-      for (int it = 0; it < kQK; ++it) {
-        const int e = tid + it * kThreads;
-        vq[it] = *reinterpret_cast<const bf8*>(wq + e * 8);
-        vk[it] = *reinterpret_cast<const bf8*>(wk + e * 8);
-        vkt[it] = *reinterpret_cast<const bf8*>(wkt + e * 8);
-      }
-#pragma unroll
-      for (int it = 0; it < kTM; ++it) {
-        const int e = tid + it * kThreads;
-        vth[it] = *reinterpret_cast<const bf8*>(wt + e * 8);
-        vtl[it] = *reinterpret_cast<const bf8*>(wt + kC * kC + e * 8);
-        vmh[it] = *reinterpret_cast<const bf8*>(wm + e * 8);
-        vml[it] = *reinterpret_cast<const bf8*>(wm + kC * kC + e * 8);
-      }
-      float gv = 0.f, grv = 0.f, gam = 0.f;
-      const float* wg = p.ws_g + hc * kGStride;
-      if (tid < kC) {
-        gv = wg[tid];
-        grv = wg[64 + tid];
-        gam = wg[128];
-      }
-      u16x8 xv[2] = {};
-      constexpr int kXV = (kC + kConvRows) * kDt / 8;  // 268 pieces
-      if (FE == 1) {
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          const int e = tid + it * kThreads;
-          if (e < kXV) xv[it] = xp_vec8(p, b, t0 - kConvRows + e / (kDt / 8), vch0 + (e % (kDt / 8)) * 8);
-        }
-      }
-#pragma unroll
-      for (int it = 0; it < kQK; ++it) {
-        const int e = tid + it * kThreads;
-        *reinterpret_cast<bf8*>(&s.q[e / (kD / 8)][(e % (kD / 8)) * 8]) = vq[it];
-        *reinterpret_cast<bf8*>(&s.k[e / (kD / 8)][(e % (kD / 8)) * 8]) = vk[it];
-        *reinterpret_cast<bf8*>(&s.kt[e / (kC / 8)][(e % (kC / 8)) * 8]) = vkt[it];
-      }
-#pragma unroll
-      for (int it = 0; it < kTM; ++it) {
-        const int e = tid + it * kThreads, i = e / (kC / 8), j8 = (e % (kC / 8)) * 8;
-        *reinterpret_cast<bf8*>(&s.th[i][j8]) = vth[it];
-        *reinterpret_cast<bf8*>(&s.tl[i][j8]) = vtl[it];
-        *reinterpret_cast<bf8*>(&s.mh[i][j8]) = vmh[it];
-        *reinterpret_cast<bf8*>(&s.ml[i][j8]) = vml[it];
-      }
-      if (tid < kC) {
-        s.eg[tid] = gv;
-        s.egr[tid] = grv;
-        if (tid == 0) s.gam = gam;
-      }
-      if (FE == 1) {
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          const int e = tid + it * kThreads;
-          if (e < kXV) *reinterpret_cast<u16x8*>(&s.xs[e / (kDt / 8)][(e % (kDt / 8)) * 8]) = xv[it];
-        }
-      }
-    }
-    if (FE == 1) {
-    } else {
-      for (int e = tid; e < kC * kDt; e += kThreads) {
-        const int pos = e / kDt, dt = e % kDt;
-        s.v[pos][dt] = pos < n ? from_bf(p.v[(((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + dt]) : 0.0f;
-      }
-    }
-    // S^T in bf16 for the K S and Q S products
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s.st[16 * ct + fr][32 * wave + 16 * rt + fq + i] = to_bf(S[rt][ct][i]);
-    __syncthreads();
-    if (FE == 1) {
-      // v = silu(conv(x)) for the tile's 32 channels (bf16 values)
-      const int dt = tid & (kDt - 1);
-      for (int pos = tid / kDt; pos < kC; pos += kThreads / kDt) {
-        float val = 0.f;
-        if (pos < n) {
-          val = silu_bf(conv4_rows(bf2f(s.xs[pos][dt]), bf2f(s.xs[pos + 1][dt]), bf2f(s.xs[pos + 2][dt]),
-                                   bf2f(s.xs[pos + 3][dt]), wv));
-        }
-        s.v[pos][dt] = val;
-      }
-      __syncthreads();
-    }
-
-    // ---- P = K S, QS = Q S (64 x 32): wave w takes position rows 16w.. ----
-    f4 QS[2];
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      f4 P = {0.f, 0.f, 0.f, 0.f};
-      QS[ct] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kD / 32; ++ks) {
-        const bf8 bs = frag(s.st, 16 * ct + fr, 32 * ks + fk);
-        P = mfma(frag(s.k, 16 * wave + fr, 32 * ks + fk), bs, P);
-        QS[ct] = mfma(frag(s.q, 16 * wave + fr, 32 * ks + fk), bs, QS[ct]);
-      }
-      // R = V - e^G . P, split into hi + lo, stored [dt][pos]
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos = 16 * wave + fq + i, dt = 16 * ct + fr;
-        const float rv = s.v[pos][dt] - s.eg[pos] * P[i];
-        const __bf16 hi = to_bf(rv);
-        s.rh[dt][pos] = hi;
-        s.rl[dt][pos] = to_bf(rv - from_bf(hi));
-      }
-    }
-    __syncthreads();
-
-    // ---- V' = T' R (split operands) ----
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kC / 32; ++ks) {
-        const bf8 ah = frag(s.th, 16 * wave + fr, 32 * ks + fk);
-        const bf8 al = frag(s.tl, 16 * wave + fr, 32 * ks + fk);
-        const bf8 bh = frag(s.rh, 16 * ct + fr, 32 * ks + fk);
-        const bf8 bl = frag(s.rl, 16 * ct + fr, 32 * ks + fk);
-        acc = mfma(ah, bh, acc);
-        acc = mfma(al, bh, acc);
-        acc = mfma(ah, bl, acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos = 16 * wave + fq + i, dt = 16 * ct + fr;
-        const __bf16 hi = to_bf(acc[i]);
-        s.vph[dt][pos] = hi;
-        s.vpl[dt][pos] = to_bf(acc[i] - from_bf(hi));
-        s.vpp[dt][pos] = to_bf(s.egr[pos] * acc[i]);
-      }
-    }
-    __syncthreads();
-
-    // ---- y = e^G . QS + M V' (split operands) ----
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < kC / 32; ++ks) {
-        const bf8 ah = frag(s.mh, 16 * wave + fr, 32 * ks + fk);
-        const bf8 al = frag(s.ml, 16 * wave + fr, 32 * ks + fk);
-        const bf8 bh = frag(s.vph, 16 * ct + fr, 32 * ks + fk);
-        const bf8 bl = frag(s.vpl, 16 * ct + fr, 32 * ks + fk);
-        acc = mfma(ah, bh, acc);
-        acc = mfma(al, bh, acc);
-        acc = mfma(ah, bl, acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos = 16 * wave + fq + i, dt = 16 * ct + fr;
-        if (pos < n) {
-          const float y = s.eg[pos] * QS[ct][i] + acc[i];
-          const size_t oi = (((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + dt;
-          if (p.o_bf16) {
-            static_cast<uint16_t*>(p.o)[oi] = f2bf(y);
-          } else {
-            static_cast<float*>(p.o)[oi] = y;
-          }
-        }
+      S[rt][ct] = f4{0.f, 0.f, 0.f, 0.f};
+      if (p.state_in) {
+        const float* sin = p.state_in + ((size_t)b * p.Hv + h) * kD * kD;
+        S[rt][ct] = *reinterpret_cast<const f4*>(sin + (size_t)(jt * kDt + 16 * ct + fr) * kD + 32 * wave + 16 * rt + fq);
       }
     }
 
-    // ---- S = e^G63 S + K^T (e^(G63-G) V') ----
-    const float gam = s.gam;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        f4 acc = S[rt][ct] * gam;
-#pragma unroll
-        for (int ks = 0; ks < kC / 32; ++ks) {
-          acc = mfma(frag(s.kt, 32 * wave + 16 * rt + fr, 32 * ks + fk), frag(s.vpp, 16 * ct + fr, 32 * ks + fk), acc);
-        }
-        S[rt][ct] = acc;
-      }
-    __syncthreads();
+  ChunkIn A, B;
+  load_chunk(p, b, g, h, jt, 0, wave, lane, A);
+  for (int c = 0; c < p.nC; c += 2) {
+    scan_chunk(p, s, S, A, B, b, g, h, jt, c, wave, lane);
+    if (c + 1 < p.nC) scan_chunk(p, s, S, B, A, b, g, h, jt, c + 1, wave, lane);
   }
 
   if (p.state_out) {
@@ -653,24 +652,35 @@ __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p)
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int dk = 32 * wave + 16 * rt + fq + i, dt = 16 * ct + fr;
-          sout[(size_t)(jt * kDt + dt) * kD + dk] = S[rt][ct][i];
-        }
+        *reinterpret_cast<f4*>(sout + (size_t)(jt * kDt + 16 * ct + fr) * kD + 32 * wave + 16 * rt + fq) = S[rt][ct];
   }
+}
+
+struct WorkspaceLayout {
+  size_t q, kt, w, m, u, g, total;
+};
+
+WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv) {
+  const size_t nC = (size_t)(T + kC - 1) / kC;
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
+  const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
+  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * 4);
+  const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
+  WorkspaceLayout L;
+  L.q = 0;
+  L.kt = L.q + qk;
+  L.w = L.kt + qk;
+  L.m = L.w + wm;
+  L.u = L.m + wm;
+  L.g = L.u + uu;
+  L.total = L.g + gg;
+  return L;
 }
 
 }  // namespace
 
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv) {
-  const size_t nC = (size_t)(T + kC - 1) / kC;
-  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t qk = al((size_t)B * Hk * nC * kC * kD * 2);
-  const size_t tm = al((size_t)B * Hv * nC * 2 * kC * kC * 2);
-  const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
-  return 3 * qk + 2 * tm + gg;
-}
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv) { return workspace_layout(B, T, Hk, Hv).total; }
 
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream) {
   PrefillParams p{};
@@ -699,28 +709,27 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.state_in = a.state_in;
   p.state_out = a.state_out;
   p.o = a.o;
-  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t nC = p.nC;
+  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv);
   char* w = static_cast<char*>(workspace);
-  const size_t qk = al((size_t)p.B * p.Hk * nC * kC * kD * 2);
-  const size_t tm = al((size_t)p.B * p.Hv * nC * 2 * kC * kC * 2);
-  p.ws_q = reinterpret_cast<__bf16*>(w);
-  p.ws_k = reinterpret_cast<__bf16*>(w + qk);
-  p.ws_kt = reinterpret_cast<__bf16*>(w + 2 * qk);
-  p.ws_T = reinterpret_cast<__bf16*>(w + 3 * qk);
-  p.ws_M = reinterpret_cast<__bf16*>(w + 3 * qk + tm);
-  p.ws_g = reinterpret_cast<float*>(w + 3 * qk + 2 * tm);
+  p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
+  p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
+  p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
+  p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
+  p.ws_u = reinterpret_cast<float*>(w + L.u);
+  p.ws_g = reinterpret_cast<float*>(w + L.g);
 
   const dim3 block(kThreads);
   const dim3 g1((unsigned)((size_t)p.B * p.Hk * p.nC));
   const dim3 g2((unsigned)((size_t)p.B * p.Hv * (kD / kDt)));
+  const bool one = p.rep <= kGroup;
   if (a.frontend == GDN_FRONTEND_CONV) {
-    hipLaunchKernelGGL((prefill_intra_kernel<1>), g1, block, 0, stream, p);
-    hipLaunchKernelGGL((prefill_scan_kernel<1>), g2, block, 0, stream, p);
+    if (one) hipLaunchKernelGGL((prefill_intra_kernel<1, true>), g1, block, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_intra_kernel<1, false>), g1, block, 0, stream, p);
   } else {
-    hipLaunchKernelGGL((prefill_intra_kernel<0>), g1, block, 0, stream, p);
-    hipLaunchKernelGGL((prefill_scan_kernel<0>), g2, block, 0, stream, p);
+    if (one) hipLaunchKernelGGL((prefill_intra_kernel<0, true>), g1, block, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_intra_kernel<0, false>), g1, block, 0, stream, p);
   }
+  hipLaunchKernelGGL(prefill_scan_kernel, g2, block, 0, stream, p);
   return hipGetLastError();
 }
 

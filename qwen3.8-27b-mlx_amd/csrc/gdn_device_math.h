@@ -28,15 +28,23 @@ __device__ __forceinline__ uint32_t f_bits(float x) { return __builtin_bit_cast(
 // exhaustively on the device).
 __device__ __forceinline__ uint16_t f2bf(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 __device__ __forceinline__ float bf2f(uint16_t h) { return bits_f((uint32_t)h << 16); }
-// Round an fp32 value to the nearest bf16 value, kept in fp32.
-__device__ __forceinline__ float rbf(float x) { return bf2f(f2bf(x)); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round an fp32 value to the nearest bf16 value, kept in fp32: the pair (0, x) packs to
+// bf16(x) << 16 | bf16(0), which is that value's fp32 bit pattern (one instruction).
+__device__ __forceinline__ float rbf(float x) {
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2_t){0.0f, x}, bf16x2_t));
+}
+
+// The special cases (NaN, overflow, underflow) are applied by select after the
+// polynomial path has run on an argument clamped into range, so the function has no
+// branches; for in-range arguments the clamp is the identity and every op is as listed.
 __device__ __forceinline__ float d_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.97208404541015625f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 89.0f);
+  const float n = __builtin_rintf(xc * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
   r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
   float p = 1.98412698412698412698e-4f;
   p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
@@ -49,7 +57,10 @@ __device__ __forceinline__ float d_expf(float x) {
   const int ni = (int)n;
   const int n1 = ni / 2, n2 = ni - n1;
   p = p * bits_f((uint32_t)(n1 + 127) << 23);
-  return p * bits_f((uint32_t)(n2 + 127) << 23);
+  float y = p * bits_f((uint32_t)(n2 + 127) << 23);
+  y = x > 88.72283935546875f ? __builtin_inff() : y;
+  y = x < -103.97208404541015625f ? 0.0f : y;
+  return x != x ? x : y;
 }
 
 // log of a positive normal argument (the only arguments used here are in (1, 2]).
@@ -96,6 +107,25 @@ __device__ __forceinline__ float d_softplusf(float x) {
   const float mn = x > 0.0f ? 0.0f : x;
   if (mn == -__builtin_inff() || mx == __builtin_inff()) return mx;
   return mx + d_log1pf(d_expf(mn - mx));
+}
+
+// silu on a bf16 value: x * sigmoid(x), both ops rounded (cpp/src/ops.cpp:20).
+__device__ __forceinline__ float silu_bf(float y) {
+  const float sg = rbf(d_sigmoidf(y));
+  return rbf(y * sg);
+}
+
+// Sum over the 16 lanes of a DPP row; every lane receives the same total.
+// quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror. When lane m of
+// the row holds the partial sum of group m, this is the butterfly p[m] += p[m ^ s],
+// s = 1, 2, 4, 8, bit for bit: after each step the lanes being combined hold equal
+// values, so the mirrors pick the same operands the xor partners would.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
+  return x;
 }
 
 // Gate math of cpp/src/model.cpp:608-612 for one (step, v-head).

@@ -41,16 +41,6 @@ constexpr int kThreads = 256;                 // 4 waves
 constexpr int kSlots = 4;                     // rows per 16-lane group
 constexpr int kTC = 8;                        // steps staged in LDS per pass
 
-// Sum over the 16 lanes of a DPP row; every lane receives the same total.
-// quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror.
-__device__ __forceinline__ float row16_sum(float x) {
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
-  return x;
-}
-
 // Butterfly sum over a whole wave64 in the fixed order p[l] += p[l ^ m],
 // m = 1, 2, 4, 8, 16, 32: the l2norm sum order, fixed so that its bf16 rounding is
 // reproducible (MLX does not pin the order of its bf16 reductions).
@@ -72,12 +62,6 @@ __device__ __forceinline__ float conv4(const float (&xv)[kTaps], const float (&w
 #pragma unroll
   for (int j = 1; j < kTaps; ++j) y = rbf(y + rbf(xv[j] * wv[j]));
   return y;
-}
-
-// silu on a bf16 value: x * sigmoid(x), both ops rounded (ops.cpp:20).
-__device__ __forceinline__ float silu_bf(float y) {
-  const float sg = rbf(d_sigmoidf(y));
-  return rbf(y * sg);
 }
 
 // l2norm of a 128-vector held as (u0, u1) = elements (lane, lane+64) of a wave
