@@ -499,7 +499,31 @@ struct ScanSmem {
   __bf16 vh[kDt][kC + kPadB];  // V' hi: [dt][pos]
   __bf16 vl[kDt][kC + kPadB];  // V' lo
   __bf16 vp[kDt][kC + kPadB];  // e^(G63-G) V'
+  float y[kC][kDt + 4];        // the chunk's outputs, written to o one chunk later
 };
+
+// The outputs staged in s.y for the chunk starting at t0 (n positions) to o: thread t
+// stores positions t / 4, columns 8 (t % 4) .. +7 of the tile, 16 or 32 bytes.
+__device__ __forceinline__ void store_outputs(const PrefillParams& p, const ScanSmem& s, int b, int h, int jt, int t0,
+                                              int n, int tid) {
+  const int pos = tid >> 2, c8 = (tid & 3) * 8;
+  if (pos >= n) return;
+  const f4 y0 = *reinterpret_cast<const f4*>(&s.y[pos][c8]);
+  const f4 y1 = *reinterpret_cast<const f4*>(&s.y[pos][c8 + 4]);
+  const size_t oi = (((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + c8;
+  if (p.o_bf16) {
+    bf8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = (__bf16)y0[e];
+      v[4 + e] = (__bf16)y1[e];
+    }
+    *reinterpret_cast<bf8*>(static_cast<__bf16*>(p.o) + oi) = v;
+  } else {
+    *reinterpret_cast<f4*>(static_cast<float*>(p.o) + oi) = y0;
+    *reinterpret_cast<f4*>(static_cast<float*>(p.o) + oi + 4) = y1;
+  }
+}
 
 // One chunk's operands of one wave, in registers.
 struct ChunkIn {
@@ -512,36 +536,53 @@ struct ChunkIn {
   float gam;      // e^G63
 };
 
-__device__ __forceinline__ void load_chunk(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
-                                           int lane, ChunkIn& in) {
+// Part PART of one chunk's operands: 0 Q and the gate factors, 1 W, 2 M and U, 3 K^T.
+// The parts are issued at different points of a chunk so that the memory pipeline is
+// fed evenly and the wave is never held at a long run of loads.
+template <int PART>
+__device__ __forceinline__ void load_part(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
+                                          int lane, ChunkIn& in) {
   const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
   const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-  const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
-  const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
-  const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
-  const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
+  if (PART == 0) {
+    const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    in.q[ks] = *reinterpret_cast<const bf8*>(q + (wave * 4 + ks) * kFrag);
-    in.w[ks] = *reinterpret_cast<const bf8*>(w + (wave * 4 + ks) * kFrag);
+    for (int ks = 0; ks < 4; ++ks) in.q[ks] = *reinterpret_cast<const bf8*>(q + (wave * 4 + ks) * kFrag);
+    const float* gg = p.ws_g + hc * kGStride + 16 * wave + 4 * (lane >> 4);
+    in.eg = *reinterpret_cast<const f4*>(gg);
+    in.egr = *reinterpret_cast<const f4*>(gg + 64);
+    in.gam = p.ws_g[hc * kGStride + 128];
+  } else if (PART == 1) {
+    const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) in.w[ks] = *reinterpret_cast<const bf8*>(w + (wave * 4 + ks) * kFrag);
+  } else if (PART == 2) {
+    const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) in.m[i][j] = *reinterpret_cast<const bf8*>(m + ((wave * 2 + i) * 2 + j) * kFrag);
+    const float* u = p.ws_u + hc * kChunkElems + lane * 4;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) in.u[ct] = *reinterpret_cast<const f4*>(u + ((2 * jt + ct) * 4 + wave) * 256);
+  } else {
+    const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) in.kt[i][j] = *reinterpret_cast<const bf8*>(kt + ((2 * wave + i) * 2 + j) * kFrag);
   }
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      in.kt[i][j] = *reinterpret_cast<const bf8*>(kt + ((2 * wave + i) * 2 + j) * kFrag);
-      in.m[i][j] = *reinterpret_cast<const bf8*>(m + ((wave * 2 + i) * 2 + j) * kFrag);
-    }
-  const float* u = p.ws_u + hc * kChunkElems + lane * 4;
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) in.u[ct] = *reinterpret_cast<const f4*>(u + ((2 * jt + ct) * 4 + wave) * 256);
-  const float* gg = p.ws_g + hc * kGStride + 16 * wave + 4 * (lane >> 4);
-  in.eg = *reinterpret_cast<const f4*>(gg);
-  in.egr = *reinterpret_cast<const f4*>(gg + 64);
-  in.gam = p.ws_g[hc * kGStride + 128];
 }
 
-// One chunk: uses `in`, loads chunk c + 1 (the last chunk again at the end) into `nx`.
+__device__ __forceinline__ void load_chunk(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
+                                           int lane, ChunkIn& in) {
+  load_part<0>(p, b, g, h, jt, c, wave, lane, in);
+  load_part<1>(p, b, g, h, jt, c, wave, lane, in);
+  load_part<2>(p, b, g, h, jt, c, wave, lane, in);
+  load_part<3>(p, b, g, h, jt, c, wave, lane, in);
+}
+
+// One chunk: uses `in`, loads chunk c + 2 (the last chunk again at the end) into `nx`.
 __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, f4 (&S)[2][2], const ChunkIn& in,
                                            ChunkIn& nx, int b, int g, int h, int jt, int c, int wave, int lane) {
   const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
@@ -552,7 +593,11 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
     for (int ct = 0; ct < 2; ++ct)
       *reinterpret_cast<bf4*>(&s.st[16 * ct + fr][32 * wave + 16 * rt + fq]) = to_bf4(S[rt][ct]);
   __syncthreads();
-  load_chunk(p, b, g, h, jt, min(c + 1, p.nC - 1), wave, lane, nx);
+  const int cn = min(c + 2, p.nC - 1);
+  load_part<0>(p, b, g, h, jt, cn, wave, lane, nx);
+  __builtin_amdgcn_sched_barrier(0);
+  // the previous chunk's outputs (staged before this chunk's first barrier)
+  if (c > 0) store_outputs(p, s, b, h, jt, (c - 1) * kC, kC, threadIdx.x);
 
   // P = W S, QS = Q S (wave w: positions 16w..); V' = U - P
   f4 QS[2];
@@ -571,12 +616,17 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
     *reinterpret_cast<bf4*>(&s.vh[16 * ct + fr][16 * wave + fq]) = hi;
     *reinterpret_cast<bf4*>(&s.vl[16 * ct + fr][16 * wave + fq]) = to_bf4(vpr - from_bf4(hi));
     *reinterpret_cast<bf4*>(&s.vp[16 * ct + fr][16 * wave + fq]) = to_bf4(in.egr * vpr);
+    if (ct == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_part<1>(p, b, g, h, jt, cn, wave, lane, nx);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __syncthreads();
+  load_part<2>(p, b, g, h, jt, cn, wave, lane, nx);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // y = e^G . QS + M V' (split operands)
-  const int t0 = c * kC;
-  const int n = min(kC, p.T - t0);
+  // y = e^G . QS + M V' (split operands), staged in LDS
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -589,21 +639,13 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
       acc = mfma(in.m[ks][0], bl, acc);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pos = 16 * wave + fq + e;
-      if (pos < n) {
-        const float y = in.eg[e] * QS[ct][e] + acc[e];
-        const size_t oi = (((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + 16 * ct + fr;
-        if (p.o_bf16) {
-          static_cast<uint16_t*>(p.o)[oi] = f2bf(y);
-        } else {
-          static_cast<float*>(p.o)[oi] = y;
-        }
-      }
-    }
+    for (int e = 0; e < 4; ++e) s.y[16 * wave + fq + e][16 * ct + fr] = in.eg[e] * QS[ct][e] + acc[e];
   }
 
   // S = e^G63 S + K^T (e^(G63-G) V')
+  __builtin_amdgcn_sched_barrier(0);
+  load_part<3>(p, b, g, h, jt, cn, wave, lane, nx);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
@@ -617,8 +659,13 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
 
 __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) ScanSmem s;
-  const int jt = blockIdx.x % (kD / kDt);
-  const int rest = blockIdx.x / (kD / kDt);
+  // Workgroups are dispatched to the 8 XCDs round robin (bid % 8); renumber them so that
+  // each XCD gets a contiguous range of (batch, v-head, tile) -- whole k-head groups when
+  // the count divides -- and the chunk operands they share are fetched into one L2.
+  int bid = blockIdx.x;
+  if (gridDim.x % 8 == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int jt = bid % (kD / kDt);
+  const int rest = bid / (kD / kDt);
   const int h = rest % p.Hv;
   const int b = rest / p.Hv;
   const int g = h / p.rep;
@@ -639,12 +686,32 @@ __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p)
       }
     }
 
-  ChunkIn A, B;
+  // Operands are loaded two chunks ahead of their use (memory latency under this load
+  // is longer than one chunk's work), in three register sets that rotate. The loop body
+  // is three unconditional chunks and is only reached through three peeled ones, so it
+  // is entered with the same loads in flight, in the same registers, as at its back
+  // edge: the waits for a chunk's operands then never cover the loads issued after them.
+  ChunkIn A, B, C;
   load_chunk(p, b, g, h, jt, 0, wave, lane, A);
-  for (int c = 0; c < p.nC; c += 2) {
-    scan_chunk(p, s, S, A, B, b, g, h, jt, c, wave, lane);
+  load_chunk(p, b, g, h, jt, min(1, p.nC - 1), wave, lane, B);
+  if (p.nC < 3) {
+    scan_chunk(p, s, S, A, C, b, g, h, jt, 0, wave, lane);
+    if (p.nC > 1) scan_chunk(p, s, S, B, A, b, g, h, jt, 1, wave, lane);
+  } else {
+    scan_chunk(p, s, S, A, C, b, g, h, jt, 0, wave, lane);
+    scan_chunk(p, s, S, B, A, b, g, h, jt, 1, wave, lane);
+    scan_chunk(p, s, S, C, B, b, g, h, jt, 2, wave, lane);
+    int c = 3;
+    for (; c + 3 <= p.nC; c += 3) {
+      scan_chunk(p, s, S, A, C, b, g, h, jt, c, wave, lane);
+      scan_chunk(p, s, S, B, A, b, g, h, jt, c + 1, wave, lane);
+      scan_chunk(p, s, S, C, B, b, g, h, jt, c + 2, wave, lane);
+    }
+    if (c < p.nC) scan_chunk(p, s, S, A, C, b, g, h, jt, c, wave, lane);
     if (c + 1 < p.nC) scan_chunk(p, s, S, B, A, b, g, h, jt, c + 1, wave, lane);
   }
+  __syncthreads();
+  store_outputs(p, s, b, h, jt, (p.nC - 1) * kC, p.T - (p.nC - 1) * kC, threadIdx.x);
 
   if (p.state_out) {
     float* sout = p.state_out + ((size_t)b * p.Hv + h) * kD * kD;
