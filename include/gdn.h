@@ -134,8 +134,9 @@ int gdn_run(const gdn_layer_args* args);
  * need no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);
 
-/* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len and head
- * counts (the other fields are not read). */
+/* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
+ * counts and front end (the conv front end stages its bf16 q, k, v in the workspace); the
+ * other fields are not read. */
 int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {

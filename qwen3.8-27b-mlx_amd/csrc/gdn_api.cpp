@@ -16,7 +16,7 @@
 
 namespace gdn {
 int recurrent_tile_rows();
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv);
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv);
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream);
 }  // namespace gdn
 
@@ -263,7 +263,8 @@ int gdn_prefill_workspace_size(const gdn_layer_args* a, size_t* bytes) {
   if (!a || !bytes) return fail(GDN_EINVAL, "gdn_prefill_workspace_size: NULL argument");
   if (a->batch < 0 || a->seq_len < 0 || a->num_k_heads < 1 || a->num_v_heads < 1)
     return fail(GDN_EINVAL, "gdn_prefill_workspace_size: bad shape");
-  *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
+  *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads,
+                                        a->frontend == GDN_FRONTEND_CONV);
   return ok();
 }
 
@@ -277,7 +278,8 @@ int gdn_prefill_chunked(const gdn_layer_args* a) {
     return fail(GDN_EINVAL, "gdn_prefill_chunked: x and conv_state_in must be 16-byte aligned");
   if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16)))
     return fail(GDN_EINVAL, "gdn_prefill_chunked: q and k must be 16-byte aligned");
-  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
+  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads,
+                                                   a->num_v_heads, a->frontend == GDN_FRONTEND_CONV);
   if (a->seq_len > 0) {
     if (!a->workspace || a->workspace_bytes < need)
       return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace of %zu bytes required (got %zu)", need,

@@ -155,18 +155,36 @@ struct IntraSmem {
   } u;
 };
 
-// q (waves 0, 1) or k (waves 2, 3) of k-head g into LDS: conv + SiLU + l2norm, bf16
-// after every op (model.cpp:585-602). Lane l: positions 32 (wave & 1) + 8 (l / 16) .. +7,
-// channels {4m .. 4m+3} and {64+4m .. 64+4m+3}, m = l % 16. The l2norm sum keeps the
-// butterfly order of a wave that holds channels (L, L+64) in lane L: lane m adds its
+// ============================================================================ front end
+
+constexpr int kFePos = 32;   // positions per front-end workgroup
+constexpr int kFeHeads = 4;  // heads of 128 channels per front-end workgroup (one per wave)
+
+// Conv + SiLU, and l2norm for q and k (q also scaled by 128^-0.5), bf16 after every op
+// (model.cpp:585-602), into bf16 q (B,T,Hk,128), k (B,T,Hk,128), v (B,T,Hv,128).
+// Workgroup: (batch, 32 positions, 4 of the 2 Hk + Hv heads in channel order q, k, v);
+// wave w takes one head; lane l takes positions 8 (l / 16) .. +7 of the block and the
+// head's channels {4m .. 4m+3} and {64+4m .. 64+4m+3}, m = l % 16. The l2norm sum keeps
+// the butterfly order of a wave that holds channels (L, L+64) in lane L: lane m adds its
 // four pairs as ((p0 + p1) + (p2 + p3)) (the first two butterfly steps), then the DPP
-// row sum does the remaining four.
-__device__ __forceinline__ void qk_frontend(const PrefillParams& p, IntraSmem& s, int b, int g, int t0, int n,
-                                            int wave, int lane) {
-  const int part = wave >> 1;
+// row sum does the remaining four. The workgroup holding position T-1 also writes the
+// conv state hand-off (rows T-3..T-1 of [conv_in ; x]) for its heads.
+__global__ __launch_bounds__(kThreads) void prefill_frontend_kernel(PrefillParams p) {
+  const int nheads = 2 * p.Hk + p.Hv;
+  const int hgroups = (nheads + kFeHeads - 1) / kFeHeads;
+  const int pblocks = (p.T + kFePos - 1) / kFePos;
+  int bid = blockIdx.x;
+  const int hg = bid % hgroups;
+  bid /= hgroups;
+  const int pb = bid % pblocks;
+  const int b = bid / pblocks;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = hg * kFeHeads + wave;
+  if (hh >= nheads) return;  // whole waves; the kernel has no barriers
   const int m = lane & 15;
-  const int p0 = (wave & 1) * 32 + 8 * (lane >> 4);
-  const int c0 = part * p.Hk * kD + g * kD + 4 * m;
+  const int p0 = pb * kFePos + 8 * (lane >> 4);
+  const int c0 = hh * kD + 4 * m;
   const int c1 = c0 + 64;
   float w0[4][kTaps], w1[4][kTaps];
 #pragma unroll
@@ -182,68 +200,64 @@ __device__ __forceinline__ void qk_frontend(const PrefillParams& p, IntraSmem& s
   u16x4 r0[8 + kConvRows], r1[8 + kConvRows];
 #pragma unroll
   for (int i = 0; i < 8 + kConvRows; ++i) {
-    r0[i] = xp_vec4(p, b, t0 + p0 - kConvRows + i, c0);
-    r1[i] = xp_vec4(p, b, t0 + p0 - kConvRows + i, c1);
+    r0[i] = xp_vec4(p, b, p0 - kConvRows + i, c0);
+    r1[i] = xp_vec4(p, b, p0 - kConvRows + i, c1);
   }
-  __bf16(*dst)[kD + kPadB] = part == 0 ? s.u.fe.q : s.u.fe.k;
+  const bool norm = hh < 2 * p.Hk;
+  const bool is_q = hh < p.Hk;
+  __bf16* dst;
+  size_t pstride;
+  if (is_q) {
+    dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
+    pstride = (size_t)p.Hk * kD;
+  } else if (norm) {
+    dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
+    pstride = (size_t)p.Hk * kD;
+  } else {
+    dst = const_cast<__bf16*>(p.v) + ((size_t)b * p.T * p.Hv + (hh - 2 * p.Hk)) * kD;
+    pstride = (size_t)p.Hv * kD;
+  }
   const float scale_b = rbf(1.0f / sqrtf((float)kD));
   const float eps_b = rbf(1e-6f);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    float u0[4], u1[4];
+    float u[8];  // channels 4m + e (e < 4) and 64 + 4m + (e - 4)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      u0[e] = silu_bf(conv4_rows(bf2f(r0[t][e]), bf2f(r0[t + 1][e]), bf2f(r0[t + 2][e]), bf2f(r0[t + 3][e]), w0[e]));
-      u1[e] = silu_bf(conv4_rows(bf2f(r1[t][e]), bf2f(r1[t + 1][e]), bf2f(r1[t + 2][e]), bf2f(r1[t + 3][e]), w1[e]));
+      u[e] = conv4_rows(bf2f(r0[t][e]), bf2f(r0[t + 1][e]), bf2f(r0[t + 2][e]), bf2f(r0[t + 3][e]), w0[e]);
+      u[4 + e] = conv4_rows(bf2f(r1[t][e]), bf2f(r1[t + 1][e]), bf2f(r1[t + 2][e]), bf2f(r1[t + 3][e]), w1[e]);
     }
-    float pr[4];
+    silu_bf_batch(u);
+    f4 y0 = {u[0], u[1], u[2], u[3]}, y1 = {u[4], u[5], u[6], u[7]};
+    if (norm) {
+      float pr[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pr[e] = rbf(u0[e] * u0[e]) + rbf(u1[e] * u1[e]);
-    const float ssum = rbf(row16_sum((pr[0] + pr[1]) + (pr[2] + pr[3])));
-    const float den = rbf(ssum + eps_b);
-    const float rs = rbf(1.0f / sqrtf(den));
-    f4 y0, y1;
+      for (int e = 0; e < 4; ++e) pr[e] = rbf(u[e] * u[e]) + rbf(u[4 + e] * u[4 + e]);
+      const float ssum = rbf(row16_sum((pr[0] + pr[1]) + (pr[2] + pr[3])));
+      const float den = rbf(ssum + eps_b);
+      const float rs = rbf(1.0f / sqrtf(den));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y0[e] = rbf(u0[e] * rs);
-      y1[e] = rbf(u1[e] * rs);
-      if (part == 0) {
-        y0[e] = rbf(y0[e] * scale_b);
-        y1[e] = rbf(y1[e] * scale_b);
+      for (int e = 0; e < 4; ++e) {
+        y0[e] = rbf(y0[e] * rs);
+        y1[e] = rbf(y1[e] * rs);
+        if (is_q) {
+          y0[e] = rbf(y0[e] * scale_b);
+          y1[e] = rbf(y1[e] * scale_b);
+        }
       }
     }
     const int pos = p0 + t;
-    if (pos >= n) {
-      y0 = f4{0.f, 0.f, 0.f, 0.f};
-      y1 = y0;
+    if (pos < p.T) {
+      __bf16* o = dst + (size_t)pos * pstride;
+      *reinterpret_cast<bf4*>(o + 4 * m) = to_bf4(y0);
+      *reinterpret_cast<bf4*>(o + 64 + 4 * m) = to_bf4(y1);
     }
-    *reinterpret_cast<bf4*>(&dst[pos][4 * m]) = to_bf4(y0);
-    *reinterpret_cast<bf4*>(&dst[pos][64 + 4 * m]) = to_bf4(y1);
   }
-}
-
-// v of v-head h into LDS as V^T [dv][pos]: conv + SiLU (model.cpp:585-595). Thread t:
-// channel t % 128, positions 32 (t / 128) .. +31.
-__device__ __forceinline__ void v_frontend(const PrefillParams& p, IntraSmem& s, int b, int h, int t0, int n,
-                                           int tid) {
-  const int dv = tid & (kD - 1), ph = (tid >> 7) * 32;
-  const int ch = 2 * p.Hk * kD + h * kD + dv;
-  float w[kTaps];
-#pragma unroll
-  for (int j = 0; j < kTaps; ++j) w[j] = bf2f(p.conv_w[(size_t)j * p.C + ch]);
-  uint16_t xr[32 + kConvRows];
-#pragma unroll
-  for (int i = 0; i < 32 + kConvRows; ++i) xr[i] = xp_row(p, b, t0 + ph - kConvRows + i, ch);
-#pragma unroll
-  for (int q8 = 0; q8 < 4; ++q8) {
-    bf8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int t = 8 * q8 + e;
-      const float y = silu_bf(conv4_rows(bf2f(xr[t]), bf2f(xr[t + 1]), bf2f(xr[t + 2]), bf2f(xr[t + 3]), w));
-      v[e] = (__bf16)(ph + t < n ? y : 0.0f);
+  if (p.conv_out && pb == pblocks - 1) {
+    for (int e = lane; e < kConvRows * kD; e += 64) {
+      const int r = e / kD, ch = hh * kD + e % kD;
+      p.conv_out[((size_t)b * kConvRows + r) * p.C + ch] = xp_row(p, b, p.T - kConvRows + r, ch);
     }
-    *reinterpret_cast<bf8*>(&s.u.pr.vt[dv][ph + 8 * q8]) = v;
   }
 }
 
@@ -265,9 +279,10 @@ __device__ __forceinline__ void invert_column(const float (*nat)[kC + 4], int j,
   }
 }
 
-// FE: 1 conv front end, 0 given q, k, v. ONE_GROUP: the k-head has at most kGroup v-heads
-// (the K K^T / Q K^T registers are then dead after the first group).
-template <int FE, bool ONE_GROUP>
+// q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output.
+// ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
+// dead after the first group).
+template <bool ONE_GROUP>
 __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) IntraSmem s;
   const int c = blockIdx.x % p.nC;
@@ -281,32 +296,23 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   const int fr = lane & 15, fk = (lane >> 4) * 8, lg = lane >> 4;
   const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
 
-  // ---- q, k of the chunk into LDS (bf16) ----
-  if (FE == 1) {
-    qk_frontend(p, s, b, g, t0, n, wave, lane);
-    // the conv state hand-off: rows T-3..T-1 of [conv_in ; x], written by the last
-    // chunk's workgroup of each k-head for its q, k and v channels
-    if (p.conv_out && c == p.nC - 1) {
-      const int nch = 2 * kD + p.rep * kD;
-      for (int e = tid; e < nch * kConvRows; e += kThreads) {
-        const int r = e / nch, cc = e % nch;
-        const int ch = cc < kD ? g * kD + cc
-                     : cc < 2 * kD ? p.Hk * kD + g * kD + (cc - kD)
-                                   : 2 * p.Hk * kD + g * p.rep * kD + (cc - 2 * kD);
-        p.conv_out[((size_t)b * kConvRows + r) * p.C + ch] = xp_row(p, b, p.T - kConvRows + r, ch);
-      }
+  // ---- q, k of the chunk into LDS (bf16); rows past the end read the last row and are
+  // zeroed, so all eight loads are in flight together ----
+  {
+    constexpr int kIt = kC * kD / 8 / kThreads;
+    bf8 qv[kIt], kv[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+      const size_t gi = (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8;
+      qv[it] = *reinterpret_cast<const bf8*>(p.q + gi);
+      kv[it] = *reinterpret_cast<const bf8*>(p.k + gi);
     }
-  } else {
-    for (int e = tid; e < kC * kD / 8; e += kThreads) {
-      const int pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      bf8 qv = {}, kv = {};
-      if (pos < n) {
-        const size_t gi = (((size_t)b * p.T + t0 + pos) * p.Hk + g) * kD + d8;
-        qv = *reinterpret_cast<const bf8*>(p.q + gi);
-        kv = *reinterpret_cast<const bf8*>(p.k + gi);
-      }
-      *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = qv;
-      *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = kv;
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+      *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
+      *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = pos < n ? kv[it] : bf8{};
     }
   }
   __syncthreads();
@@ -424,9 +430,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     for (int r = 0; r < gs; ++r) {
       const int h = g * p.rep + r0 + r;
       const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-      if (FE == 1) {
-        v_frontend(p, s, b, h, t0, n, tid);
-      } else {
+      {
         const int dv = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
         for (int q8 = 0; q8 < 4; ++q8) {
@@ -724,10 +728,11 @@ __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p)
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, w, m, u, g, total;
+  size_t q, kt, w, m, u, g, fq, fk, fv, total;
 };
 
-WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv) {
+// conv: the conv front end's bf16 q, k, v (B,T,H,128) are staged in the workspace too.
+WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
@@ -741,13 +746,20 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv) {
   L.m = L.w + wm;
   L.u = L.m + wm;
   L.g = L.u + uu;
-  L.total = L.g + gg;
+  const size_t fqk = conv ? al((size_t)B * T * Hk * kD * 2) : 0;
+  const size_t fv = conv ? al((size_t)B * T * Hv * kD * 2) : 0;
+  L.fq = L.g + gg;
+  L.fk = L.fq + fqk;
+  L.fv = L.fk + fqk;
+  L.total = L.fv + fv;
   return L;
 }
 
 }  // namespace
 
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv) { return workspace_layout(B, T, Hk, Hv).total; }
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv) {
+  return workspace_layout(B, T, Hk, Hv, conv).total;
+}
 
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream) {
   PrefillParams p{};
@@ -776,7 +788,8 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.state_in = a.state_in;
   p.state_out = a.state_out;
   p.o = a.o;
-  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv);
+  const bool conv = a.frontend == GDN_FRONTEND_CONV;
+  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv, conv);
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
@@ -784,17 +797,24 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
   p.ws_u = reinterpret_cast<float*>(w + L.u);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
+  if (conv) {
+    p.q = reinterpret_cast<const __bf16*>(w + L.fq);
+    p.k = reinterpret_cast<const __bf16*>(w + L.fk);
+    p.v = reinterpret_cast<const __bf16*>(w + L.fv);
+  }
 
   const dim3 block(kThreads);
   const dim3 g1((unsigned)((size_t)p.B * p.Hk * p.nC));
   const dim3 g2((unsigned)((size_t)p.B * p.Hv * (kD / kDt)));
-  const bool one = p.rep <= kGroup;
-  if (a.frontend == GDN_FRONTEND_CONV) {
-    if (one) hipLaunchKernelGGL((prefill_intra_kernel<1, true>), g1, block, 0, stream, p);
-    else hipLaunchKernelGGL((prefill_intra_kernel<1, false>), g1, block, 0, stream, p);
+  if (conv) {
+    const size_t nh = ((size_t)2 * p.Hk + p.Hv + kFeHeads - 1) / kFeHeads;
+    const dim3 g0((unsigned)((size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
+    hipLaunchKernelGGL(prefill_frontend_kernel, g0, block, 0, stream, p);
+  }
+  if (p.rep <= kGroup) {
+    hipLaunchKernelGGL((prefill_intra_kernel<true>), g1, block, 0, stream, p);
   } else {
-    if (one) hipLaunchKernelGGL((prefill_intra_kernel<0, true>), g1, block, 0, stream, p);
-    else hipLaunchKernelGGL((prefill_intra_kernel<0, false>), g1, block, 0, stream, p);
+    hipLaunchKernelGGL((prefill_intra_kernel<false>), g1, block, 0, stream, p);
   }
   hipLaunchKernelGGL(prefill_scan_kernel, g2, block, 0, stream, p);
   return hipGetLastError();

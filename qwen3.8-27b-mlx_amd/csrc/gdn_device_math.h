@@ -115,6 +115,37 @@ __device__ __forceinline__ float silu_bf(float y) {
   return rbf(y * sg);
 }
 
+// silu_bf for N bf16 values at once, bit-identical to silu_bf on every bf16 input. The
+// hardware 2^x and reciprocal give sigmoid(y) within 0.83 (5 + |y|) ulp of d_sigmoidf(y)
+// on every bf16 y >= -60 (all 65536 inputs checked on the device); when that fast value
+// lies more than 16 + 2|y| ulp from a bf16 rounding midpoint (bits 0x8000 of its low
+// half), both round to the same bf16. Other values -- near a midpoint, y < -60, NaN,
+// about 0.1% of inputs with |y| < 10 -- take the exact path, in one branch per batch
+// so that the fast paths of the batch interleave.
+template <int N>
+__device__ __forceinline__ void silu_bf_batch(float (&y)[N]) {
+  float sg[N];
+  uint32_t ok_mask = 0;  // bitwise, not short-circuit: the checks stay straight-line code
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float ex = __builtin_amdgcn_exp2f(-y[e] * 1.44269504088896341f);
+    const float s = __builtin_amdgcn_rcpf(1.0f + ex);
+    const int lo = (int)(f_bits(s) & 0xffffu) - 0x8000;
+    const float dist = (float)(lo < 0 ? -lo : lo);
+    const uint32_t ok = (uint32_t)(y[e] >= -60.0f) & (uint32_t)(dist > 16.0f + 2.0f * __builtin_fabsf(y[e]));
+    sg[e] = rbf(s);
+    ok_mask |= ok << e;
+  }
+  if (__builtin_expect(ok_mask != (1u << N) - 1u, 0)) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      if (!((ok_mask >> e) & 1u)) sg[e] = rbf(d_sigmoidf(y[e]));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) y[e] = rbf(y[e] * sg[e]);
+}
+
 // Sum over the 16 lanes of a DPP row; every lane receives the same total.
 // quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror. When lane m of
 // the row holds the partial sum of group m, this is the butterfly p[m] += p[m ^ s],

@@ -129,8 +129,10 @@ def call_commit(args: CommitArgs) -> None:
     _check(lib().gdn_commit(ctypes.byref(args)))
 
 
-def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48) -> int:
-    args = LayerArgs(n_layers=1, batch=B, seq_len=T, num_k_heads=Hk, num_v_heads=Hv)
+def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48, conv: bool = True) -> int:
+    """Workspace bytes of gdn_prefill_chunked; `conv` for the conv front end (x given)."""
+    args = LayerArgs(n_layers=1, batch=B, seq_len=T, num_k_heads=Hk, num_v_heads=Hv,
+                     frontend=FRONTEND_CONV if conv else FRONTEND_QKV)
     out = ctypes.c_size_t(0)
     _check(lib().gdn_prefill_workspace_size(ctypes.byref(args), ctypes.byref(out)))
     return out.value
@@ -274,7 +276,8 @@ def prefill_chunked(*, x=None, q=None, k=None, v=None, a=None, b=None, A_log=Non
     conv_out = (torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
                 if x is not None else None)
     if workspace is None and T > 0:
-        workspace = torch.empty(prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device=dev)
+        workspace = torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None),
+                                dtype=torch.uint8, device=dev)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
                       A_log=A_log, dt_bias=dt_bias, alpha=alpha, beta=beta, state_in=state,

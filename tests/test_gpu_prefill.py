@@ -119,3 +119,47 @@ def test_prefill_then_decode_continues(O, gdn, dev):
     torch.cuda.synchronize()
     check(O, to_np(out["o"]), ref["o"][:, 130:], "decode o after prefill")
     check(O, to_np(out["state"]), ref["state"], "state after prefill + decode")
+
+
+def _from_fragments(blocks, rows: int, cols: int):
+    """A matrix stored in MFMA A-fragment order -- 16 x 32 blocks, row block major; in a
+    block, lane l = 16 lg + fr holds row fr, columns 8 lg .. 8 lg + 7 -- to row-major."""
+    lead = blocks.shape[:-1]
+    a = blocks.reshape(*lead, rows // 16, cols // 32, 4, 16, 8)   # [rt][ks][lg][fr][i]
+    nd = a.ndim
+    a = np.moveaxis(a, nd - 2, nd - 4)                              # [rt][fr][ks][lg][i]
+    return a.reshape(*lead, rows, cols)
+
+
+def test_prefill_frontend_is_bit_exact(O, gdn, dev):
+    """The prefill's own conv + SiLU + l2norm front end (fast SiLU with exact fallback)
+    against the oracle's, bit for bit: Q and K^T as the intra-chunk kernel leaves them in
+    the workspace (Q at offset 0, K^T after it, one 64 x 128 block per (b, k-head, chunk)
+    in fragment order). B=2, a conv state carried in, T=200 (last chunk partial)."""
+    import torch
+    log_case("prefill front end bits B=2 T=200 with conv state")
+    B, T, Hk, Hv = 2, 200, 16, 48
+    inp = O.make_inputs(config=4, layer=99, B=B, L=T, conv=True, state_std=0.05)
+    q_ref, k_ref, _, _ = O.conv_frontend(inp.x, inp.conv_state, inp.conv_w, Hk, Hv)
+    nC = (T + 63) // 64
+    ws = torch.empty(gdn.prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device=dev)
+    run_kw = dict(x=to_dev(inp.x, dev), conv_weight=to_dev(inp.conv_w, dev),
+                  conv_state=to_dev(inp.conv_state, dev), a=to_dev(inp.a, dev), b=to_dev(inp.b, dev),
+                  A_log=to_dev(inp.A_log, dev), dt_bias=to_dev(inp.dt_bias, dev),
+                  state=to_dev(inp.state, dev), Hk=Hk, Hv=Hv, workspace=ws)
+    gdn.prefill_chunked(**run_kw)
+    torch.cuda.synchronize()
+    raw = to_np(ws).view(np.uint16)
+    plane = B * Hk * nC * 8192
+    kt_off = -(-plane * 2 // 256) * 256 // 2
+    wq = _from_fragments(raw[:plane].reshape(B, Hk, nC, 8192), 64, 128)         # [b][g][c][pos][dk]
+    wkt = _from_fragments(raw[kt_off:kt_off + plane].reshape(B, Hk, nC, 8192), 128, 64)  # [b][g][c][dk][pos]
+    qr = np.zeros((B, nC * 64, Hk, 128), np.uint16)
+    kr = np.zeros((B, nC * 64, Hk, 128), np.uint16)
+    qr[:, :T] = q_ref.view(np.uint16)
+    kr[:, :T] = k_ref.view(np.uint16)
+    q_got = wq.transpose(0, 2, 3, 1, 4).reshape(B, nC * 64, Hk, 128)
+    k_got = wkt.transpose(0, 2, 4, 1, 3).reshape(B, nC * 64, Hk, 128)
+    print(f"  q mismatches {(q_got != qr).sum()}, k mismatches {(k_got != kr).sum()}", flush=True)
+    assert np.array_equal(q_got, qr)
+    assert np.array_equal(k_got, kr)
