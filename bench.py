@@ -140,9 +140,8 @@ class Timer:
 
 
 def bench_decode(torch, gdn, dev, timer, B: int, conv: bool, steps: int, warmup: int,
-                 sets: int):
-    """48-layer decode step, rotating over `sets` independent state sets."""
-    NL = 48
+                 sets: int, NL: int = 48):
+    """NL-layer decode step, rotating over `sets` independent state sets."""
     inps = [make_layer_inputs(torch, dev, NL, B, 1, conv, seed=100 + s) for s in range(sets)]
     states = []
     for s in range(sets):
@@ -225,6 +224,43 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
                 intra_flop=intra, inter_flop=inter)
 
 
+def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str):
+    """48 layers of the DeltaNet projections at B=1 in one launch: "in_proj" = in_proj_qkv,
+    in_proj_z, in_proj_a, in_proj_b on x (5120); "out_proj" = GatedRMSNorm of o (6144,
+    fp32) with z, then out_proj (5120 rows). Synthetic 4-bit weights (random words, scales
+    and biases in the checkpoint's ranges)."""
+    NL = 48
+    g = torch.Generator(device=dev)
+    g.manual_seed(700 if which == "in_proj" else 701)
+
+    def mat(n, k):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (NL, n, k // 8), dtype=torch.int32, device=dev, generator=g)
+        sc = (torch.rand((NL, n, k // 64), device=dev, generator=g) * 0.03 + 0.002).to(torch.bfloat16)
+        bi = ((torch.rand((NL, n, k // 64), device=dev, generator=g) - 0.5) * 0.4).to(torch.bfloat16)
+        return gdn.QuantLinear(w, sc, bi)
+
+    if which == "in_proj":
+        K, ns = 5120, [C, HV * D, HV, HV]
+        mats = [mat(n, K) for n in ns]
+        x = torch.randn((NL, 1, K), device=dev, generator=g).to(torch.bfloat16)
+        args, _ys = gdn.qlinear_args(mats, x, n_layers=NL)
+        operand = K * 2
+    else:
+        K, ns = HV * D, [5120]
+        mats = [mat(n, K) for n in ns]
+        o = torch.randn((NL, 1, K), device=dev, generator=g) * 0.3
+        z = torch.randn((NL, 1, K), device=dev, generator=g).to(torch.bfloat16)
+        gamma = torch.rand((NL, D), device=dev, generator=g) + 0.5
+        args, _ys = gdn.qlinear_args(mats, norm=(o, z, gamma, 1e-6), n_layers=NL)
+        operand = K * 4 + K * 2 + D * 4
+    r = timer.time_calls(lambda it: gdn.call_qlinear(args), steps, warmup)
+    per_layer = sum(n * K // 2 + n * (K // 64) * 4 + n * 2 for n in ns) + operand
+    nbytes = NL * per_layer
+    return dict(GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+                frac_hbm=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                us_per_step=round(r["ms_per_step"] * 1e3, 2), bytes_per_step=nbytes)
+
+
 def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
     """Device-to-device copy of 604 MB: a practical streaming ceiling for comparison."""
     n = 4 * 48 * HV * D * D // 2
@@ -251,10 +287,22 @@ def cpu_baseline(target_seconds: float = 12.0):
         if el >= target_seconds or reps >= 200:
             break
     per_step = el / reps
+    # and on one core, a shorter sample
+    reps1, t0 = 0, time.perf_counter()
+    while True:
+        for inp in inps:
+            O.reference_layer(inp, materialize=True, threads=1)
+        reps1 += 1
+        el1 = time.perf_counter() - t0
+        if el1 >= target_seconds / 3 or reps1 >= 50:
+            break
+    per_step1 = el1 / reps1
     nbytes = 48 * bytes_decode_layer(1, True)
     return dict(value=nbytes / per_step / 1e9, unit="GB/s", cores=threads, kind="port",
                 sample=f"{reps} full 48-layer B=1 decode steps with the conv front end "
-                       f"(oracle, one pass per op, fp32), {per_step * 1e3:.1f} ms per step")
+                       f"(oracle, one pass per op, fp32), {per_step * 1e3:.1f} ms per step",
+                value_1core=nbytes / per_step1 / 1e9,
+                sample_1core=f"{reps1} steps on one thread, {per_step1 * 1e3:.1f} ms per step")
 
 
 def load_traffic(name: str):
@@ -273,7 +321,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list: decode1,decode32,verify,prefill,copy")
+    ap.add_argument("--only", default="",
+                    help="comma list: decode1,decode1layer,decode32,verify,prefill,in_proj,"
+                         "out_proj,copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the gated-delta path "
@@ -298,6 +348,14 @@ def main() -> int:
                             warmup=args.warmup, sets=4)
         print(f"# decode B=1 x48 conv: {head['ms_per_step'] * 1e3:.1f} us/step, "
               f"{head['GBps']:.0f} GB/s", flush=True)
+    if want("decode1layer"):
+        # one layer, B=1, q, k, v given: one launch per step; 96 state sets (302 MB)
+        r = bench_decode(torch, gdn, dev, timer, B=1, conv=False, steps=args.steps,
+                         warmup=args.warmup, sets=96, NL=1)
+        sec["decode_1layer_b1"] = dict(GBps=round(r["GBps"], 1), frac_hbm=round(r["GBps"] / HBM_PEAK_GBPS, 4),
+                                       us_per_step=round(r["ms_per_step"] * 1e3, 2),
+                                       bytes_per_step=r["bytes_per_step"])
+        print(f"# decode 1 layer B=1: {r['ms_per_step'] * 1e3:.2f} us/step, {r['GBps']:.0f} GB/s", flush=True)
     if want("decode32"):
         r = bench_decode(torch, gdn, dev, timer, B=32, conv=False,
                          steps=max(10, args.steps // 10), warmup=3, sets=2)
@@ -316,6 +374,11 @@ def main() -> int:
         sec["prefill_t4096"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         print(f"# prefill T=4096: {r['us_per_call']:.1f} us, {r['tokens_per_s'] / 1e6:.2f} M tok/s, "
               f"intra MFMA frac {r['intra_frac_mfma']:.4f}", flush=True)
+    for which in ("in_proj", "out_proj"):
+        if want(which):
+            r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)
+            sec[f"{which}_48_layers_b1"] = r
+            print(f"# {which} x48 B=1 (4-bit): {r['us_per_step']:.1f} us/step, {r['GBps']:.0f} GB/s", flush=True)
     if want("copy"):
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)

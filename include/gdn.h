@@ -21,6 +21,9 @@
  *                       the call site it drops into is model.cpp:622-624.
  *   gdn_prefill_chunked chunked_delta         python/qwen35.py:365-431
  *   gdn_commit          DeltaCache::commit    cpp/src/model.cpp:439-457
+ *   gdn_qlinear         Linear::operator()    cpp/src/model.cpp:356-372 (quantized), for
+ *                       the layer's in_proj_* and, with GatedRMSNorm::operator()
+ *                       (model.cpp:350-354) in front, its out_proj
  *   gdn_available       delta::available      cpp/src/delta.hpp:51 (delta.cpp:133-135)
  *
  * Conventions
@@ -160,6 +163,44 @@ typedef struct gdn_commit_args {
 
 /* DeltaCache::commit(n): accept the first n tokens of a recorded block. */
 int gdn_commit(const gdn_commit_args* args);
+
+/* ---- quantized linear: the DeltaNet layer's projections ----
+ * y = x W^T with W in the reference's 4-bit affine layout, as Linear::operator() computes
+ * it for quantized weights (cpp/src/model.cpp:356-372: mx::quantized_matmul, transpose
+ * = true, group 64, bits 4; layout python/mlp_kernel.py:54-56): w (N, K/8) uint32 holds 8
+ * values per word, value i in nibble i (low nibble first); element (n, k) = nibble *
+ * scales[n, k/64] + biases[n, k/64]. The result is rounded to bf16 once. Up to
+ * GDN_QLINEAR_MAX_SEGS matrices that read the same operand run in one launch: the
+ * layer's in_proj_qkv, in_proj_z, in_proj_a and in_proj_b (model.cpp:587, 608-609, 626).
+ * With norm_x set, the operand is the layer's GatedRMSNorm of the recurrence output
+ * (model.cpp:350-354, 626-627), bf16(rmsnorm(norm_x) * norm_gamma * silu(norm_z)) over
+ * each 128-value head, so norm + out_proj (model.cpp:641) is one call. */
+#define GDN_QLINEAR_MAX_SEGS 4
+#define GDN_QLINEAR_MAX_ROWS 4
+
+typedef struct gdn_qlinear_seg {
+  const void* w;      /* (N, K/8) uint32, 16-byte aligned */
+  const void* scales; /* (N, K/64) bf16 */
+  const void* biases; /* (N, K/64) bf16 */
+  void* y;            /* (M, N) bf16; must not overlap any input */
+  int n;              /* N >= 1 */
+} gdn_qlinear_seg;
+
+typedef struct gdn_qlinear_args {
+  int n_layers; /* >= 1; layer l of every tensor starts at l times its per-layer size */
+  int m;        /* rows of the operand (B * L), 1 .. GDN_QLINEAR_MAX_ROWS, m * k <= 30720 */
+  int k;        /* in features: 1024, 2048, 4096, 5120, 6144 or 8192 */
+  const void* x; /* (M, K) bf16, 16-byte aligned; NULL when norm_x is set */
+  const float* norm_x;     /* (M, K) fp32 (the recurrence output o), or NULL */
+  const void* norm_z;      /* (M, K) bf16 gate z */
+  const float* norm_gamma; /* (128) fp32 norm weight */
+  float norm_eps;          /* >= 0 */
+  int n_segs;   /* 1 .. GDN_QLINEAR_MAX_SEGS */
+  gdn_qlinear_seg segs[GDN_QLINEAR_MAX_SEGS];
+  void* stream; /* hipStream_t */
+} gdn_qlinear_args;
+
+int gdn_qlinear(const gdn_qlinear_args* args);
 
 /* 1 if the current HIP device is a gfx950 the kernels were built for, else 0. */
 int gdn_available(void);

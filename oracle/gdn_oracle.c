@@ -646,3 +646,46 @@ int gdno_commit(int B, int T, int Hv, int C, int n, const float* states,
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Quantized linear, cpp/src/model.cpp:356-372 (mx::quantized_matmul, transpose = true,
+ * group 64, 4 bits): 8 values per uint32, value i in nibble i, low nibble first
+ * (python/mlp_kernel.py:54-56), element = nibble * scale + bias. */
+
+void gdno_qlinear_f64(int M, int N, int K, const uint16_t* x, const uint32_t* w,
+                      const uint16_t* scales, const uint16_t* biases, double* y) {
+  const int G = K / 64;
+  for (int n = 0; n < N; ++n) {
+    for (int m = 0; m < M; ++m) {
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k) {
+        const uint32_t word = w[(int64_t)n * (K / 8) + k / 8];
+        const double nib = (double)((word >> (4 * (k % 8))) & 0xFu);
+        const double s = gdno_bf16_to_f32(scales[(int64_t)n * G + k / 64]);
+        const double bb = gdno_bf16_to_f32(biases[(int64_t)n * G + k / 64]);
+        acc += (double)gdno_bf16_to_f32(x[(int64_t)m * K + k]) * (nib * s + bb);
+      }
+      y[(int64_t)m * N + n] = acc;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------- */
+/* GatedRMSNorm, cpp/src/model.cpp:350-354: fast::rms_norm in fp32 (x * rsqrt(mean(x^2) +
+ * eps) * w), then times silu(fp32(z)), rounded to the activation dtype (bf16). */
+
+void gdno_gated_rmsnorm(int64_t rows, int dim, const float* o, const uint16_t* z,
+                        const float* gamma, float eps, uint16_t* out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = o + r * dim;
+    float ss = 0.0f;
+    for (int i = 0; i < dim; ++i) ss += x[i] * x[i];
+    const float rs = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = 0; i < dim; ++i) {
+      const float h = x[i] * rs * gamma[i];
+      const float zf = gdno_bf16_to_f32(z[r * dim + i]);
+      const float g = zf * gdno_sigmoidf(zf);
+      out[r * dim + i] = gdno_f32_to_bf16(h * g);
+    }
+  }
+}

@@ -14,6 +14,9 @@
  *   cpp/src/delta.cpp:175-204   delta::run_reference       (per-step op order, collect layout)
  *   python/qwen35.py:350-431    _invert_unit_lower, chunked_delta
  *   python/qwen35.py:434-475    _delta_step, sequential_delta
+ *   cpp/src/model.cpp:356-372   Linear::operator(), quantized branch (mx::quantized_matmul,
+ *                               4-bit affine, group 64; layout python/mlp_kernel.py:54-56)
+ *   cpp/src/model.cpp:350-354   GatedRMSNorm::operator() (normalise, then gate)
  *
  * Conventions: bf16 tensors are passed as uint16 bit patterns; fp32 state is
  * (B, Hv, Dv, Dk) with Dk contiguous; q,k carry Hk heads and v-head h reads k-head
@@ -101,6 +104,19 @@ void gdno_chunked_f32(int B, int L, int Hk, int Hv, int C, const float* q, const
  * Returns 0, or -1 when n is outside [0, T] (the reference throws). */
 int gdno_commit(int B, int T, int Hv, int C, int n, const float* states,
                 const float* S_prev, const uint16_t* xp, float* S_dst, uint16_t* conv_dst);
+
+/* ---- quantized linear, model.cpp:356-372 (mx::quantized_matmul, transpose = true) ----
+ * x (M, K) bf16; w (N, K/8) uint32, value i of a word in nibble i (low nibble first);
+ * scales, biases (N, K/64) bf16; element (n, k) = nibble * scale[n, k/64] + bias[n, k/64].
+ * y (M, N) = x W^T accumulated in fp64 (the reference rounds its result to bf16). */
+void gdno_qlinear_f64(int M, int N, int K, const uint16_t* x, const uint32_t* w,
+                      const uint16_t* scales, const uint16_t* biases, double* y);
+
+/* ---- GatedRMSNorm, model.cpp:350-354 ----
+ * rows of D fp32 values o, bf16 gate z, fp32 gamma (D): h = o * rsqrt(mean(o^2) + eps) * gamma
+ * in fp32 (mx::fast::rms_norm), out = bf16(h * silu(fp32(z))), silu(z) = z * sigmoid(z). */
+void gdno_gated_rmsnorm(int64_t rows, int dim, const float* o, const uint16_t* z,
+                        const float* gamma, float eps, uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,7 @@ def lib() -> ctypes.CDLL:
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -73,6 +74,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gdno_chunked_f32.argtypes = [_int, _int, _int, _int, _int, _f32p, _f32p, _f32p, _f32p,
                                    _f32p, _f32p, _f32p, _f32p, _int]
     L.gdno_commit.argtypes = [_int, _int, _int, _int, _int, _f32p, _f32p, _u16p, _f32p, _u16p]
+    L.gdno_qlinear_f64.argtypes = [_int, _int, _int, _u16p, _u32p, _u16p, _u16p, _f64p]
+    L.gdno_gated_rmsnorm.argtypes = [_i64, _int, _f32p, _u16p, _f32p, ctypes.c_float, _u16p]
     L.gdno_commit.restype = _int
 
 
@@ -218,6 +221,31 @@ def commit(n: int, states, S_prev, xp_bf16):
     if rc != 0:
         raise ValueError("DeltaCache::commit out of range")
     return S_dst, conv
+
+
+def qlinear(x_bf16, w_u32, scales_bf16, biases_bf16):
+    """Linear::operator(), quantized branch (mx::quantized_matmul, 4-bit, group 64):
+    x (M, K) bf16 bits, w (N, K/8) uint32, scales/biases (N, K/64) bf16 bits -> (M, N) fp64."""
+    x, s, b = _u16(x_bf16), _u16(scales_bf16), _u16(biases_bf16)
+    w = np.ascontiguousarray(w_u32, dtype=np.uint32)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape == (N, K // 8) and s.shape == (N, K // 64) and b.shape == (N, K // 64)
+    y = np.empty((M, N), np.float64)
+    lib().gdno_qlinear_f64(M, N, K, _p(x, _u16p), _p(w, _u32p), _p(s, _u16p), _p(b, _u16p),
+                           _p(y, _f64p))
+    return y
+
+
+def gated_rmsnorm(o, z_bf16, gamma, eps: float = 1e-6):
+    """GatedRMSNorm: rows of o (..., D) fp32, z bf16 bits, gamma (D) fp32 -> bf16 bits."""
+    o, z, g = _f32(o), _u16(z_bf16), _f32(gamma)
+    D = o.shape[-1]
+    rows = o.size // D
+    out = np.empty(o.shape, np.uint16)
+    lib().gdno_gated_rmsnorm(rows, D, _p(o, _f32p), _p(z, _u16p), _p(g, _f32p), eps,
+                             _p(out, _u16p))
+    return out
 
 
 # --------------------------------------------------------------------------

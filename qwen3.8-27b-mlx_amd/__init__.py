@@ -4,6 +4,7 @@ from .gdn import (  # noqa: F401
     CONV_TAPS, DTYPE_BF16, DTYPE_F32, EXPORTS, FRONTEND_CONV, FRONTEND_QKV, GATES_PRECOMPUTED,
     GATES_RAW, GDN_EDEVICE, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_OK, HEAD_DIM, LIB_PATH,
     STATES_BHT, STATES_TBH, CommitArgs, DeltaCache, GdnError, LayerArgs, Result, available,
-    call_commit, call_prefill, call_run, commit, last_error, layer, layer_args, lib,
-    prefill_chunked, prefill_workspace_size, run,
+    call_commit, call_prefill, call_qlinear, call_run, commit, last_error, layer, layer_args,
+    lib, prefill_chunked, prefill_workspace_size, qlinear, qlinear_args, QLinearArgs,
+    QLinearSeg, QuantLinear, QLINEAR_MAX_ROWS, QLINEAR_MAX_SEGS, run,
 )

@@ -7,7 +7,7 @@ import subprocess
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libgdn.so")
-SOURCES = ["gdn_api.cpp", "gdn_recurrent.hip", "gdn_commit.hip", "gdn_chunked.hip"]
+SOURCES = ["gdn_api.cpp", "gdn_recurrent.hip", "gdn_commit.hip", "gdn_chunked.hip", "gdn_qlinear.hip"]
 
 # -ffp-contract=off: the bf16 front end must round exactly as written (fma only where
 #   the code asks for it with __builtin_fmaf).

@@ -358,4 +358,63 @@ int gdn_commit(const gdn_commit_args* a) {
   return ok();
 }
 
+int gdn_qlinear(const gdn_qlinear_args* a) {
+  if (!a) return fail(GDN_EINVAL, "gdn_qlinear: args is NULL");
+  if (a->n_layers < 1 || a->m < 1 || a->m > GDN_QLINEAR_MAX_ROWS)
+    return fail(GDN_EINVAL, "gdn_qlinear: bad shape (n_layers=%d m=%d; m must be 1..%d)", a->n_layers, a->m,
+                GDN_QLINEAR_MAX_ROWS);
+  if (!gdn::qlinear_k_supported(a->k))
+    return fail(GDN_EINVAL, "gdn_qlinear: k=%d unsupported (1024, 2048, 4096, 5120, 6144, 8192)", a->k);
+  if (a->n_segs < 1 || a->n_segs > GDN_QLINEAR_MAX_SEGS)
+    return fail(GDN_EINVAL, "gdn_qlinear: n_segs must be 1..%d", GDN_QLINEAR_MAX_SEGS);
+  if ((int64_t)a->m * (a->k / 32) * 68 > 65536)  // the staged operand's LDS
+    return fail(GDN_EINVAL, "gdn_qlinear: m * k too large (m=%d k=%d; m * k <= 30720)", a->m, a->k);
+  const int64_t L = a->n_layers, M = a->m, K = a->k;
+  const bool norm = a->norm_x != nullptr;
+  if (norm == (a->x != nullptr))
+    return fail(GDN_EINVAL, "gdn_qlinear: exactly one of x and norm_x is required");
+  Range in[3];
+  if (norm) {
+    if (!a->norm_z || !a->norm_gamma) return fail(GDN_EINVAL, "gdn_qlinear: the norm needs norm_z and norm_gamma");
+    if (!(a->norm_eps >= 0.0f)) return fail(GDN_EINVAL, "gdn_qlinear: norm_eps must be >= 0");
+    if (!aligned(a->norm_x, 16) || !aligned(a->norm_z, 16) || !aligned(a->norm_gamma, 16))
+      return fail(GDN_EINVAL, "gdn_qlinear: norm_x, norm_z and norm_gamma must be 16-byte aligned");
+    in[0] = range_of(a->norm_x, L * M * K * 4);
+    in[1] = range_of(a->norm_z, L * M * K * 2);
+    in[2] = range_of(a->norm_gamma, L * 128 * 4);
+  } else {
+    if (!aligned(a->x, 16)) return fail(GDN_EINVAL, "gdn_qlinear: x must be 16-byte aligned");
+    in[0] = range_of(a->x, L * M * K * 2);
+  }
+  int64_t rows = 0;
+  for (int i = 0; i < a->n_segs; ++i) {
+    const gdn_qlinear_seg& g = a->segs[i];
+    if (!g.w || !g.scales || !g.biases || !g.y || g.n < 1)
+      return fail(GDN_EINVAL, "gdn_qlinear: segment %d needs w, scales, biases, y and n >= 1", i);
+    if (!aligned(g.w, 16) || !aligned(g.scales, 2) || !aligned(g.biases, 2) || !aligned(g.y, 2))
+      return fail(GDN_EINVAL, "gdn_qlinear: segment %d: w must be 16-byte and scales, biases, y 2-byte aligned", i);
+    rows += g.n;
+  }
+  if (rows * L > (int64_t)1 << 31) return fail(GDN_EINVAL, "gdn_qlinear: too many rows");
+  for (int i = 0; i < a->n_segs; ++i) {
+    const gdn_qlinear_seg& g = a->segs[i];
+    const Range y = range_of(g.y, L * M * g.n * 2);
+    for (const Range& r : in)
+      if (overlap(y, r)) return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap the operand", i);
+    for (int j = 0; j < a->n_segs; ++j) {
+      const gdn_qlinear_seg& h = a->segs[j];
+      if (overlap(y, range_of(h.w, L * h.n * K / 2)) || overlap(y, range_of(h.scales, L * h.n * K / 32)) ||
+          overlap(y, range_of(h.biases, L * h.n * K / 32)))
+        return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap a weight tensor", i);
+      if (j != i && overlap(y, range_of(h.y, L * M * h.n * 2)))
+        return fail(GDN_EINVAL, "gdn_qlinear: outputs of segments %d and %d overlap", i, j);
+    }
+  }
+  int rc = check_device();
+  if (rc != GDN_OK) return rc;
+  hipError_t e = gdn::launch_qlinear(*a, static_cast<hipStream_t>(a->stream));
+  if (e != hipSuccess) return hip_fail(e, "gdn_qlinear launch");
+  return ok();
+}
+
 }  // extern "C"

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/gdn.h"
+
 namespace gdn {
 
 constexpr int kD = 128;     // Dk = Dv
@@ -59,5 +61,9 @@ struct CommitParams {
   uint16_t* conv_dst;
 };
 hipError_t launch_commit(const CommitParams& p, hipStream_t stream);
+
+// Quantized linear (arguments validated by the caller).
+bool qlinear_k_supported(int k);
+hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream);
 
 }  // namespace gdn

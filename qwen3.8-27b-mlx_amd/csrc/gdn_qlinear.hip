@@ -1,0 +1,255 @@
+// Quantized linear for the DeltaNet layer's projections on gfx950: y = x W^T with W in
+// the reference's 4-bit affine layout (cpp/src/model.cpp:356-372, mx::quantized_matmul
+// with transpose = true, group 64; python/mlp_kernel.py:54-56): uint32 words of 8 values,
+// value i in nibble i (low nibble first), element = nibble * scale + bias per group of
+// 64, scales and biases bf16. Up to four matrices that read the same x run in one launch
+// (in_proj_qkv, in_proj_z, in_proj_a, in_proj_b of one layer), and an optional prologue
+// applies the layer's GatedRMSNorm (model.cpp:350-354) to the recurrence output before
+// out_proj, so norm and projection are one launch.
+//
+// HBM-bound at decode (M = B * L rows of x, 1..4): every weight byte is read once.
+// Mapping: a workgroup stages its operand in LDS, then each wave takes 4 output rows at a
+// time, one per 16-lane DPP row; lane m of a row reads the row's 16-byte pieces m, m + 16,
+// m + 32, ... (each 32 nibbles = half a group), so a load instruction reads 4 x 256
+// contiguous bytes. A nibble v becomes the bf16 value 128 + v with one and-or
+// ((w >> 4i) & 0x000F000F | 0x43004300 gives nibbles i and i + 4 of the word as two bf16),
+// v_dot2 multiplies pairs by the operand staged in the same pair order, and scale and
+// bias are applied once per half-group: sum x (q s + b) = s * sum x (128 + q) +
+// (b - 128 s) * sum x. The row total is a DPP row sum; the result is rounded to bf16 once.
+#include "../../include/gdn.h"
+#include "gdn_device_math.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kTileRows = 64;  // 4 waves x 4 DPP rows x 4 passes
+
+struct QParams {
+  int M, K, R, tiles, nseg;
+  const uint16_t* x;     // (L, M, K) bf16, or NULL with the norm prologue
+  const float* xf;       // (L, M, K) fp32 recurrence output (norm prologue)
+  const uint16_t* z;     // (L, M, K) bf16 gate (norm prologue)
+  const float* gamma;    // (L, 128) fp32 (norm prologue)
+  float eps;
+  const uint32_t* w[GDN_QLINEAR_MAX_SEGS];
+  const uint16_t* s[GDN_QLINEAR_MAX_SEGS];
+  const uint16_t* b[GDN_QLINEAR_MAX_SEGS];
+  uint16_t* y[GDN_QLINEAR_MAX_SEGS];
+  int n[GDN_QLINEAR_MAX_SEGS];
+  int row0[GDN_QLINEAR_MAX_SEGS];  // first global row of each segment
+};
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
+}
+
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Operand chunk (32 values) to LDS: four 16-byte words, word i holding the pairs
+// (v[8i+j], v[8i+j+4]), j = 0..3, the order the nibble pairs come out in; plus the sum
+// of the 32 values.
+__device__ __forceinline__ void stage_chunk(u32x4* xs, float* xsum, int nch, int mm, int c, const float (&v)[32]) {
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) sum += v[e];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4 q;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = pack_bf2(v[8 * i + j], v[8 * i + j + 4]);
+    xs[(mm * 4 + i) * nch + c] = q;
+  }
+  xsum[mm * nch + c] = sum;
+}
+
+template <int J, bool NORM>
+__global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int layer = blockIdx.x / p.tiles;
+  const int tile = blockIdx.x % p.tiles;
+  const int K = J * 512, nch = K / 32;
+  u32x4* xs = reinterpret_cast<u32x4*>(smem);                 // [M][4][nch]
+  float* xsum = reinterpret_cast<float*>(xs + p.M * 4 * nch);  // [M][nch]
+  const int tid = threadIdx.x;
+
+  // ---- stage the operand: thread task t = (row mm, chunk c); the four chunks of a
+  // 128-value head are the four lanes of a DPP quad ----
+  for (int t = tid; t < p.M * nch; t += kThreads) {
+    const int mm = t / nch, c = t % nch;
+    const size_t base = ((size_t)layer * p.M + mm) * K + 32 * c;
+    float v[32];
+    if (NORM) {
+      // GatedRMSNorm: h = o * rsqrt(mean(o^2) + eps) * gamma (fp32), times silu(fp32(z)),
+      // rounded to bf16 (the activation dtype out_proj takes)
+      float o[32];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const f4 f = *reinterpret_cast<const f4*>(p.xf + base + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[4 * q + e] = f[e];
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) ss += o[e] * o[e];
+      ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0xB1, 0xF, 0xF, true));
+      ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0x4E, 0xF, 0xF, true));
+      const float rs = 1.0f / sqrtf(ss / 128.0f + p.eps);
+      const float* gm = p.gamma + (size_t)layer * 128 + 32 * (c & 3);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u16x8 zz = *reinterpret_cast<const u16x8*>(p.z + base + 8 * q);
+        const f4 g0 = *reinterpret_cast<const f4*>(gm + 8 * q);
+        const f4 g1 = *reinterpret_cast<const f4*>(gm + 8 * q + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float zf = bf2f(zz[e]);
+          const float h = o[8 * q + e] * rs * (e < 4 ? g0[e] : g1[e - 4]);
+          v[8 * q + e] = rbf(h * (zf * d_sigmoidf(zf)));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u16x8 xx = *reinterpret_cast<const u16x8*>(p.x + base + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[8 * q + e] = bf2f(xx[e]);
+      }
+    }
+    stage_chunk(xs, xsum, nch, mm, c, v);
+  }
+  __syncthreads();
+
+  // ---- 4 passes of 4 rows per wave ----
+  const int lane = tid & 63, m = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int pass = 0; pass < 4; ++pass) {
+    const int grow = tile * kTileRows + wave * 16 + pass * 4 + (lane >> 4);
+    const bool valid = grow < p.R;
+    const int row = valid ? grow : p.R - 1;
+    int sg = 0;
+#pragma unroll
+    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= p.row0[q]) ? 1 : 0;
+    const uint32_t* wseg = p.w[0];
+    const uint16_t *sseg = p.s[0], *bseg = p.b[0];
+    uint16_t* yseg = p.y[0];
+    int nseg = p.n[0], r0 = p.row0[0];
+#pragma unroll
+    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) {
+      if (sg == q) {
+        wseg = p.w[q];
+        sseg = p.s[q];
+        bseg = p.b[q];
+        yseg = p.y[q];
+        nseg = p.n[q];
+        r0 = p.row0[q];
+      }
+    }
+    const size_t lrow = (size_t)layer * nseg + (row - r0);
+    const u32x4* wr = reinterpret_cast<const u32x4*>(wseg + lrow * (K / 8));
+    const uint16_t* sr = sseg + lrow * (K / 64);
+    const uint16_t* br = bseg + lrow * (K / 64);
+    u32x4 wv[J];
+    uint16_t sv[J], bv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = m + 16 * j;
+      wv[j] = __builtin_nontemporal_load(wr + c);
+      sv[j] = sr[c >> 1];
+      bv[j] = br[c >> 1];
+    }
+    float y[GDN_QLINEAR_MAX_ROWS] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = m + 16 * j;
+      const float sc = bf2f(sv[j]);
+      const float off = bf2f(bv[j]) - 128.0f * sc;
+      uint32_t pr[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t wd = wv[j][i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pr[i][q] = ((wd >> (4 * q)) & 0x000F000Fu) | 0x43004300u;
+      }
+#pragma unroll
+      for (int mm = 0; mm < GDN_QLINEAR_MAX_ROWS; ++mm) {
+        if (mm < p.M) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4 xq = xs[(mm * 4 + i) * nch + c];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = dot2(pr[i][q], xq[q], acc);
+          }
+          y[mm] = __builtin_fmaf(sc, acc, __builtin_fmaf(off, xsum[mm * nch + c], y[mm]));
+        }
+      }
+    }
+#pragma unroll
+    for (int mm = 0; mm < GDN_QLINEAR_MAX_ROWS; ++mm) {
+      if (mm < p.M) {
+        const float tot = row16_sum(y[mm]);
+        if (m == 0 && valid) yseg[((size_t)layer * p.M + mm) * nseg + (row - r0)] = f2bf(tot);
+      }
+    }
+  }
+}
+
+template <bool NORM>
+hipError_t launch_j(int J, const QParams& p, dim3 grid, size_t smem, hipStream_t stream) {
+  switch (J) {
+#define GDN_QL_CASE(j) \
+  case j:              \
+    hipLaunchKernelGGL((qlinear_kernel<j, NORM>), grid, dim3(kThreads), smem, stream, p); break;
+    GDN_QL_CASE(2) GDN_QL_CASE(4) GDN_QL_CASE(8) GDN_QL_CASE(10) GDN_QL_CASE(12) GDN_QL_CASE(16)
+#undef GDN_QL_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool qlinear_k_supported(int k) {
+  return k == 1024 || k == 2048 || k == 4096 || k == 5120 || k == 6144 || k == 8192;
+}
+
+hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
+  QParams p{};
+  p.M = a.m;
+  p.K = a.k;
+  p.nseg = a.n_segs;
+  p.x = static_cast<const uint16_t*>(a.x);
+  p.xf = a.norm_x;
+  p.z = static_cast<const uint16_t*>(a.norm_z);
+  p.gamma = a.norm_gamma;
+  p.eps = a.norm_eps;
+  int R = 0;
+  for (int q = 0; q < GDN_QLINEAR_MAX_SEGS; ++q) {
+    const int qq = q < a.n_segs ? q : 0;  // unused slots repeat segment 0 (never selected)
+    p.w[q] = static_cast<const uint32_t*>(a.segs[qq].w);
+    p.s[q] = static_cast<const uint16_t*>(a.segs[qq].scales);
+    p.b[q] = static_cast<const uint16_t*>(a.segs[qq].biases);
+    p.y[q] = static_cast<uint16_t*>(a.segs[qq].y);
+    p.n[q] = a.segs[qq].n;
+    p.row0[q] = R;
+    if (q < a.n_segs) R += a.segs[q].n;
+  }
+  p.R = R;
+  p.tiles = (R + kTileRows - 1) / kTileRows;
+  const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles));
+  const size_t smem = (size_t)p.M * (a.k / 32) * (4 * 16 + 4);
+  const bool norm = a.norm_x != nullptr;
+  return norm ? launch_j<true>(a.k / 512, p, grid, smem, stream) : launch_j<false>(a.k / 512, p, grid, smem, stream);
+}
+
+}  // namespace gdn

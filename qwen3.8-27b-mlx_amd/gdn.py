@@ -31,8 +31,11 @@ STATES_BHT, STATES_TBH = 0, 1
 HEAD_DIM = 128
 CONV_TAPS = 4
 
+QLINEAR_MAX_SEGS = 4
+QLINEAR_MAX_ROWS = 4
+
 EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-           "gdn_available", "gdn_abi_version", "gdn_last_error")
+           "gdn_qlinear", "gdn_available", "gdn_abi_version", "gdn_last_error")
 
 
 class GdnError(RuntimeError):
@@ -75,6 +78,22 @@ class CommitArgs(ctypes.Structure):
     ]
 
 
+class QLinearSeg(ctypes.Structure):
+    """struct gdn_qlinear_seg (include/gdn.h)."""
+    _fields_ = [("w", _vp), ("scales", _vp), ("biases", _vp), ("y", _vp), ("n", _int)]
+
+
+class QLinearArgs(ctypes.Structure):
+    """struct gdn_qlinear_args (include/gdn.h)."""
+    _fields_ = [
+        ("n_layers", _int), ("m", _int), ("k", _int),
+        ("x", _vp),
+        ("norm_x", _vp), ("norm_z", _vp), ("norm_gamma", _vp), ("norm_eps", ctypes.c_float),
+        ("n_segs", _int), ("segs", QLinearSeg * QLINEAR_MAX_SEGS),
+        ("stream", _vp),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -93,6 +112,8 @@ def lib() -> ctypes.CDLL:
         L.gdn_prefill_workspace_size.restype = _int
         L.gdn_commit.argtypes = [ctypes.POINTER(CommitArgs)]
         L.gdn_commit.restype = _int
+        L.gdn_qlinear.argtypes = [ctypes.POINTER(QLinearArgs)]
+        L.gdn_qlinear.restype = _int
         L.gdn_available.argtypes = []
         L.gdn_available.restype = _int
         L.gdn_abi_version.argtypes = []
@@ -127,6 +148,10 @@ def call_prefill(args: LayerArgs) -> None:
 
 def call_commit(args: CommitArgs) -> None:
     _check(lib().gdn_commit(ctypes.byref(args)))
+
+
+def call_qlinear(args: QLinearArgs) -> None:
+    _check(lib().gdn_qlinear(ctypes.byref(args)))
 
 
 def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48, conv: bool = True) -> int:
@@ -356,3 +381,50 @@ class DeltaCache:
         self.offset = self.base_offset + n
         self.pending = None
         self.record = False
+
+
+# --------------------------------------------------------------------------
+# quantized linear: Linear::operator() for 4-bit weights (cpp/src/model.cpp:356-372)
+
+@dataclass
+class QuantLinear:
+    """One quantized weight as the reference stores it (cpp/src/model.hpp Linear): w
+    (N, K/8) uint32 (stored as int32 by torch), scales and biases (N, K/64) bf16; with a
+    leading layer dimension when several layers are stacked."""
+    w: object
+    scales: object
+    biases: object
+
+    @property
+    def n(self) -> int:
+        return self.w.shape[-2]
+
+
+def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
+    """gdn_qlinear_args for y_i = x W_i^T, i over `mats` (1..4 QuantLinear reading the same
+    x), or with norm = (o, z, gamma, eps) the layer's GatedRMSNorm of o as the operand.
+    Allocates the outputs; returns (args, [y_i])."""
+    import torch
+    src = x if x is not None else norm[0]
+    K = src.shape[-1]
+    M = src.shape[-2]
+    ys = []
+    a = QLinearArgs(n_layers=n_layers, m=M, k=K, x=_ptr(x), n_segs=len(mats), stream=_stream(stream))
+    if norm is not None:
+        o, z, gamma, eps = norm
+        a.norm_x, a.norm_z, a.norm_gamma, a.norm_eps = _ptr(o), _ptr(z), _ptr(gamma), float(eps)
+    for i, q in enumerate(mats):
+        shape = (n_layers, M, q.n) if n_layers > 1 else (M, q.n)
+        y = torch.empty(shape, dtype=torch.bfloat16, device=src.device)
+        ys.append(y)
+        a.segs[i] = QLinearSeg(w=_ptr(q.w), scales=_ptr(q.scales), biases=_ptr(q.biases), y=_ptr(y), n=q.n)
+    return a, ys
+
+
+def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
+    """Linear::operator() for quantized weights (model.cpp:356-372) over 1..4 matrices
+    sharing x -- e.g. the layer's in_proj_qkv, in_proj_z, in_proj_a, in_proj_b -- or, with
+    norm = (o, z, gamma, eps), out_proj(GatedRMSNorm(o, z)) (model.cpp:626-641)."""
+    args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, stream=stream)
+    call_qlinear(args)
+    return ys

@@ -22,7 +22,7 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(
         ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-         "gdn_available", "gdn_abi_version", "gdn_last_error"])
+         "gdn_qlinear", "gdn_available", "gdn_abi_version", "gdn_last_error"])
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -55,7 +55,9 @@ def _c_layout(struct: str, fields):
 
 
 @pytest.mark.parametrize("cls,struct", [("LayerArgs", "gdn_layer_args"),
-                                        ("CommitArgs", "gdn_commit_args")])
+                                        ("CommitArgs", "gdn_commit_args"),
+                                        ("QLinearArgs", "gdn_qlinear_args"),
+                                        ("QLinearSeg", "gdn_qlinear_seg")])
 def test_ctypes_mirror_matches_c_layout(gdn, cls, struct):
     C = getattr(gdn, cls)
     names = [f for f, _ in C._fields_]
@@ -207,3 +209,38 @@ def test_product_does_not_touch_the_oracle():
             if f.endswith((".py", ".hip", ".cpp", ".h", ".hpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.lower() and "gdno_" not in text, f
+
+
+def _ql(gdn, **kw):
+    segs = kw.pop("segs", None)
+    base = dict(n_layers=1, m=1, k=5120, x=0x10000, n_segs=1)
+    base.update(kw)
+    a = gdn.QLinearArgs(**base)
+    for i, sg in enumerate(segs or [dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x4000000, n=64)]):
+        a.segs[i] = gdn.QLinearSeg(**sg)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(m=0), "bad shape"),
+    (dict(m=5), "bad shape"),
+    (dict(n_layers=0), "bad shape"),
+    (dict(k=5000), "unsupported"),
+    (dict(m=4, k=8192), "too large"),
+    (dict(n_segs=5), "n_segs"),
+    (dict(x=None), "exactly one"),
+    (dict(norm_x=0x20000), "exactly one"),
+    (dict(x=None, norm_x=0x20000), "norm_z and norm_gamma"),
+    (dict(x=0x10008), "16-byte"),
+    (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0, y=0x4000000, n=64)]), "segment 0"),
+    (dict(segs=[dict(w=0x1000008, scales=0x2000000, biases=0x3000000, y=0x4000000, n=64)]), "16-byte"),
+    (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x10000 + 64, n=64)]), "operand"),
+    (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x1000000 + 64, n=64)]), "weight"),
+    (dict(n_segs=2, segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x4000000, n=64),
+                          dict(w=0x5000000, scales=0x6000000, biases=0x7000000, y=0x4000000 + 2, n=8)]),
+     "overlap"),
+])
+def test_qlinear_rejects_bad_arguments(gdn, kw, msg):
+    rc = gdn.lib().gdn_qlinear(ctypes.byref(_ql(gdn, **kw)))
+    assert rc == gdn.GDN_EINVAL
+    assert msg in gdn.last_error(), gdn.last_error()

@@ -1,0 +1,115 @@
+"""GPU parity of gdn_qlinear -- Linear::operator() for 4-bit weights
+(cpp/src/model.cpp:356-372) and the GatedRMSNorm + out_proj pair (model.cpp:350-354,
+626-641) -- against the oracle's fp64 dequantize-and-dot.
+
+Tolerance: the result is rounded to bf16 once (half an ulp: 2^-9 relative), and the fp32
+accumulation (products of x with the offset bf16 values 128 + nibble, per 32-value piece)
+adds at most 2^-20 of sum_k |x_k| (143 |s_k| + |b_k|), the magnitudes it accumulates. The
+test allows 2^-8 |y| plus that bound. MLX's own accumulation order is unpinned at bit
+level; the reference rounds its fp32 result to bf16 as this does.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _util import bf16_to_f32, log_case, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def quant_inputs(O, L, M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    x = O.to_bf16(rng.standard_normal((L, M, K)).astype(np.float32))
+    w = rng.integers(0, 2 ** 32, (L, N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = O.to_bf16(rng.uniform(0.002, 0.03, (L, N, K // 64)).astype(np.float32))
+    b = O.to_bf16(rng.uniform(-0.2, 0.2, (L, N, K // 64)).astype(np.float32))
+    return x, w, s, b
+
+
+def dev_mat(gdn, dev, w, s, b):
+    return gdn.QuantLinear(to_dev(w.view(np.int32), dev), to_dev(s, dev), to_dev(b, dev))
+
+
+def bound(O, x_bf16, s, b):
+    """Per-output fp32 accumulation bound: 2^-20 sum_k |x_k| (143 |s_k| + |b_k|)."""
+    xa = np.abs(bf16_to_f32(x_bf16)).astype(np.float64)                 # (M, K)
+    mag = 143.0 * np.abs(bf16_to_f32(s)) + np.abs(bf16_to_f32(b))        # (N, K/64)
+    return 2.0 ** -20 * (xa @ np.repeat(mag, 64, axis=1).T)              # (M, N)
+
+
+def check(got_bf16, ref, tol_abs, what):
+    got = bf16_to_f32(got_bf16).astype(np.float64)
+    err = np.abs(got - ref)
+    lim = 2.0 ** -8 * np.abs(ref) + tol_abs
+    worst = (err / np.maximum(lim, 1e-30)).max()
+    print(f"  {what}: max |err| {err.max():.3e}, worst err / limit {worst:.3f}", flush=True)
+    assert np.all(np.isfinite(got)), what
+    assert np.all(err <= lim), what
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 200, 1024), (2, 96, 5120), (4, 130, 6144), (3, 64, 8192),
+                                   (1, 48, 2048), (4, 17, 4096)])
+def test_qlinear_single_matrix(O, gdn, dev, M, N, K):
+    import torch
+    log_case(f"qlinear M={M} N={N} K={K}")
+    x, w, s, b = quant_inputs(O, 1, M, N, K, seed=N + K + M)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    ref = O.qlinear(x[0], w[0], s[0], b[0])
+    check(to_np(y), ref, bound(O, x[0], s[0], b[0]), "y")
+
+
+def test_qlinear_in_proj_four_matrices_two_layers(O, gdn, dev):
+    """The DeltaNet layer's in_proj_qkv (10240), in_proj_z (6144), in_proj_a, in_proj_b (48)
+    on one x of 5120 (model.cpp:587, 608-609, 626), two layers stacked, B=1."""
+    import torch
+    log_case("qlinear in_proj 4 segments x 2 layers, K=5120")
+    L, M, K = 2, 1, 5120
+    ns = [10240, 6144, 48, 48]
+    mats, host = [], []
+    x = None
+    for i, n in enumerate(ns):
+        xi, w, s, b = quant_inputs(O, L, M, n, K, seed=100 + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w, s, b))
+        host.append((w, s, b))
+    ys = gdn.qlinear(mats, to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        got = to_np(y)
+        for l in range(L):
+            ref = O.qlinear(x[l], w[l], s[l], b[l])
+            check(got[l], ref, bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
+
+
+def test_qlinear_gated_rmsnorm_prologue(O, gdn, dev):
+    """out_proj(GatedRMSNorm(o, z)) in one call (model.cpp:626-641): o fp32 (M, 6144), z bf16,
+    gamma (128); against the oracle's norm (bf16 operand) then its fp64 product. A one-ulp
+    flip of an operand element between the two norms (fp32 reductions in different
+    orders) moves y by at most 2^-8 |x_k w_k|; three such flips are allowed per output."""
+    import torch
+    log_case("qlinear out_proj with GatedRMSNorm, M=2, K=6144, N=5120")
+    M, K, N = 2, 6144, 5120
+    rng = np.random.default_rng(77)
+    o = (rng.standard_normal((M, K)) * 0.3).astype(np.float32)
+    z = O.to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    gamma = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    _, w, s, b = quant_inputs(O, 1, M, N, K, seed=78)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])],
+                       norm=(to_dev(o, dev), to_dev(z, dev), to_dev(gamma, dev), 1e-6))
+    torch.cuda.synchronize()
+    xn = O.gated_rmsnorm(o.reshape(M * 48, 128), z.reshape(M * 48, 128), gamma, 1e-6).reshape(M, K)
+    ref = O.qlinear(xn, w[0], s[0], b[0])
+    W = (np.abs(np.repeat(bf16_to_f32(s[0]), 64, axis=1)) * 15 + np.abs(np.repeat(bf16_to_f32(b[0]), 64, axis=1)))
+    flip = 3 * 2.0 ** -8 * (np.abs(bf16_to_f32(xn)).max(axis=1, keepdims=True) * W.max(axis=1)[None, :])
+    check(to_np(y), ref, bound(O, xn, s[0], b[0]) + flip, "y")
+
+
+def test_qlinear_rejects_bad_arguments_on_gpu(gdn, dev):
+    import torch
+    x = torch.zeros((1, 5000), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((8, 625), dtype=torch.int32, device=dev)
+    sb = torch.zeros((8, 78), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(gdn.GdnError, match="unsupported"):
+        gdn.qlinear([gdn.QuantLinear(w, sb, sb)], x)

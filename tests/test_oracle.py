@@ -373,3 +373,74 @@ def test_commit_semantics(O):
         O.commit(T + 1, states, S0, xp)
     with pytest.raises(ValueError):
         O.commit(-1, states, S0, xp)
+
+
+# ---------------------------------------------------------------- quantized linear / norm
+
+def _unpack_np(w):
+    """Independent unpacking of the 4-bit layout with numpy bit ops: value i of a word in
+    nibble i, low nibble first (python/mlp_kernel.py:54-56)."""
+    N, W8 = w.shape
+    sh = (4 * np.arange(8, dtype=np.uint32))
+    return ((w[:, :, None] >> sh) & 0xF).reshape(N, W8 * 8).astype(np.float64)
+
+
+def _qlin_inputs(O, M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    x = O.to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    w = rng.integers(0, 2 ** 32, (N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = O.to_bf16(rng.uniform(0.005, 0.05, (N, K // 64)).astype(np.float32))
+    b = O.to_bf16(rng.uniform(-0.2, 0.2, (N, K // 64)).astype(np.float32))
+    return x, w, s, b
+
+
+def test_qlinear_matches_numpy_dequantize(O):
+    x, w, s, b = _qlin_inputs(O, 3, 37, 256, 5)
+    W = (_unpack_np(w) * np.repeat(O.from_bf16(s).astype(np.float64), 64, axis=1)
+         + np.repeat(O.from_bf16(b).astype(np.float64), 64, axis=1))
+    ref = O.from_bf16(x).astype(np.float64) @ W.T
+    assert np.abs(O.qlinear(x, w, s, b) - ref).max() <= 1e-12 * np.abs(ref).max()
+
+
+def test_qlinear_nibble_order_known_answers(O):
+    """A single nonzero nibble at value position i of word j selects x[8j + i]; scale 1,
+    bias 0; an all-zero w with bias b gives b * sum(x) per group."""
+    K, N = 128, 16
+    x = O.to_bf16(np.arange(1, K + 1, dtype=np.float32) / 64)
+    xf = O.from_bf16(x).astype(np.float64)
+    w = np.zeros((N, K // 8), np.uint32)
+    for n in range(N):
+        j, i = n % (K // 8), n % 8
+        w[n, j] = np.uint32(3) << np.uint32(4 * i)
+    one = O.to_bf16(np.ones((N, K // 64), np.float32))
+    zero = O.to_bf16(np.zeros((N, K // 64), np.float32))
+    y = O.qlinear(x[None], w, one, zero)[0]
+    for n in range(N):
+        j, i = n % (K // 8), n % 8
+        assert y[n] == 3 * xf[8 * j + i]
+    half = O.to_bf16(np.full((N, K // 64), 0.5, np.float32))
+    y = O.qlinear(x[None], np.zeros_like(w), one, half)[0]
+    assert np.allclose(y, 0.5 * xf.sum())
+
+
+def test_gated_rmsnorm_closed_forms_and_fp64(O):
+    rng = np.random.default_rng(9)
+    o = rng.standard_normal((6, 128)).astype(np.float32)
+    z = O.to_bf16(rng.standard_normal((6, 128)).astype(np.float32))
+    g = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    out = O.from_bf16(O.gated_rmsnorm(o, z, g, 1e-6)).astype(np.float64)
+    od, zd = o.astype(np.float64), O.from_bf16(z).astype(np.float64)
+    ref = od / np.sqrt((od ** 2).mean(-1, keepdims=True) + 1e-6) * g * (zd / (1 + np.exp(-zd)))
+    assert np.all(np.abs(out - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-7)
+    # silu(0) = 0 gates everything off
+    assert np.all(O.gated_rmsnorm(o, O.to_bf16(np.zeros_like(o)), g, 1e-6) & 0x7FFF == 0)
+    # scale invariance of the norm (eps aside): o and 1000 o give the same output
+    a = O.gated_rmsnorm(o, z, g, 0.0)
+    bb = O.gated_rmsnorm(o * 1024.0, z, g, 0.0)
+    assert np.array_equal(a, bb)
+    # a constant row c normalises to sign(c) gamma
+    c = np.full((1, 128), -3.0, np.float32)
+    one = O.to_bf16(np.full((1, 128), 20.0, np.float32))   # silu(20) rounds to 20
+    r = O.from_bf16(O.gated_rmsnorm(c, one, g, 0.0))[0]
+    expect = O.from_bf16(O.to_bf16((-g * (20.0 / (1 + np.exp(-20.0)))).astype(np.float32)))
+    assert np.allclose(r, expect, rtol=2 ** -8)
