@@ -29,10 +29,11 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kTileRows = 64;  // 4 waves x 4 DPP rows x 4 passes
+constexpr int kRowsPerPass = 16;  // 4 waves x 4 DPP rows
 
 struct QParams {
   int M, K, R, tiles, nseg;
+  int passes;            // row passes per workgroup: a tile is 16 x passes rows
   const uint16_t* x;     // (L, M, K) bf16, or NULL with the norm prologue
   const float* xf;       // (L, M, K) fp32 recurrence output (norm prologue)
   const uint16_t* z;     // (L, M, K) bf16 gate (norm prologue)
@@ -128,11 +129,12 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   }
   __syncthreads();
 
-  // ---- 4 passes of 4 rows per wave ----
+  // ---- passes of 4 rows per wave ----
   const int lane = tid & 63, m = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int pass = 0; pass < 4; ++pass) {
-    const int grow = tile * kTileRows + wave * 16 + pass * 4 + (lane >> 4);
+  const int passes = p.passes;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int grow = (tile * passes + pass) * kRowsPerPass + wave * 4 + (lane >> 4);
     const bool valid = grow < p.R;
     const int row = valid ? grow : p.R - 1;
     int sg = 0;
@@ -245,10 +247,13 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
     if (q < a.n_segs) R += a.segs[q].n;
   }
   p.R = R;
-  p.tiles = (R + kTileRows - 1) / kTileRows;
+  const bool norm = a.norm_x != nullptr;
+  // rows per workgroup: 64, or 256 with the norm prologue (every workgroup normalises
+  // the whole operand, so fewer, taller tiles)
+  p.passes = norm ? 16 : 4;
+  p.tiles = (R + kRowsPerPass * p.passes - 1) / (kRowsPerPass * p.passes);
   const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles));
   const size_t smem = (size_t)p.M * (a.k / 32) * (4 * 16 + 4);
-  const bool norm = a.norm_x != nullptr;
   return norm ? launch_j<true>(a.k / 512, p, grid, smem, stream) : launch_j<false>(a.k / 512, p, grid, smem, stream);
 }
 
