@@ -258,7 +258,8 @@ def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str):
     nbytes = NL * per_layer
     return dict(GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1),
                 frac_hbm=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                us_per_step=round(r["ms_per_step"] * 1e3, 2), bytes_per_step=nbytes)
+                us_per_step=round(r["ms_per_step"] * 1e3, 2), bytes_per_step=nbytes,
+                traffic=load_traffic("in_proj_48_layers_b1" if which == "in_proj" else "out_proj_norm_48_layers_b1"))
 
 
 def bench_copy_ceiling(torch, dev, timer, steps: int = 50):

@@ -7,6 +7,8 @@
 //                       front end + gates + delta::run + cache advance  cpp/src/model.cpp:585-638
 //   gdn::DeltaCache     DeltaCache with record / commit(n)             cpp/src/model.hpp:211-227,
 //                                                                       cpp/src/model.cpp:439-457
+//   gdn::linear(s)      Linear::operator(), 4-bit weights              cpp/src/model.cpp:356-372
+//   gdn::norm_out_proj  out_proj(GatedRMSNorm(o, z))                   cpp/src/model.cpp:626-641
 // Errors are C++ exceptions on this side of the ABI (the reference's fail() /
 // std::runtime_error convention); the ABI itself never throws.
 //
@@ -196,5 +198,54 @@ class DeltaCache {
   const void* pending_x_ = nullptr;
   int pending_T_ = -1;
 };
+
+// Linear::operator() for the reference's 4-bit weights (cpp/src/model.cpp:356-372), on
+// device pointers in the checkpoint's layout: w (N, K/8) uint32, scales and biases
+// (N, K/64) bf16.
+struct QuantLinear {
+  const void* w = nullptr;
+  const void* scales = nullptr;
+  const void* biases = nullptr;
+  int n = 0;  // out features
+};
+
+// y[i] (M, W[i].n) bf16 = x (M, K) bf16 times W[i]^T, for count <= GDN_QLINEAR_MAX_SEGS
+// matrices sharing x in one launch -- the layer's in_proj_qkv, in_proj_z, in_proj_a,
+// in_proj_b (model.cpp:587, 608-609, 626).
+inline void linears(int M, int K, const void* x, const QuantLinear* W, void* const* y, int count,
+                    hipStream_t stream = nullptr) {
+  gdn_qlinear_args a{};
+  a.n_layers = 1;
+  a.m = M;
+  a.k = K;
+  a.x = x;
+  a.n_segs = count;
+  for (int i = 0; i < count && i < GDN_QLINEAR_MAX_SEGS; ++i)
+    a.segs[i] = gdn_qlinear_seg{W[i].w, W[i].scales, W[i].biases, y[i], W[i].n};
+  a.stream = stream;
+  check(gdn_qlinear(&a));
+}
+
+inline void linear(const QuantLinear& W, int M, int K, const void* x, void* y, hipStream_t stream = nullptr) {
+  linears(M, K, x, &W, &y, 1, stream);
+}
+
+// out_proj(GatedRMSNorm(o, z)) (model.cpp:626-641): o (M, K) fp32 recurrence output, z (M,
+// K) bf16, gamma (128) fp32 -> y (M, W.n) bf16.
+inline void norm_out_proj(const QuantLinear& W, int M, int K, const float* o, const void* z, const float* gamma,
+                          float eps, void* y, hipStream_t stream = nullptr) {
+  gdn_qlinear_args a{};
+  a.n_layers = 1;
+  a.m = M;
+  a.k = K;
+  a.norm_x = o;
+  a.norm_z = z;
+  a.norm_gamma = gamma;
+  a.norm_eps = eps;
+  a.n_segs = 1;
+  a.segs[0] = gdn_qlinear_seg{W.w, W.scales, W.biases, y, W.n};
+  a.stream = stream;
+  check(gdn_qlinear(&a));
+}
 
 }  // namespace gdn

@@ -2,7 +2,7 @@
 // reference's self-test (cpp/src/tests.cpp:36-56 rel_err/check, 196-243 test_delta):
 // gdn::run vs the oracle's run_reference restatement on the reference's shapes and input
 // distributions, with and without collect, bound 2e-5; then DeltaCache record/commit
-// against plain decoding. The oracle (oracle/gdn_oracle.h) is the checker only.
+// against plain decoding; then the quantized projections (gdn::linears, norm_out_proj). The oracle (oracle/gdn_oracle.h) is the checker only.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -186,6 +186,95 @@ void test_cache() {
 
 }  // namespace
 
+// gdn::linears (the layer's four in_proj matrices on one x) and gdn::norm_out_proj vs the
+// oracle's fp64 dequantize-and-dot: within half a bf16 ulp plus the fp32 accumulation.
+void test_qlinear() {
+  printf("quantized linear (model.cpp:356-372)\n");
+  const int M = 1, K = 5120;
+  const int ns[4] = {256, 96, 48, 48};
+  uint64_t st = 12345;
+  std::vector<uint16_t> x(M * K);
+  {
+    std::vector<float> xf = normal(501, x.size());
+    gdno_round_bf16(xf.data(), x.data(), (int64_t)x.size());
+  }
+  uint16_t* dx = to_dev(x);
+  std::vector<gdn::QuantLinear> W(4);
+  std::vector<void*> y(4);
+  std::vector<std::vector<uint32_t>> hw(4);
+  std::vector<std::vector<uint16_t>> hs(4), hb(4);
+  for (int i = 0; i < 4; ++i) {
+    const int N = ns[i];
+    hw[i].resize((size_t)N * K / 8);
+    for (auto& v : hw[i]) v = (uint32_t)gdno_splitmix64_next(&st);
+    std::vector<float> sf(N * K / 64), bf(N * K / 64);
+    gdno_fill_uniform(600 + i, 0.002f, 0.03f, sf.data(), (int64_t)sf.size());
+    gdno_fill_uniform(700 + i, -0.2f, 0.2f, bf.data(), (int64_t)bf.size());
+    hs[i].resize(sf.size());
+    hb[i].resize(bf.size());
+    gdno_round_bf16(sf.data(), hs[i].data(), (int64_t)sf.size());
+    gdno_round_bf16(bf.data(), hb[i].data(), (int64_t)bf.size());
+    W[i] = gdn::QuantLinear{to_dev(hw[i]), to_dev(hs[i]), to_dev(hb[i]), N};
+    gdn::check_hip(hipMalloc(&y[i], (size_t)M * N * 2), "hipMalloc");
+  }
+  gdn::linears(M, K, dx, W.data(), y.data(), 4);
+  gdn::check_hip(hipDeviceSynchronize(), "sync");
+  for (int i = 0; i < 4; ++i) {
+    const int N = ns[i];
+    std::vector<double> ref((size_t)M * N);
+    gdno_qlinear_f64(M, N, K, x.data(), hw[i].data(), hs[i].data(), hb[i].data(), ref.data());
+    std::vector<uint16_t> got = to_host(static_cast<uint16_t*>(y[i]), (size_t)M * N);
+    double worst = 0;
+    for (int n = 0; n < N; ++n) {
+      double acc = 0;  // 2^-20 sum |x| (143 |s| + |b|)
+      for (int k = 0; k < K; ++k)
+        acc += std::fabs(gdno_bf16_to_f32(x[k])) * (143.0 * std::fabs(gdno_bf16_to_f32(hs[i][(size_t)n * K / 64 + k / 64])) +
+                                                   std::fabs(gdno_bf16_to_f32(hb[i][(size_t)n * K / 64 + k / 64])));
+      const double lim = std::ldexp(std::fabs(ref[n]), -8) + std::ldexp(acc, -20);
+      worst = std::max(worst, std::fabs(gdno_bf16_to_f32(got[n]) - ref[n]) / lim);
+    }
+    char buf[128];
+    snprintf(buf, sizeof(buf), "in_proj segment %d (N=%d): worst err / limit %.3f", i, N, worst);
+    check(worst <= 1.0, buf);
+  }
+  // norm + out_proj
+  {
+    const int Ko = 6144, No = 64;
+    std::vector<float> o = normal(801, (size_t)M * Ko, 0.3f), zf = normal(802, (size_t)M * Ko);
+    std::vector<uint16_t> z(zf.size());
+    gdno_round_bf16(zf.data(), z.data(), (int64_t)z.size());
+    std::vector<float> gamma(128);
+    gdno_fill_uniform(803, 0.5f, 1.5f, gamma.data(), 128);
+    std::vector<uint32_t> w((size_t)No * Ko / 8);
+    for (auto& v : w) v = (uint32_t)gdno_splitmix64_next(&st);
+    std::vector<float> sf(No * Ko / 64, 0.01f), bf(No * Ko / 64, 0.05f);
+    std::vector<uint16_t> sh(sf.size()), bh(bf.size());
+    gdno_round_bf16(sf.data(), sh.data(), (int64_t)sf.size());
+    gdno_round_bf16(bf.data(), bh.data(), (int64_t)bf.size());
+    gdn::QuantLinear Wo{to_dev(w), to_dev(sh), to_dev(bh), No};
+    float* dout = nullptr;
+    gdn::check_hip(hipMalloc(&dout, (size_t)M * No * 2), "hipMalloc");
+    gdn::norm_out_proj(Wo, M, Ko, to_dev(o), to_dev(z), to_dev(gamma), 1e-6f, dout);
+    gdn::check_hip(hipDeviceSynchronize(), "sync");
+    std::vector<uint16_t> xn((size_t)M * Ko);
+    gdno_gated_rmsnorm((int64_t)M * Ko / 128, 128, o.data(), z.data(), gamma.data(), 1e-6f, xn.data());
+    std::vector<double> ref((size_t)M * No);
+    gdno_qlinear_f64(M, No, Ko, xn.data(), w.data(), sh.data(), bh.data(), ref.data());
+    std::vector<uint16_t> got = to_host(reinterpret_cast<uint16_t*>(dout), (size_t)M * No);
+    double xmax = 0;
+    for (uint16_t v : xn) xmax = std::max(xmax, (double)std::fabs(gdno_bf16_to_f32(v)));
+    double worst = 0;
+    for (int n = 0; n < No; ++n) {
+      // bf16 rounding, accumulation, and up to 3 one-ulp operand flips between the norms
+      const double lim = std::ldexp(std::fabs(ref[n]), -8) + 1e-3 * xmax + 3 * std::ldexp(xmax * (15 * 0.01 + 0.05), -8);
+      worst = std::max(worst, std::fabs(gdno_bf16_to_f32(got[n]) - ref[n]) / lim);
+    }
+    char buf[128];
+    snprintf(buf, sizeof(buf), "GatedRMSNorm + out_proj (N=%d, K=%d): worst err / limit %.3f", No, Ko, worst);
+    check(worst <= 1.0, buf);
+  }
+}
+
 int main() {
   if (!gdn::available()) {
     printf("[skip] no gfx950 device\n");
@@ -194,6 +283,7 @@ int main() {
   try {
     test_delta();
     test_cache();
+    test_qlinear();
   } catch (const std::exception& e) {
     printf("  [FAIL] exception: %s\n", e.what());
     ++g_fail;
