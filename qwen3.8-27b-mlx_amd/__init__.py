@@ -8,3 +8,4 @@ from .gdn import (  # noqa: F401
     lib, prefill_chunked, prefill_workspace_size, qlinear, qlinear_args, QLinearArgs,
     QLinearSeg, QuantLinear, QLINEAR_MAX_ROWS, QLINEAR_MAX_SEGS, run,
 )
+from . import weights  # noqa: F401,E402  (checkpoint reader for the path's weights)

@@ -2,7 +2,7 @@
 (cpp/src/model.cpp:356-372) and the GatedRMSNorm + out_proj pair (model.cpp:350-354,
 626-641) -- against the oracle's fp64 dequantize-and-dot.
 
-Tolerance: the result is rounded to bf16 once (half an ulp: 2^-9 relative), and the fp32
+Tolerance: the result is rounded to bf16 once (half an ulp: at most 2^-8 relative), and the fp32
 accumulation (products of x with the offset bf16 values 128 + nibble, per 32-value piece)
 adds at most 2^-20 of sum_k |x_k| (143 |s_k| + |b_k|), the magnitudes it accumulates. The
 test allows 2^-8 |y| plus that bound. MLX's own accumulation order is unpinned at bit
