@@ -153,7 +153,10 @@ typedef struct gdn_commit_args {
   int states_layout;         /* gdn_states_layout */
   const float* state_prev;   /* (B, Hv, 128, 128): the state the block started from */
   float* state_dst;          /* (B, Hv, 128, 128) <- n == 0 ? state_prev : states[n-1];
-                                may equal state_prev */
+                                may equal state_prev; with n_layers = 1 and the
+                                GDN_STATES_TBH layout it may BE step n-1's block
+                                (states + (n-1)*B*Hv*128*128): the pointer-swap commit,
+                                which copies no state (only the conv window moves) */
   const void* conv_state_in; /* (B, 3, C) bf16 the block started from, or NULL (zeros) */
   const void* x;             /* (B, T, C) bf16, the block's conv input */
   void* conv_state_dst;      /* (B, 3, C) bf16 <- rows n..n+2 of [conv_state_in ; x]; may

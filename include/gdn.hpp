@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -89,30 +90,38 @@ struct LayerParams {
 // every step (the kernel never updates them in place).
 class DeltaCache {
  public:
+  // Recorded blocks go to two buffers of max_record_steps states each, (T, B, Hv) order,
+  // used in turn: commit(n) adopts step n-1 of the block by pointer (no copy), and the
+  // next block is recorded into the other buffer, which no longer holds the live state.
   DeltaCache(const LayerParams& p, int batch, int max_record_steps)
       : p_(p), B_(batch), max_T_(max_record_steps) {
     const size_t D = GDN_HEAD_DIM;
     state_bytes_ = (size_t)B_ * p_.num_v_heads * D * D * sizeof(float);
     conv_bytes_ = (size_t)B_ * (GDN_CONV_TAPS - 1) * p_.conv_dim() * 2;
-    check_hip(hipMalloc(&state_, state_bytes_), "hipMalloc state");
+    check_hip(hipMalloc(&own_state_, state_bytes_), "hipMalloc state");
     check_hip(hipMalloc(&conv_, conv_bytes_), "hipMalloc conv");
     check_hip(hipMalloc(&conv_spare_, conv_bytes_), "hipMalloc conv");
-    if (max_T_ > 0) check_hip(hipMalloc(&states_, state_bytes_ * max_T_), "hipMalloc states");
-    check_hip(hipMemset(state_, 0, state_bytes_), "hipMemset");
+    for (float*& r : rec_)
+      if (max_T_ > 0) check_hip(hipMalloc(&r, state_bytes_ * max_T_), "hipMalloc states");
+    check_hip(hipMemset(own_state_, 0, state_bytes_), "hipMemset");
     check_hip(hipMemset(conv_, 0, conv_bytes_), "hipMemset");
+    state_ = own_state_;
   }
   DeltaCache(const DeltaCache&) = delete;
   DeltaCache& operator=(const DeltaCache&) = delete;
   ~DeltaCache() {
-    (void)hipFree(state_);
+    (void)hipFree(own_state_);
     (void)hipFree(conv_);
     (void)hipFree(conv_spare_);
-    if (states_) (void)hipFree(states_);
+    for (float* r : rec_)
+      if (r) (void)hipFree(r);
   }
 
   int offset = 0;
   bool record = false;
 
+  // The live state (B, Hv, 128, 128) fp32. After a commit(n > 0) it is a block of a
+  // recording buffer, so re-read the pointer after every commit.
   float* state() const { return state_; }
   void* conv() const { return conv_; }
   size_t state_bytes() const { return state_bytes_; }
@@ -145,7 +154,8 @@ class DeltaCache {
     g.stream = stream;
     if (record) {
       if (T > max_T_) throw Error(GDN_EINVAL, "DeltaCache: record block longer than max_record_steps");
-      g.states = states_;
+      pending_states_ = holds_state(rec_[0]) ? rec_[1] : rec_[0];
+      g.states = pending_states_;
       check(gdn_run(&g));
       base_offset_ = offset;
       pending_x_ = x;
@@ -170,15 +180,18 @@ class DeltaCache {
     c.num_v_heads = p_.num_v_heads;
     c.conv_dim = p_.conv_dim();
     c.n = n;
-    c.states = states_;
+    c.states = pending_states_;
     c.states_layout = GDN_STATES_TBH;
     c.state_prev = state_;
-    c.state_dst = state_;
+    // pointer swap: step n-1 of the block becomes the state where it lies
+    float* adopted = n == 0 ? state_ : pending_states_ + (size_t)(n - 1) * (state_bytes_ / sizeof(float));
+    c.state_dst = adopted;
     c.conv_state_in = conv_;
     c.x = pending_x_;
     c.conv_state_dst = conv_;
     c.stream = stream;
     check(gdn_commit(&c));
+    state_ = adopted;
     offset = base_offset_ + n;
     pending_T_ = -1;
     pending_x_ = nullptr;
@@ -190,10 +203,17 @@ class DeltaCache {
   int B_;
   int max_T_;
   size_t state_bytes_ = 0, conv_bytes_ = 0;
-  float* state_ = nullptr;
+  bool holds_state(const float* rec) const {
+    const uintptr_t s = reinterpret_cast<uintptr_t>(state_), r = reinterpret_cast<uintptr_t>(rec);
+    return rec && s >= r && s < r + state_bytes_ * (size_t)max_T_;
+  }
+
+  float* own_state_ = nullptr;
+  float* state_ = nullptr;  // own_state_ or a block of rec_[0] / rec_[1]
   void* conv_ = nullptr;
   void* conv_spare_ = nullptr;
-  float* states_ = nullptr;
+  float* rec_[2] = {nullptr, nullptr};
+  float* pending_states_ = nullptr;
   int base_offset_ = 0;
   const void* pending_x_ = nullptr;
   int pending_T_ = -1;

@@ -60,7 +60,13 @@ __global__ void commit_conv_kernel(CommitParams p) {
 }  // namespace
 
 hipError_t launch_commit(const CommitParams& p, hipStream_t stream) {
-  const bool copy_state = !(p.n == 0 && p.state_prev == p.state_dst);
+  // Nothing to copy when the destination already is the adopted state: n == 0 onto the
+  // previous state, or the pointer swap (one layer, (T, B, Hv) states, destination = step
+  // n-1's contiguous block).
+  const bool keep_prev = p.n == 0 && p.state_prev == p.state_dst;
+  const bool swapped = p.n > 0 && p.states_tbh && p.n_layers == 1 &&
+                       p.states + (size_t)(p.n - 1) * p.B * p.Hv * kD * kD == p.state_dst;
+  const bool copy_state = !keep_prev && !swapped;
   if (copy_state) {
     const size_t total = (size_t)p.n_layers * p.B * p.Hv * kD * kD / 4;
     const size_t blocks = std::min<size_t>((total + 255) / 256, 8192);

@@ -329,6 +329,10 @@ class DeltaCache:
     """DeltaCache (cpp/src/model.hpp:211-227) over device buffers: `record` mode keeps
     the per-step states of a block instead of advancing; commit(n) adopts step n.
 
+    The per-step states of a block are recorded in (T, B, Hv) order, so step n-1 is one
+    contiguous state and commit(n) adopts it by pointer: `state` becomes a view of the
+    recorded block and no state is copied (only the 3-row conv window moves).
+
     The conv state is kept in two buffers that swap roles each call (the library never
     updates it in place: every workgroup must see the old rows)."""
 
@@ -351,11 +355,12 @@ class DeltaCache:
         o = torch.empty((B, T, self.Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16,
                         device=x.device)
         if self.record:
-            states = torch.empty((B, self.Hv, T, HEAD_DIM, HEAD_DIM), dtype=torch.float32,
+            states = torch.empty((T, B, self.Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32,
                                  device=x.device)
             args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,
                               conv_state_in=self.conv, a=a, b=b, A_log=A_log, dt_bias=dt_bias,
-                              state_in=self.state, states=states, o=o, stream=stream)
+                              state_in=self.state, states=states, states_layout=STATES_TBH,
+                              o=o, stream=stream)
             call_run(args)
             self.base_offset = self.offset
             self.pending = (x, states, T)
@@ -376,8 +381,11 @@ class DeltaCache:
         x, states, T = self.pending
         if n < 0 or n > T:
             raise GdnError(GDN_EINVAL, "DeltaCache::commit out of range")
-        commit(n=n, T=T, states=states, state_prev=self.state, state_dst=self.state, x=x,
-               conv_state_in=self.conv, conv_state_dst=self.conv, stream=stream)
+        adopted = self.state if n == 0 else states[n - 1]   # the pointer swap
+        commit(n=n, T=T, states=states, state_prev=self.state, state_dst=adopted, x=x,
+               conv_state_in=self.conv, conv_state_dst=self.conv, states_layout=STATES_TBH,
+               stream=stream)
+        self.state = adopted
         self.offset = self.base_offset + n
         self.pending = None
         self.record = False

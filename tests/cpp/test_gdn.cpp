@@ -141,19 +141,27 @@ void test_cache() {
       memcpy(&h[(size_t)bb * n * width], &src[((size_t)bb * (T + 1) + t0) * width], (size_t)n * width * 2);
     return to_dev(h);
   };
-  for (int j : {0, 2, 5}) {
+  // two speculative rounds in a row (the block is tokens 0..T-1 both times): the first
+  // commit adopts its state by pointer, the second block is recorded into the other buffer
+  const int rounds[4][2] = {{0, 3}, {2, 5}, {5, 1}, {3, 0}};
+  for (const auto& jj : rounds) {
     gdn::DeltaCache spec(p, B, T), plain(p, B, 0);
     uint16_t* xb = block(x, 0, T, C);
     uint16_t* ab = block(a, 0, T, Hv);
     uint16_t* bb_ = block(b, 0, T, Hv);
-    spec.record = true;
-    spec.step(xb, ab, bb_, T, o, nullptr);
-    spec.commit(j, nullptr);
-    for (int t = 0; t < j; ++t) {
-      uint16_t *xt = token(x, t, C), *at = token(a, t, Hv), *bt = token(b, t, Hv);
-      plain.step(xt, at, bt, 1, o, nullptr);
-      gdn::check_hip(hipDeviceSynchronize(), "sync");
-      (void)hipFree(xt); (void)hipFree(at); (void)hipFree(bt);
+    bool swapped = true;
+    for (int j : jj) {
+      const float* before = spec.state();
+      spec.record = true;
+      spec.step(xb, ab, bb_, T, o, nullptr);
+      spec.commit(j, nullptr);
+      swapped = swapped && ((j > 0) == (spec.state() != before));
+      for (int t = 0; t < j; ++t) {
+        uint16_t *xt = token(x, t, C), *at = token(a, t, Hv), *bt = token(b, t, Hv);
+        plain.step(xt, at, bt, 1, o, nullptr);
+        gdn::check_hip(hipDeviceSynchronize(), "sync");
+        (void)hipFree(xt); (void)hipFree(at); (void)hipFree(bt);
+      }
     }
     uint16_t *xt = token(x, T, C), *at = token(a, T, Hv), *bt = token(b, T, Hv);
     spec.step(xt, at, bt, 1, o, nullptr);
@@ -163,10 +171,12 @@ void test_cache() {
     const auto s2 = to_host(plain.state(), plain.state_bytes() / 4);
     const auto c1 = to_host((const uint16_t*)spec.conv(), spec.conv_bytes() / 2);
     const auto c2 = to_host((const uint16_t*)plain.conv(), plain.conv_bytes() / 2);
-    char buf[160];
-    snprintf(buf, sizeof(buf), "commit(%d) then one step == plain decoding of %d tokens (offset %d)", j, j,
-             spec.offset);
-    check(s1 == s2 && c1 == c2 && spec.offset == plain.offset && spec.offset == j + 1, buf);
+    char buf[200];
+    snprintf(buf, sizeof(buf),
+             "commit(%d), commit(%d) then one step == plain decoding of %d + %d tokens (offset %d)", jj[0],
+             jj[1], jj[0], jj[1], spec.offset);
+    check(s1 == s2 && c1 == c2 && spec.offset == plain.offset && spec.offset == jj[0] + jj[1] + 1, buf);
+    check(swapped, "commit(n > 0) adopts the recorded state by pointer, commit(0) keeps the state");
     for (uint16_t* ptr : {xb, ab, bb_, xt, at, bt}) (void)hipFree(ptr);
   }
   bool threw = false;

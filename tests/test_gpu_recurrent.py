@@ -240,6 +240,18 @@ def test_verify_b8_t5_conv_with_commit(O, gdn, dev, tbh):
             assert np.array_equal(to_np(S), st[:, :, n - 1])
         check_state(O, to_np(S), S_ref, f"commit({n}) state")
         assert np.array_equal(to_np(conv), conv_ref)
+        if tbh and n > 0:
+            # the pointer swap: the destination is step n-1's block itself; nothing moves
+            # but the conv window
+            states_dev = to_dev(out["states"], dev)
+            conv = to_dev(inp.conv_state, dev)
+            dst = states_dev[0, n - 1]
+            gdn.commit(n=n, T=5, states=states_dev[0], state_prev=to_dev(inp.state, dev),
+                       state_dst=dst, x=x, conv_state_in=conv, conv_state_dst=conv,
+                       states_layout=gdn.STATES_TBH)
+            torch.cuda.synchronize()
+            assert np.array_equal(to_np(states_dev), out["states"])
+            assert np.array_equal(to_np(conv), conv_ref)
 
 
 @pytest.mark.parametrize("B,L,H", [(1, 1, 48), (1, 4, 48), (1, 9, 48), (2, 3, 16), (1, 64, 48),
@@ -321,34 +333,43 @@ def test_in_place_equals_out_of_place_multi_layer(O, gdn, dev):
 
 
 def test_deltacache_spec_equals_plain(O, gdn, dev):
-    """The verify contract (session.cpp:476-515): record a 5-token block, commit(j), then
-    decode on; the cache must equal one that decoded the j accepted tokens directly."""
+    """The verify contract (session.cpp:476-515): record a 5-token block, commit(j), again
+    for a second block, then decode on; the cache must equal one that decoded the accepted
+    tokens directly. commit(j > 0) adopts the recorded state by pointer (no copy)."""
     import torch
-    log_case("DeltaCache record/commit == plain decode")
+    log_case("DeltaCache record/commit (two rounds) == plain decode")
     B = 2
     inp = O.make_inputs(config=3, layer=4, B=B, L=6, conv=True)
     w = to_dev(inp.conv_w, dev)
     Al, dt = to_dev(inp.A_log, dev), to_dev(inp.dt_bias, dev)
     x = to_dev(inp.x, dev)
     a, b = to_dev(inp.a, dev), to_dev(inp.b, dev)
-    for j in (0, 2, 5):
+    blk = lambda t: t[:, :5].contiguous()  # noqa: E731
+    tok = lambda t, i: t[:, i:i + 1].contiguous()  # noqa: E731
+    for j1, j2 in ((0, 3), (2, 5), (5, 1), (3, 0)):
         spec = gdn.DeltaCache(B, device=dev)
         plain = gdn.DeltaCache(B, device=dev)
         for c in (spec, plain):
             c.state.copy_(to_dev(inp.state, dev))
             c.conv.copy_(to_dev(inp.conv_state, dev))
-        spec.record = True
-        spec.step(x[:, :5].contiguous(), w, a[:, :5].contiguous(), b[:, :5].contiguous(), Al, dt)
-        spec.commit(j)
-        for t in range(j):
-            plain.step(x[:, t:t + 1].contiguous(), w, a[:, t:t + 1].contiguous(),
-                       b[:, t:t + 1].contiguous(), Al, dt)
-        assert spec.offset == plain.offset == j
-        o1 = spec.step(x[:, 5:6].contiguous(), w, a[:, 5:6].contiguous(), b[:, 5:6].contiguous(), Al, dt)
-        o2 = plain.step(x[:, 5:6].contiguous(), w, a[:, 5:6].contiguous(), b[:, 5:6].contiguous(), Al, dt)
+        for j in (j1, j2):
+            spec.record = True
+            spec.step(blk(x), w, blk(a), blk(b), Al, dt)
+            states = spec.pending[1]
+            before = spec.state.data_ptr()
+            spec.commit(j)
+            if j > 0:
+                assert spec.state.data_ptr() == states[j - 1].data_ptr()   # adopted in place
+            else:
+                assert spec.state.data_ptr() == before
+            for t in range(j):
+                plain.step(tok(x, t), w, tok(a, t), tok(b, t), Al, dt)
+        assert spec.offset == plain.offset == j1 + j2
+        o1 = spec.step(tok(x, 5), w, tok(a, 5), tok(b, 5), Al, dt)
+        o2 = plain.step(tok(x, 5), w, tok(a, 5), tok(b, 5), Al, dt)
         torch.cuda.synchronize()
         assert torch.equal(spec.conv.view(torch.int16), plain.conv.view(torch.int16))
-        assert torch.equal(spec.state, plain.state), j
+        assert torch.equal(spec.state, plain.state), (j1, j2)
         assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
 
 
