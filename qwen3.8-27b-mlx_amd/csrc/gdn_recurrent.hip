@@ -34,6 +34,10 @@ namespace gdn {
 namespace {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+// cache-policy operand of the buffer store builtins: bit 4 = sc1 (device scope)
+constexpr int kCachePolicySc1 = 16;
 
 constexpr int kTileRows = 64;                 // Dv rows per workgroup
 constexpr int kTilesPerHead = kD / kTileRows; // 2
@@ -128,8 +132,48 @@ __device__ __forceinline__ void load_state(const RecurrentParams& p, const Tile&
   }
 }
 
+// State stores come in two cache policies. Non-temporal stores are written back: the
+// lines stay in the L2 of the XCD that wrote them until evicted, and what is still there
+// when the kernel ends is written back after its last wave (the 8 XCDs' L2s are not
+// coherent with each other), which lengthens a launch by up to the L2s' 32 MB at HBM
+// speed. Device-scope stores (sc1) write through instead, at a somewhat lower streaming
+// rate. So the bulk of a large grid writes back and its tail writes through: the
+// workgroups dispatched last (highest block ids) write the final kWtTailBytes of state.
+// Measured on MI355X, 48-layer B=1 decode: 56.0 -> 53.0 us. Small grids (a single-layer
+// decode: 3 MB) write back throughout -- there write-through is slower.
+constexpr unsigned kWtTailBytes = 40u << 20;
+constexpr unsigned kWtTailGroups = kWtTailBytes / (kTileRows * kD * 4);  // 1280 workgroups
+constexpr unsigned kWtMinGroups = 1024;
+// A collecting launch whose whole grid is resident at once (256 CUs x 8 workgroups) writes
+// every per-step state through (the verify block B = 8, T = 5: 126 MB of per-step states,
+// 32.1 -> 26.4 us); a larger one writes its last step through.
+constexpr unsigned kResidentGroups = 2048;
+constexpr unsigned long long kWtMinCollectBytes = 16ull << 20;
+
+// The grid-size conditions are taken on the host (kernels are instantiated with a WT flag,
+// so a grid that never writes through keeps the plain store code and its registers); the
+// per-workgroup part is taken here.
+__device__ __forceinline__ bool tail_write_through() { return blockIdx.x + kWtTailGroups >= gridDim.x; }
+
+__device__ __forceinline__ bool collect_write_through(const RecurrentParams& p, int step) {
+  return gridDim.x <= kResidentGroups || step == p.T - 1;
+}
+
 __device__ __forceinline__ void store_rows(float* base, const Tile& t, int wave, int grp, int j16,
-                                           const f4v (&s)[kSlots][2]) {
+                                           const f4v (&s)[kSlots][2], bool write_through) {
+  if (write_through) {
+    // buffer stores with sc1 (device scope); every offset is inside the 64 KB state
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, kD * kD * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int row = t.r0 + row_of(wave, i, grp);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, s[i][hf]), rs,
+                                               (row * kD + hf * 64 + j16 * 4) * 4, 0, kCachePolicySc1);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
     const int row = t.r0 + row_of(wave, i, grp);
@@ -166,7 +210,7 @@ __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const T
   }
 }
 
-template <bool COLLECT>
+template <bool COLLECT, bool WT>
 __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
                                            float al, float be, const float* kk, const float* qq,
                                            const float* vv, int wave, int grp, int j16,
@@ -210,7 +254,7 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
     float* dst = p.states_tbh
                      ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
                      : p.states + (t.head * p.T + step) * kD * kD;
-    store_rows(dst, t, wave, grp, j16, s);
+    store_rows(dst, t, wave, grp, j16, s, WT && collect_write_through(p, step));
   }
   // lane j (< kSlots) of each group writes the output of slot j
   if (j16 < kSlots) {
@@ -291,7 +335,7 @@ __device__ __forceinline__ int fe_channel(const RecurrentParams& p, const Tile& 
 
 // ---------------------------------------------------------------- decode, T = 1
 
-template <int FE>
+template <int FE, bool WT>
 __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   __shared__ float sm_q[kD];
   __shared__ float sm_k[kD];
@@ -378,8 +422,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   __syncthreads();
 
   // 4. the step, then the state goes back
-  apply_step<false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
-  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+  apply_step<false, false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
+  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s, WT && tail_write_through());
 
   // 5. conv state hand-off from the rows already in registers: new rows 0..2 are xp
   // rows 1..3. This tile's v channels; the q (tile 0) or k (tile 1) channels of the
@@ -403,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
 
 // ---------------------------------------------------------------- any T (verify, prefill-size L)
 
-template <int FE, bool COLLECT>
+template <int FE, bool COLLECT, bool WT>
 __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
   __shared__ float sm_q[kTC][kD];
   __shared__ float sm_k[kTC][kD];
@@ -511,12 +555,14 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     __syncthreads();
 
     for (int tt = 0; tt < tc; ++tt) {
-      apply_step<COLLECT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave,
+      apply_step<COLLECT, WT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave,
                           grp, j16, s);
     }
   }
 
-  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+  if (p.state_out)
+    store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s,
+               WT && (COLLECT ? collect_write_through(p, p.T - 1) : tail_write_through()));
   if (FE == 1 && p.conv_out) write_conv_out(p, t, x_b, cin_b);
 }
 
@@ -537,27 +583,36 @@ __global__ void copy_u16_kernel(uint16_t* __restrict__ dst, const uint16_t* __re
 
 }  // namespace
 
+template <int FE>
+static void launch_steps(const RecurrentParams& p, bool collect, bool wt, dim3 grid, dim3 block, hipStream_t stream) {
+  if (collect) {
+    if (wt) hipLaunchKernelGGL((steps_kernel<FE, true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((steps_kernel<FE, true, false>), grid, block, 0, stream, p);
+  } else {
+    if (wt) hipLaunchKernelGGL((steps_kernel<FE, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((steps_kernel<FE, false, false>), grid, block, 0, stream, p);
+  }
+}
+
 hipError_t launch_recurrent(const RecurrentParams& p, int frontend, bool collect,
                             hipStream_t stream) {
   const dim3 grid(p.nblocks), block(kThreads);
+  // write-through is possible for a large grid's tail, or for a collecting launch that
+  // writes enough per-step states
+  const bool wt = collect ? (unsigned long long)p.nblocks * p.T * (kTileRows * kD * 4) >= kWtMinCollectBytes
+                          : p.nblocks >= (int)kWtMinGroups;
   if (p.T == 1 && !collect) {
     if (frontend == 0) {
-      hipLaunchKernelGGL((decode_kernel<0>), grid, block, 0, stream, p);
+      if (wt) hipLaunchKernelGGL((decode_kernel<0, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((decode_kernel<0, false>), grid, block, 0, stream, p);
     } else {
-      hipLaunchKernelGGL((decode_kernel<1>), grid, block, 0, stream, p);
+      if (wt) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((decode_kernel<1, false>), grid, block, 0, stream, p);
     }
   } else if (frontend == 0) {
-    if (collect) {
-      hipLaunchKernelGGL((steps_kernel<0, true>), grid, block, 0, stream, p);
-    } else {
-      hipLaunchKernelGGL((steps_kernel<0, false>), grid, block, 0, stream, p);
-    }
+    launch_steps<0>(p, collect, wt, grid, block, stream);
   } else {
-    if (collect) {
-      hipLaunchKernelGGL((steps_kernel<1, true>), grid, block, 0, stream, p);
-    } else {
-      hipLaunchKernelGGL((steps_kernel<1, false>), grid, block, 0, stream, p);
-    }
+    launch_steps<1>(p, collect, wt, grid, block, stream);
   }
   return hipGetLastError();
 }
