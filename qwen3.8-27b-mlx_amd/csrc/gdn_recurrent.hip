@@ -145,19 +145,16 @@ constexpr unsigned kWtTailBytes = 40u << 20;
 constexpr unsigned kWtTailGroups = kWtTailBytes / (kTileRows * kD * 4);  // 1280 workgroups
 constexpr unsigned kWtMinGroups = 1024;
 // A collecting launch whose whole grid is resident at once (256 CUs x 8 workgroups) writes
-// every per-step state through (the verify block B = 8, T = 5: 126 MB of per-step states,
-// 32.1 -> 26.4 us); a larger one writes its last step through.
+// all its per-step states through (the verify block B = 8, T = 5, 126 MB of per-step
+// states: 32.1 -> 30.5 us); a larger one writes back throughout (through was slower there:
+// the last step through, 4 layers: 122.5 -> 127 us).
 constexpr unsigned kResidentGroups = 2048;
 constexpr unsigned long long kWtMinCollectBytes = 16ull << 20;
 
 // The grid-size conditions are taken on the host (kernels are instantiated with a WT flag,
 // so a grid that never writes through keeps the plain store code and its registers); the
-// per-workgroup part is taken here.
+// tail's per-workgroup test is taken here.
 __device__ __forceinline__ bool tail_write_through() { return blockIdx.x + kWtTailGroups >= gridDim.x; }
-
-__device__ __forceinline__ bool collect_write_through(const RecurrentParams& p, int step) {
-  return gridDim.x <= kResidentGroups || step == p.T - 1;
-}
 
 __device__ __forceinline__ void store_rows(float* base, const Tile& t, int wave, int grp, int j16,
                                            const f4v (&s)[kSlots][2], bool write_through) {
@@ -254,7 +251,7 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
     float* dst = p.states_tbh
                      ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
                      : p.states + (t.head * p.T + step) * kD * kD;
-    store_rows(dst, t, wave, grp, j16, s, WT && collect_write_through(p, step));
+    store_rows(dst, t, wave, grp, j16, s, WT);
   }
   // lane j (< kSlots) of each group writes the output of slot j
   if (j16 < kSlots) {
@@ -562,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
 
   if (p.state_out)
     store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s,
-               WT && (COLLECT ? collect_write_through(p, p.T - 1) : tail_write_through()));
+               WT && (COLLECT || tail_write_through()));
   if (FE == 1 && p.conv_out) write_conv_out(p, t, x_b, cin_b);
 }
 
@@ -597,9 +594,10 @@ static void launch_steps(const RecurrentParams& p, bool collect, bool wt, dim3 g
 hipError_t launch_recurrent(const RecurrentParams& p, int frontend, bool collect,
                             hipStream_t stream) {
   const dim3 grid(p.nblocks), block(kThreads);
-  // write-through is possible for a large grid's tail, or for a collecting launch that
-  // writes enough per-step states
-  const bool wt = collect ? (unsigned long long)p.nblocks * p.T * (kTileRows * kD * 4) >= kWtMinCollectBytes
+  // write-through: a large grid's tail, or every per-step state of a collecting launch that
+  // is resident at once and writes enough of them
+  const bool wt = collect ? (unsigned long long)p.nblocks * p.T * (kTileRows * kD * 4) >= kWtMinCollectBytes &&
+                                p.nblocks <= (int)kResidentGroups
                           : p.nblocks >= (int)kWtMinGroups;
   if (p.T == 1 && !collect) {
     if (frontend == 0) {
