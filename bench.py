@@ -368,7 +368,7 @@ def main() -> int:
         r = bench_verify(torch, gdn, dev, timer, steps=args.steps, warmup=args.warmup, sets=4)
         sec["verify_b8_t5"] = dict(GBps=round(r["GBps"], 1), frac_hbm=round(r["GBps"] / HBM_PEAK_GBPS, 4),
                                    us_per_call=round(r["ms_per_step"] * 1e3, 2),
-                                   bytes_per_call=r["bytes_per_step"])
+                                   bytes_per_call=r["bytes_per_step"], traffic=load_traffic("verify_b8_t5"))
         print(f"# verify B=8 T=5: {r['ms_per_step'] * 1e3:.1f} us, {r['GBps']:.0f} GB/s", flush=True)
     if want("prefill"):
         r = bench_prefill(torch, gdn, dev, timer, steps=max(5, args.steps // 10), warmup=3)
