@@ -131,15 +131,15 @@ int gdn_run(const gdn_layer_args* args);
 
 /* Chunked form (chunk 64, WY/UT transform) for prefill; same arguments as gdn_run
  * except that `states` must be NULL, a workspace is required, x and conv_state_in (conv
- * front end) or q and k (qkv front end) must be 16-byte aligned, and the qkv front end
+ * front end) or q, k and v (qkv front end) must be 16-byte aligned, and the qkv front end
  * takes bf16 q, k, v only. Intra-chunk products run on bf16 MFMA with fp32 accumulation;
  * the state hand-off between chunks stays fp32. The workspace contents are scratch: they
  * need no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);
 
 /* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
- * counts and front end (the conv front end stages its bf16 q, k, v in the workspace); the
- * other fields are not read. */
+ * counts and front end (the conv front end also stages its bf16 q, k in the workspace);
+ * the other fields are not read. */
 int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {

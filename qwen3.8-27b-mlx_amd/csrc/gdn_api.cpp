@@ -276,8 +276,8 @@ int gdn_prefill_chunked(const gdn_layer_args* a) {
     return fail(GDN_EINVAL, "gdn_prefill_chunked: the qkv front end takes bf16 q, k, v");
   if (a->frontend == GDN_FRONTEND_CONV && (!aligned(a->x, 16) || !aligned(a->conv_state_in, 16)))
     return fail(GDN_EINVAL, "gdn_prefill_chunked: x and conv_state_in must be 16-byte aligned");
-  if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16)))
-    return fail(GDN_EINVAL, "gdn_prefill_chunked: q and k must be 16-byte aligned");
+  if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16)))
+    return fail(GDN_EINVAL, "gdn_prefill_chunked: q, k and v must be 16-byte aligned");
   const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads,
                                                    a->num_v_heads, a->frontend == GDN_FRONTEND_CONV);
   if (a->seq_len > 0) {

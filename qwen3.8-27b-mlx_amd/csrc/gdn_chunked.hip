@@ -10,16 +10,21 @@
 //   y  = e^G . (Q S) + M V'                              (= MU0 + Qeff S)
 //   S  = e^{G_63} S + K^T (e^{G_63 - G} . V')
 //
-// Two kernels:
+// Three kernels, one stream:
+//   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position into bf16 q, k
+//                  (B, T, Hk, 128) and v, which goes straight into the fragment order of
+//                  U's B operand (with q, k, v given by the caller, prefill_vfrag reorders
+//                  v instead).
 //   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
-//                  per CU: the conv front end for q, k, v (or the given q, k, v), K K^T and
-//                  K Q^T on bf16 MFMA, and for the k-head's v-heads the gates, A and M,
-//                  T = (I + A)^-1 (one wave per v-head, fp32), U and W (bf16 MFMA, T'
-//                  split into bf16 hi + lo for U). Results go to the workspace, already in
-//                  the register order of the MFMA operands that read them.
+//                  per CU: K K^T and K Q^T on bf16 MFMA, and for the k-head's v-heads the
+//                  gates, A and M, T = (I + A)^-1 (one wave per v-head, fp32, left in LDS),
+//                  U = T'V and W = T'diag(e^G)K on bf16 MFMA, every wave building its T'
+//                  fragments from T in LDS (T' split into bf16 hi + lo for U). Results go
+//                  to the workspace, already in the register order of the MFMA operands
+//                  that read them.
 //   prefill_scan   one workgroup per (batch, v-head, 32-column Dv tile), serial over the
 //                  chunks; the fp32 state tile lives in MFMA accumulators. Each chunk's
-//                  operands go from the workspace straight into registers, one chunk
+//                  operands go from the workspace straight into registers, two chunks
 //                  ahead of their use; LDS holds only the operands all four waves share
 //                  (S^T and V'). W S, Q S and K^T V'' use bf16 operands; M V' splits both
 //                  operands into bf16 hi + lo (three MFMAs).
@@ -98,6 +103,9 @@ struct PrefillParams {
   __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64) in fragment order, hi and lo blocks interleaved
   float* ws_u;    // (B, Hv, nC): U   (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]
   float* ws_g;    // (B, Hv, nC, kGStride): e^G [64], e^(G63-G) [64], e^G63
+  __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
+                  // block 2 (dv / 16) + pos / 32, lane 16 ((pos % 32) / 8) + dv % 16, element
+                  // pos % 8; positions past T are zeros
 };
 
 // Causal depthwise conv from 4 rows (model.cpp:385-395), bf16 after every op.
@@ -140,18 +148,14 @@ struct IntraSmem {
   __bf16 kt[kD][kC + kPadB];  // K^T [dk][pos]
   float G[kGroup][kC];
   float beta[kGroup][kC];
+  float eG[kGroup][kC];  // e^G
   union {
     struct {
       __bf16 q[kC][kD + kPadB];
       __bf16 k[kC][kD + kPadB];
     } fe;
-    float nat[kGroup][kC][kC + 4];  // -A^T per v-head: [j][i] = -A_ij
-    struct {
-      __bf16 th[kC][kC + kPadB];  // T' hi
-      __bf16 tl[kC][kC + kPadB];  // T' lo
-      __bf16 te[kC][kC + kPadB];  // T' diag(e^G)
-      __bf16 vt[kD][kC + kPadB];  // V^T [dv][pos]
-    } pr;
+    // per v-head: -A^T ([j][i] = -A_ij) for the inverse, then T = (I + A)^-1 ([i][j]) over it
+    float nat[kGroup][kC][kC + 4];
   } u;
 };
 
@@ -159,9 +163,11 @@ struct IntraSmem {
 
 constexpr int kFePos = 32;   // positions per front-end workgroup
 constexpr int kFeHeads = 4;  // heads of 128 channels per front-end workgroup (one per wave)
+static_assert(kC == 2 * kFePos, "a chunk is two front-end position blocks");
 
 // Conv + SiLU, and l2norm for q and k (q also scaled by 128^-0.5), bf16 after every op
-// (model.cpp:585-602), into bf16 q (B,T,Hk,128), k (B,T,Hk,128), v (B,T,Hv,128).
+// (model.cpp:585-602), into bf16 q (B,T,Hk,128), k (B,T,Hk,128) and v in the fragment order
+// of ws_vf.
 // Workgroup: (batch, 32 positions, 4 of the 2 Hk + Hv heads in channel order q, k, v);
 // wave w takes one head; lane l takes positions 8 (l / 16) .. +7 of the block and the
 // head's channels {4m .. 4m+3} and {64+4m .. 64+4m+3}, m = l % 16. The l2norm sum keeps
@@ -169,7 +175,12 @@ constexpr int kFeHeads = 4;  // heads of 128 channels per front-end workgroup (o
 // four pairs as ((p0 + p1) + (p2 + p3)) (the first two butterfly steps), then the DPP
 // row sum does the remaining four. The workgroup holding position T-1 also writes the
 // conv state hand-off (rows T-3..T-1 of [conv_in ; x]) for its heads.
-__global__ __launch_bounds__(kThreads) void prefill_frontend_kernel(PrefillParams p) {
+// A v head's outputs go through the wave's LDS tile ([channel][position]), so that each
+// lane then writes eight positions of one channel as one 16-byte piece of the fragment
+// order (the q/k and v paths share the conv and SiLU code and their registers). At most 128
+// VGPRs: four waves per SIMD for this VALU-bound kernel.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_frontend_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) __bf16 vtile[kFeHeads][kD][kFePos + 8];
   const int nheads = 2 * p.Hk + p.Hv;
   const int hgroups = (nheads + kFeHeads - 1) / kFeHeads;
   const int pblocks = (p.T + kFePos - 1) / kFePos;
@@ -205,20 +216,13 @@ __global__ __launch_bounds__(kThreads) void prefill_frontend_kernel(PrefillParam
   }
   const bool norm = hh < 2 * p.Hk;
   const bool is_q = hh < p.Hk;
-  __bf16* dst;
-  size_t pstride;
-  if (is_q) {
-    dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
-    pstride = (size_t)p.Hk * kD;
-  } else if (norm) {
-    dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
-    pstride = (size_t)p.Hk * kD;
-  } else {
-    dst = const_cast<__bf16*>(p.v) + ((size_t)b * p.T * p.Hv + (hh - 2 * p.Hk)) * kD;
-    pstride = (size_t)p.Hv * kD;
-  }
+  __bf16* dst = nullptr;
+  if (is_q) dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
+  else if (norm) dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
+  const size_t pstride = (size_t)p.Hk * kD;
   const float scale_b = rbf(1.0f / sqrtf((float)kD));
   const float eps_b = rbf(1e-6f);
+  auto& vt = vtile[wave];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     float u[8];  // channels 4m + e (e < 4) and 64 + 4m + (e - 4)
@@ -228,8 +232,9 @@ __global__ __launch_bounds__(kThreads) void prefill_frontend_kernel(PrefillParam
       u[4 + e] = conv4_rows(bf2f(r1[t][e]), bf2f(r1[t + 1][e]), bf2f(r1[t + 2][e]), bf2f(r1[t + 3][e]), w1[e]);
     }
     silu_bf_batch(u);
-    f4 y0 = {u[0], u[1], u[2], u[3]}, y1 = {u[4], u[5], u[6], u[7]};
+    const int pos = p0 + t;
     if (norm) {
+      f4 y0 = {u[0], u[1], u[2], u[3]}, y1 = {u[4], u[5], u[6], u[7]};
       float pr[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) pr[e] = rbf(u[e] * u[e]) + rbf(u[4 + e] * u[4 + e]);
@@ -245,12 +250,32 @@ __global__ __launch_bounds__(kThreads) void prefill_frontend_kernel(PrefillParam
           y1[e] = rbf(y1[e] * scale_b);
         }
       }
+      if (pos < p.T) {
+        __bf16* o = dst + (size_t)pos * pstride;
+        *reinterpret_cast<bf4*>(o + 4 * m) = to_bf4(y0);
+        *reinterpret_cast<bf4*>(o + 64 + 4 * m) = to_bf4(y1);
+      }
+    } else {
+      const int tp = 8 * (lane >> 4) + t;  // position within the block
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[4 * m + e][tp] = pos < p.T ? (__bf16)u[e] : (__bf16)0.0f;
+        vt[64 + 4 * m + e][tp] = pos < p.T ? (__bf16)u[4 + e] : (__bf16)0.0f;
+      }
     }
-    const int pos = p0 + t;
-    if (pos < p.T) {
-      __bf16* o = dst + (size_t)pos * pstride;
-      *reinterpret_cast<bf4*>(o + 4 * m) = to_bf4(y0);
-      *reinterpret_cast<bf4*>(o + 64 + 4 * m) = to_bf4(y1);
+  }
+  if (!norm) {
+    // v: the B operand of U = T' V in fragment order (block 2 (dv / 16) + half chunk, lane
+    // 16 (position / 8) + dv % 16); this wave's LDS tile, written above by this wave only
+    const int hv = hh - 2 * p.Hk;
+    const int kh = pb & 1;  // which half of the 64-position chunk (kFePos = kC / 2)
+    __bf16* vf = p.ws_vf + (((size_t)b * p.Hv + hv) * p.nC + pb / 2) * kChunkElems;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int piece = 64 * i + lane;          // (dv tile, lane of the fragment)
+      const int dv = 16 * (piece >> 6) + (lane & 15), pg = lane >> 4;
+      *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + kh) * kFrag + lane * 8) =
+          *reinterpret_cast<const bf8*>(&vt[dv][8 * pg]);
     }
   }
   if (p.conv_out && pb == pblocks - 1) {
@@ -385,9 +410,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       }
       s.G[wave][lane] = G;
       s.beta[wave][lane] = be;
+      const float eg = d_expf(G);
+      s.eG[wave][lane] = eg;
       const float Gl = __shfl(G, 63, 64);
       float* wg = p.ws_g + hc * kGStride;
-      wg[lane] = d_expf(G);
+      wg[lane] = eg;
       wg[64 + lane] = d_expf(Gl - G);
       if (lane == 0) wg[128] = d_expf(Gl);
     }
@@ -422,61 +449,82 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
     __syncthreads();
 
-    // T = (I + A)^-1: wave r inverts v-head r0 + r, lane j = column j
-    float x[kC];
-    if (wave < gs) invert_column(s.u.nat[wave], lane, x);
+    // T = (I + A)^-1: wave r inverts v-head r0 + r, lane j = column j, and writes T over
+    // its own -A^T as [i][j] (only this wave has read that slot)
+    if (wave < gs) {
+      float x[kC];
+      invert_column(s.u.nat[wave], lane, x);
+#pragma unroll
+      for (int i = 0; i < kC; ++i) s.u.nat[wave][i][lane] = x[i];
+    }
     __syncthreads();
 
     for (int r = 0; r < gs; ++r) {
       const int h = g * p.rep + r0 + r;
       const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
+      // V: the B operand of U, straight from the workspace (a half chunk wholly past T was
+      // never written: zeros)
+      bf8 vb[kD / 16][2];
       {
-        const int dv = tid & (kD - 1), ph = (tid >> 7) * 32;
+        const __bf16* vf = p.ws_vf + hc * kChunkElems + lane * 8;
 #pragma unroll
-        for (int q8 = 0; q8 < 4; ++q8) {
-          bf8 v;
+        for (int d = 0; d < kD / 16; ++d)
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+            vb[d][kh] = 32 * kh < n ? *reinterpret_cast<const bf8*>(vf + (2 * d + kh) * kFrag) : bf8{};
+      }
+      // column factors of T' = T diag(beta) and T' diag(e^G) for this lane's columns
+      // j = 32 kh + fk + e
+      float bj[2][8], ej[2][8];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          bj[kh][e] = s.beta[r][32 * kh + fk + e];
+          ej[kh][e] = s.eG[r][32 * kh + fk + e];
+        }
+      // U = T' V: wave w takes position tile w, all eight dv tiles; T' split into hi + lo
+      {
+        bf8 ah[2], al[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const float* xr = &s.u.nat[r][16 * wave + fr][32 * kh + fk];
+          const f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const int pos = ph + 8 * q8 + e;
-            const __bf16 val = p.v[(((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hv + h) * kD + dv];
-            v[e] = pos < n ? val : (__bf16)0.0f;
+            const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
+            const __bf16 hi = (__bf16)tv;
+            ah[kh][e] = hi;
+            al[kh][e] = (__bf16)(tv - (float)hi);
           }
-          *reinterpret_cast<bf8*>(&s.u.pr.vt[dv][ph + 8 * q8]) = v;
         }
-      }
-      if (wave == r) {
-        // T' = T diag(beta) (hi + lo) and T' diag(e^G), column j = lane
-        const float bj = s.beta[r][lane];
-        const float ej = d_expf(s.G[r][lane]);
-#pragma unroll
-        for (int i = 0; i < kC; ++i) {
-          const float tv = x[i] * bj;
-          const __bf16 hi = (__bf16)tv;
-          s.u.pr.th[i][lane] = hi;
-          s.u.pr.tl[i][lane] = (__bf16)(tv - (float)hi);
-          s.u.pr.te[i][lane] = (__bf16)(tv * ej);
-        }
-      }
-      __syncthreads();
-      // U = T' V: wave w takes position tile w, all eight dv tiles
-      {
-        const bf8 ah0 = frag(s.u.pr.th, 16 * wave + fr, fk), ah1 = frag(s.u.pr.th, 16 * wave + fr, 32 + fk);
-        const bf8 al0 = frag(s.u.pr.tl, 16 * wave + fr, fk), al1 = frag(s.u.pr.tl, 16 * wave + fr, 32 + fk);
         float* wu = p.ws_u + hc * kChunkElems + lane * 4;
 #pragma unroll
         for (int d = 0; d < kD / 16; ++d) {
-          const bf8 b0 = frag(s.u.pr.vt, 16 * d + fr, fk), b1 = frag(s.u.pr.vt, 16 * d + fr, 32 + fk);
           f4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mfma(ah0, b0, acc);
-          acc = mfma(al0, b0, acc);
-          acc = mfma(ah1, b1, acc);
-          acc = mfma(al1, b1, acc);
+          acc = mfma(ah[0], vb[d][0], acc);
+          acc = mfma(al[0], vb[d][0], acc);
+          acc = mfma(ah[1], vb[d][1], acc);
+          acc = mfma(al[1], vb[d][1], acc);
           *reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256) = acc;
         }
       }
       // W^T = K^T (T' e^G)^T: wave w takes dk tiles 2w, 2w+1, all position tiles; lane
       // gets W[i = 16 bt + fr][dk = 16 a + 4 lg .. +3]
       {
+        bf8 te[4][2];
+#pragma unroll
+        for (int bt = 0; bt < 4; ++bt)
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            const float* xr = &s.u.nat[r][16 * bt + fr][32 * kh + fk];
+            const f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
+              te[bt][kh][e] = (__bf16)(tv * ej[kh][e]);
+            }
+          }
         __bf16* ww = p.ws_w + hc * kChunkElems;
 #pragma unroll
         for (int a2 = 0; a2 < 2; ++a2) {
@@ -485,14 +533,49 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
 #pragma unroll
           for (int bt = 0; bt < 4; ++bt) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = mfma(k0, frag(s.u.pr.te, 16 * bt + fr, fk), acc);
-            acc = mfma(k1, frag(s.u.pr.te, 16 * bt + fr, 32 + fk), acc);
+            acc = mfma(k0, te[bt][0], acc);
+            acc = mfma(k1, te[bt][1], acc);
             *reinterpret_cast<bf4*>(ww + frag_off(16 * bt + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
           }
         }
       }
-      __syncthreads();
     }
+    __syncthreads();  // the next group rewrites G, beta and the LDS union
+  }
+}
+
+// v (B,T,Hv,128) bf16 given by the caller -> ws_vf (the conv front end writes ws_vf itself).
+// Workgroup = (batch, v-head, chunk): the 64 x 128 tile goes to LDS transposed ([dv][pos]),
+// then each thread writes four 16-byte pieces of eight consecutive positions.
+__global__ __launch_bounds__(kThreads) void prefill_vfrag_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) __bf16 vt[kD][kC + kPadB];
+  const int c = blockIdx.x % p.nC;
+  const int rest = blockIdx.x / p.nC;
+  const int h = rest % p.Hv;
+  const int b = rest / p.Hv;
+  const int t0 = c * kC, n = min(kC, p.T - t0);
+  const int tid = threadIdx.x;
+  constexpr int kIt = kC * kD / 8 / kThreads;  // 16-byte pieces per thread
+  bf8 raw[kIt];
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+    raw[it] = *reinterpret_cast<const bf8*>(p.v + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hv + h) * kD + d8);
+  }
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vt[d8 + i][pos] = pos < n ? raw[it][i] : (__bf16)0.0f;
+  }
+  __syncthreads();
+  __bf16* vf = p.ws_vf + (((size_t)b * p.Hv + h) * p.nC + c) * kChunkElems;
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const int e = tid + it * kThreads;        // (block f, lane l) piece
+    const int f = e / 64, l = e % 64;
+    const int dv = 16 * (f / 2) + (l & 15), pos = 32 * (f & 1) + 8 * (l >> 4);
+    *reinterpret_cast<bf8*>(vf + e * 8) = *reinterpret_cast<const bf8*>(&vt[dv][pos]);
   }
 }
 
@@ -728,10 +811,11 @@ __global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p)
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, w, m, u, g, fq, fk, fv, total;
+  size_t q, kt, w, m, u, g, vf, fq, fk, total;
 };
 
-// conv: the conv front end's bf16 q, k, v (B,T,H,128) are staged in the workspace too.
+// conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
+// goes to vf, which the qkv front end fills from the caller's v).
 WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -747,11 +831,10 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
   L.u = L.m + wm;
   L.g = L.u + uu;
   const size_t fqk = conv ? al((size_t)B * T * Hk * kD * 2) : 0;
-  const size_t fv = conv ? al((size_t)B * T * Hv * kD * 2) : 0;
-  L.fq = L.g + gg;
+  L.vf = L.g + gg;
+  L.fq = L.vf + wm;
   L.fk = L.fq + fqk;
-  L.fv = L.fk + fqk;
-  L.total = L.fv + fv;
+  L.total = L.fk + fqk;
   return L;
 }
 
@@ -797,10 +880,11 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
   p.ws_u = reinterpret_cast<float*>(w + L.u);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
+  p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {
     p.q = reinterpret_cast<const __bf16*>(w + L.fq);
     p.k = reinterpret_cast<const __bf16*>(w + L.fk);
-    p.v = reinterpret_cast<const __bf16*>(w + L.fv);
+    p.v = nullptr;  // the front end writes v straight into ws_vf
   }
 
   const dim3 block(kThreads);
@@ -810,6 +894,9 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
     const size_t nh = ((size_t)2 * p.Hk + p.Hv + kFeHeads - 1) / kFeHeads;
     const dim3 g0((unsigned)((size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
     hipLaunchKernelGGL(prefill_frontend_kernel, g0, block, 0, stream, p);
+  } else {
+    const dim3 gv((unsigned)((size_t)p.B * p.Hv * p.nC));
+    hipLaunchKernelGGL(prefill_vfrag_kernel, gv, block, 0, stream, p);
   }
   if (p.rep <= kGroup) {
     hipLaunchKernelGGL((prefill_intra_kernel<true>), g1, block, 0, stream, p);
