@@ -224,11 +224,12 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
                 intra_flop=intra, inter_flop=inter)
 
 
-def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str):
-    """48 layers of the DeltaNet projections at B=1 in one launch: "in_proj" = in_proj_qkv,
-    in_proj_z, in_proj_a, in_proj_b on x (5120); "out_proj" = GatedRMSNorm of o (6144,
-    fp32) with z, then out_proj (5120 rows). Synthetic 4-bit weights (random words, scales
-    and biases in the checkpoint's ranges)."""
+def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str, M: int = 1):
+    """48 layers of the DeltaNet projections for M operand rows in one launch (M = 1: B=1
+    decode, the GEMV kernel; M = 40: a B=8, T=5 verify block, the MFMA kernel): "in_proj" =
+    in_proj_qkv, in_proj_z, in_proj_a, in_proj_b on x (5120); "out_proj" = GatedRMSNorm of
+    o (6144, fp32) with z, then out_proj (5120 rows). Synthetic 4-bit weights (random
+    words, scales and biases in the checkpoint's ranges)."""
     NL = 48
     g = torch.Generator(device=dev)
     g.manual_seed(700 if which == "in_proj" else 701)
@@ -242,24 +243,30 @@ def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str):
     if which == "in_proj":
         K, ns = 5120, [C, HV * D, HV, HV]
         mats = [mat(n, K) for n in ns]
-        x = torch.randn((NL, 1, K), device=dev, generator=g).to(torch.bfloat16)
+        x = torch.randn((NL, M, K), device=dev, generator=g).to(torch.bfloat16)
         args, _ys = gdn.qlinear_args(mats, x, n_layers=NL)
         operand = K * 2
     else:
         K, ns = HV * D, [5120]
         mats = [mat(n, K) for n in ns]
-        o = torch.randn((NL, 1, K), device=dev, generator=g) * 0.3
-        z = torch.randn((NL, 1, K), device=dev, generator=g).to(torch.bfloat16)
+        o = torch.randn((NL, M, K), device=dev, generator=g) * 0.3
+        z = torch.randn((NL, M, K), device=dev, generator=g).to(torch.bfloat16)
         gamma = torch.rand((NL, D), device=dev, generator=g) + 0.5
         args, _ys = gdn.qlinear_args(mats, norm=(o, z, gamma, 1e-6), n_layers=NL)
         operand = K * 4 + K * 2 + D * 4
     r = timer.time_calls(lambda it: gdn.call_qlinear(args), steps, warmup)
-    per_layer = sum(n * K // 2 + n * (K // 64) * 4 + n * 2 for n in ns) + operand
+    # algorithmic bytes: weights, scales and biases once, the operand and the outputs (the
+    # MFMA path's workspace round trip is not counted)
+    per_layer = sum(n * K // 2 + n * (K // 64) * 4 + M * n * 2 for n in ns) + M * operand
     nbytes = NL * per_layer
-    return dict(GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1),
-                frac_hbm=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                us_per_step=round(r["ms_per_step"] * 1e3, 2), bytes_per_step=nbytes,
-                traffic=load_traffic("in_proj_48_layers_b1" if which == "in_proj" else "out_proj_norm_48_layers_b1"))
+    flop = NL * 2 * M * K * sum(ns)
+    out = dict(M=M, GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+               frac_hbm=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+               us_per_step=round(r["ms_per_step"] * 1e3, 2), bytes_per_step=nbytes,
+               TFLOPs=round(flop / (r["ms_per_step"] * 1e-3) / 1e12, 2))
+    if M == 1:
+        out["traffic"] = load_traffic("in_proj_48_layers_b1" if which == "in_proj" else "out_proj_norm_48_layers_b1")
+    return out
 
 
 def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
@@ -324,7 +331,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="comma list: decode1,decode1layer,decode32,verify,prefill,in_proj,"
-                         "out_proj,copy")
+                         "out_proj,in_proj40,out_proj40,copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the gated-delta path "
@@ -380,6 +387,11 @@ def main() -> int:
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)
             sec[f"{which}_48_layers_b1"] = r
             print(f"# {which} x48 B=1 (4-bit): {r['us_per_step']:.1f} us/step, {r['GBps']:.0f} GB/s", flush=True)
+        if want(which + "40"):
+            r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 8), warmup=3, which=which, M=40)
+            sec[f"{which}_48_layers_m40"] = r
+            print(f"# {which} x48 M=40 (4-bit, MFMA): {r['us_per_step']:.1f} us/step, {r['GBps']:.0f} GB/s, "
+                  f"{r['TFLOPs']:.1f} TFLOP/s", flush=True)
     if want("copy"):
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)

@@ -24,6 +24,8 @@
  *   gdn_qlinear         Linear::operator()    cpp/src/model.cpp:356-372 (quantized), for
  *                       the layer's in_proj_* and, with GatedRMSNorm::operator()
  *                       (model.cpp:350-354) in front, its out_proj
+ *   gdn_qlinear_workspace_size                 (sizes the workspace above; the
+ *                       reference allocates inside MLX)
  *   gdn_available       delta::available      cpp/src/delta.hpp:51 (delta.cpp:133-135)
  *
  * Conventions
@@ -49,7 +51,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 #define GDN_HEAD_DIM 128 /* Dk = Dv */
 #define GDN_CONV_TAPS 4  /* conv kernel size; the conv state holds GDN_CONV_TAPS-1 rows */
 
@@ -177,9 +179,14 @@ int gdn_commit(const gdn_commit_args* args);
  * layer's in_proj_qkv, in_proj_z, in_proj_a and in_proj_b (model.cpp:587, 608-609, 626).
  * With norm_x set, the operand is the layer's GatedRMSNorm of the recurrence output
  * (model.cpp:350-354, 626-627), bf16(rmsnorm(norm_x) * norm_gamma * silu(norm_z)) over
- * each 128-value head, so norm + out_proj (model.cpp:641) is one call. */
+ * each 128-value head, so norm + out_proj (model.cpp:641) is one call.
+ * Up to GDN_QLINEAR_GEMV_ROWS operand rows (decode) the call needs no workspace; more
+ * rows (verify blocks, batched decode: up to GDN_QLINEAR_MAX_ROWS, the range the reference
+ * keeps quantized_matmul for, model.hpp:137) run on MFMA and take a workspace of
+ * gdn_qlinear_workspace_size() bytes for the operand in MFMA fragment order. */
 #define GDN_QLINEAR_MAX_SEGS 4
-#define GDN_QLINEAR_MAX_ROWS 4
+#define GDN_QLINEAR_GEMV_ROWS 4
+#define GDN_QLINEAR_MAX_ROWS 512
 
 typedef struct gdn_qlinear_seg {
   const void* w;      /* (N, K/8) uint32, 16-byte aligned */
@@ -191,7 +198,8 @@ typedef struct gdn_qlinear_seg {
 
 typedef struct gdn_qlinear_args {
   int n_layers; /* >= 1; layer l of every tensor starts at l times its per-layer size */
-  int m;        /* rows of the operand (B * L), 1 .. GDN_QLINEAR_MAX_ROWS, m * k <= 30720 */
+  int m;        /* rows of the operand (B * L), 1 .. GDN_QLINEAR_MAX_ROWS; up to
+                   GDN_QLINEAR_GEMV_ROWS also m * k <= 30720 (else the MFMA path) */
   int k;        /* in features: 1024, 2048, 4096, 5120, 6144 or 8192 */
   const void* x; /* (M, K) bf16, 16-byte aligned; NULL when norm_x is set */
   const float* norm_x;     /* (M, K) fp32 (the recurrence output o), or NULL */
@@ -200,10 +208,18 @@ typedef struct gdn_qlinear_args {
   float norm_eps;          /* >= 0 */
   int n_segs;   /* 1 .. GDN_QLINEAR_MAX_SEGS */
   gdn_qlinear_seg segs[GDN_QLINEAR_MAX_SEGS];
+  void* workspace;        /* MFMA path only: device memory of at least
+                             gdn_qlinear_workspace_size() bytes, 256-byte aligned; its
+                             contents are scratch */
+  size_t workspace_bytes;
   void* stream; /* hipStream_t */
 } gdn_qlinear_args;
 
 int gdn_qlinear(const gdn_qlinear_args* args);
+
+/* Workspace bytes gdn_qlinear needs for these arguments' n_layers, m and k (0 on the
+ * GEMV path); the other fields are not read. */
+int gdn_qlinear_workspace_size(const gdn_qlinear_args* args, size_t* bytes);
 
 /* 1 if the current HIP device is a gfx950 the kernels were built for, else 0. */
 int gdn_available(void);

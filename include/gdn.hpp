@@ -229,11 +229,24 @@ struct QuantLinear {
   int n = 0;  // out features
 };
 
+// Workspace bytes the projections below need for M rows of K (0 up to
+// GDN_QLINEAR_GEMV_ROWS rows: the GEMV kernel; more rows run on MFMA).
+inline size_t qlinear_workspace_size(int M, int K) {
+  gdn_qlinear_args a{};
+  a.n_layers = 1;
+  a.m = M;
+  a.k = K;
+  size_t n = 0;
+  check(gdn_qlinear_workspace_size(&a, &n));
+  return n;
+}
+
 // y[i] (M, W[i].n) bf16 = x (M, K) bf16 times W[i]^T, for count <= GDN_QLINEAR_MAX_SEGS
 // matrices sharing x in one launch -- the layer's in_proj_qkv, in_proj_z, in_proj_a,
-// in_proj_b (model.cpp:587, 608-609, 626).
+// in_proj_b (model.cpp:587, 608-609, 626). More than GDN_QLINEAR_GEMV_ROWS rows need a
+// workspace of qlinear_workspace_size(M, K) bytes.
 inline void linears(int M, int K, const void* x, const QuantLinear* W, void* const* y, int count,
-                    hipStream_t stream = nullptr) {
+                    hipStream_t stream = nullptr, void* workspace = nullptr, size_t workspace_bytes = 0) {
   gdn_qlinear_args a{};
   a.n_layers = 1;
   a.m = M;
@@ -242,18 +255,22 @@ inline void linears(int M, int K, const void* x, const QuantLinear* W, void* con
   a.n_segs = count;
   for (int i = 0; i < count && i < GDN_QLINEAR_MAX_SEGS; ++i)
     a.segs[i] = gdn_qlinear_seg{W[i].w, W[i].scales, W[i].biases, y[i], W[i].n};
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
   a.stream = stream;
   check(gdn_qlinear(&a));
 }
 
-inline void linear(const QuantLinear& W, int M, int K, const void* x, void* y, hipStream_t stream = nullptr) {
-  linears(M, K, x, &W, &y, 1, stream);
+inline void linear(const QuantLinear& W, int M, int K, const void* x, void* y, hipStream_t stream = nullptr,
+                   void* workspace = nullptr, size_t workspace_bytes = 0) {
+  linears(M, K, x, &W, &y, 1, stream, workspace, workspace_bytes);
 }
 
 // out_proj(GatedRMSNorm(o, z)) (model.cpp:626-641): o (M, K) fp32 recurrence output, z (M,
 // K) bf16, gamma (128) fp32 -> y (M, W.n) bf16.
 inline void norm_out_proj(const QuantLinear& W, int M, int K, const float* o, const void* z, const float* gamma,
-                          float eps, void* y, hipStream_t stream = nullptr) {
+                          float eps, void* y, hipStream_t stream = nullptr, void* workspace = nullptr,
+                          size_t workspace_bytes = 0) {
   gdn_qlinear_args a{};
   a.n_layers = 1;
   a.m = M;
@@ -264,6 +281,8 @@ inline void norm_out_proj(const QuantLinear& W, int M, int K, const float* o, co
   a.norm_eps = eps;
   a.n_segs = 1;
   a.segs[0] = gdn_qlinear_seg{W.w, W.scales, W.biases, y, W.n};
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
   a.stream = stream;
   check(gdn_qlinear(&a));
 }

@@ -6,6 +6,7 @@ from .gdn import (  # noqa: F401
     STATES_BHT, STATES_TBH, CommitArgs, DeltaCache, GdnError, LayerArgs, Result, available,
     call_commit, call_prefill, call_qlinear, call_run, commit, last_error, layer, layer_args,
     lib, prefill_chunked, prefill_workspace_size, qlinear, qlinear_args, QLinearArgs,
-    QLinearSeg, QuantLinear, QLINEAR_MAX_ROWS, QLINEAR_MAX_SEGS, run,
+    QLinearSeg, QuantLinear, QLINEAR_GEMV_ROWS, QLINEAR_MAX_ROWS, QLINEAR_MAX_SEGS,
+    qlinear_workspace_size, run,
 )
 from . import weights  # noqa: F401,E402  (checkpoint reader for the path's weights)

@@ -367,9 +367,14 @@ int gdn_qlinear(const gdn_qlinear_args* a) {
     return fail(GDN_EINVAL, "gdn_qlinear: k=%d unsupported (1024, 2048, 4096, 5120, 6144, 8192)", a->k);
   if (a->n_segs < 1 || a->n_segs > GDN_QLINEAR_MAX_SEGS)
     return fail(GDN_EINVAL, "gdn_qlinear: n_segs must be 1..%d", GDN_QLINEAR_MAX_SEGS);
-  if ((int64_t)a->m * (a->k / 32) * 68 > 65536)  // the staged operand's LDS
-    return fail(GDN_EINVAL, "gdn_qlinear: m * k too large (m=%d k=%d; m * k <= 30720)", a->m, a->k);
   const int64_t L = a->n_layers, M = a->m, K = a->k;
+  const size_t ws_need = gdn::qlinear_workspace_bytes(a->n_layers, a->m, a->k);
+  if (ws_need > 0) {  // MFMA path: the operand in fragment order goes to the workspace
+    if (!a->workspace || a->workspace_bytes < ws_need)
+      return fail(GDN_EINVAL, "gdn_qlinear: m=%d k=%d needs a workspace of %zu bytes (got %zu)", a->m, a->k, ws_need,
+                  a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(GDN_EINVAL, "gdn_qlinear: workspace must be 256-byte aligned");
+  }
   const bool norm = a->norm_x != nullptr;
   if (norm == (a->x != nullptr))
     return fail(GDN_EINVAL, "gdn_qlinear: exactly one of x and norm_x is required");
@@ -396,9 +401,16 @@ int gdn_qlinear(const gdn_qlinear_args* a) {
     rows += g.n;
   }
   if (rows * L > (int64_t)1 << 31) return fail(GDN_EINVAL, "gdn_qlinear: too many rows");
+  const Range ws = range_of(ws_need > 0 ? a->workspace : nullptr, (int64_t)ws_need);
+  for (const Range& r : in)
+    if (overlap(ws, r)) return fail(GDN_EINVAL, "gdn_qlinear: the workspace must not overlap the operand");
   for (int i = 0; i < a->n_segs; ++i) {
     const gdn_qlinear_seg& g = a->segs[i];
     const Range y = range_of(g.y, L * M * g.n * 2);
+    if (overlap(y, ws)) return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap the workspace", i);
+    if (overlap(ws, range_of(g.w, L * g.n * K / 2)) || overlap(ws, range_of(g.scales, L * g.n * K / 32)) ||
+        overlap(ws, range_of(g.biases, L * g.n * K / 32)))
+      return fail(GDN_EINVAL, "gdn_qlinear: the workspace must not overlap segment %d's weights", i);
     for (const Range& r : in)
       if (overlap(y, r)) return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap the operand", i);
     for (int j = 0; j < a->n_segs; ++j) {
@@ -414,6 +426,14 @@ int gdn_qlinear(const gdn_qlinear_args* a) {
   if (rc != GDN_OK) return rc;
   hipError_t e = gdn::launch_qlinear(*a, static_cast<hipStream_t>(a->stream));
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear launch");
+  return ok();
+}
+
+int gdn_qlinear_workspace_size(const gdn_qlinear_args* a, size_t* bytes) {
+  if (!a || !bytes) return fail(GDN_EINVAL, "gdn_qlinear_workspace_size: NULL argument");
+  if (a->n_layers < 1 || a->m < 1 || a->m > GDN_QLINEAR_MAX_ROWS || !gdn::qlinear_k_supported(a->k))
+    return fail(GDN_EINVAL, "gdn_qlinear_workspace_size: bad shape (n_layers=%d m=%d k=%d)", a->n_layers, a->m, a->k);
+  *bytes = gdn::qlinear_workspace_bytes(a->n_layers, a->m, a->k);
   return ok();
 }
 

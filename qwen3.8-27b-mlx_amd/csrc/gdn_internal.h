@@ -64,6 +64,9 @@ hipError_t launch_commit(const CommitParams& p, hipStream_t stream);
 
 // Quantized linear (arguments validated by the caller).
 bool qlinear_k_supported(int k);
+// m rows of k on the GEMV path (no workspace); otherwise the MFMA path
+bool qlinear_uses_gemv(int m, int k);
+size_t qlinear_workspace_bytes(int n_layers, int m, int k);
 hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream);
 
 }  // namespace gdn

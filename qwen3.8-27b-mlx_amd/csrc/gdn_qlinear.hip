@@ -16,9 +16,19 @@
 // v_dot2 multiplies pairs by the operand staged in the same pair order, and scale and
 // bias are applied once per half-group: sum x (q s + b) = s * sum x (128 + q) +
 // (b - 128 s) * sum x. The row total is a DPP row sum; the result is rounded to bf16 once.
+//
+// More rows (verify blocks, batched decode) run on MFMA (v_mfma_f32_16x16x32_bf16) with the
+// same arithmetic: qprep writes the operand once into the workspace in the MFMA fragment
+// order (the norm prologue applied there, as above), then in qgemm each lane's weight row
+// gives B fragments straight from its nibble words and the operand fragments come from
+// the workspace; per 64-value group acc = sum x (128 + q) and, from a ones operand, sum x,
+// both fp32, then y += s * acc + (b - 128 s) * sum x. A workgroup's 4 waves split K and add
+// their partial sums in LDS at the end, so each wave reads a quarter of the operand.
 #include "../../include/gdn.h"
 #include "gdn_device_math.h"
 #include "gdn_internal.h"
+
+#include <algorithm>
 
 namespace gdn {
 namespace {
@@ -27,6 +37,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = 16;  // 4 waves x 4 DPP rows
@@ -45,6 +57,12 @@ struct QParams {
   uint16_t* y[GDN_QLINEAR_MAX_SEGS];
   int n[GDN_QLINEAR_MAX_SEGS];
   int row0[GDN_QLINEAR_MAX_SEGS];  // first global row of each segment
+  // MFMA path: the operand in fragment order, (L, mtiles, K / 32) blocks of 64 lanes x 8
+  // bf16; lane 16 g4 + mm of block f = 2 g + s holds row 16 mt + mm, values
+  // k = 64 g + 16 g4 + 8 s + (0, 4, 1, 5, 2, 6, 3, 7) (the nibble pair order); rows past M
+  // are zeros
+  uint16_t* xfrag;
+  int mtiles;
 };
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -72,6 +90,50 @@ __device__ __forceinline__ void stage_chunk(u32x4* xs, float* xsum, int nch, int
   xsum[mm * nch + c] = sum;
 }
 
+// The operand of row mrow, values 32 c .. 32 c + 31, into v: x as given, or the GatedRMSNorm
+// of (xf, z) (the four pieces of a 128-value head are the lanes of a DPP quad).
+template <bool NORM>
+__device__ __forceinline__ void operand_piece(const QParams& p, int layer, int mrow, int c, float (&v)[32]) {
+  const size_t base = ((size_t)layer * p.M + mrow) * p.K + 32 * c;
+  if (NORM) {
+    // GatedRMSNorm: h = o * rsqrt(mean(o^2) + eps) * gamma (fp32), times silu(fp32(z)),
+    // rounded to bf16 (the activation dtype out_proj takes)
+    float o[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const f4 f = *reinterpret_cast<const f4*>(p.xf + base + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[4 * q + e] = f[e];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) ss += o[e] * o[e];
+    ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0xB1, 0xF, 0xF, true));
+    ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0x4E, 0xF, 0xF, true));
+    const float rs = 1.0f / sqrtf(ss / 128.0f + p.eps);
+    const float* gm = p.gamma + (size_t)layer * 128 + 32 * (c & 3);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u16x8 zz = *reinterpret_cast<const u16x8*>(p.z + base + 8 * q);
+      const f4 g0 = *reinterpret_cast<const f4*>(gm + 8 * q);
+      const f4 g1 = *reinterpret_cast<const f4*>(gm + 8 * q + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float zf = bf2f(zz[e]);
+        const float h = o[8 * q + e] * rs * (e < 4 ? g0[e] : g1[e - 4]);
+        v[8 * q + e] = rbf(h * (zf * d_sigmoidf(zf)));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u16x8 xx = *reinterpret_cast<const u16x8*>(p.x + base + 8 * q);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[8 * q + e] = bf2f(xx[e]);
+    }
+  }
+}
+
 template <int J, bool NORM>
 __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -86,45 +148,8 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   // 128-value head are the four lanes of a DPP quad ----
   for (int t = tid; t < p.M * nch; t += kThreads) {
     const int mm = t / nch, c = t % nch;
-    const size_t base = ((size_t)layer * p.M + mm) * K + 32 * c;
     float v[32];
-    if (NORM) {
-      // GatedRMSNorm: h = o * rsqrt(mean(o^2) + eps) * gamma (fp32), times silu(fp32(z)),
-      // rounded to bf16 (the activation dtype out_proj takes)
-      float o[32];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const f4 f = *reinterpret_cast<const f4*>(p.xf + base + 4 * q);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[4 * q + e] = f[e];
-      }
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) ss += o[e] * o[e];
-      ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0xB1, 0xF, 0xF, true));
-      ss += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ss), 0x4E, 0xF, 0xF, true));
-      const float rs = 1.0f / sqrtf(ss / 128.0f + p.eps);
-      const float* gm = p.gamma + (size_t)layer * 128 + 32 * (c & 3);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u16x8 zz = *reinterpret_cast<const u16x8*>(p.z + base + 8 * q);
-        const f4 g0 = *reinterpret_cast<const f4*>(gm + 8 * q);
-        const f4 g1 = *reinterpret_cast<const f4*>(gm + 8 * q + 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float zf = bf2f(zz[e]);
-          const float h = o[8 * q + e] * rs * (e < 4 ? g0[e] : g1[e - 4]);
-          v[8 * q + e] = rbf(h * (zf * d_sigmoidf(zf)));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u16x8 xx = *reinterpret_cast<const u16x8*>(p.x + base + 8 * q);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[8 * q + e] = bf2f(xx[e]);
-      }
-    }
+    operand_piece<NORM>(p, layer, mm, c, v);
     stage_chunk(xs, xsum, nch, mm, c, v);
   }
   __syncthreads();
@@ -168,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
       sv[j] = sr[c >> 1];
       bv[j] = br[c >> 1];
     }
-    float y[GDN_QLINEAR_MAX_ROWS] = {0.f, 0.f, 0.f, 0.f};
+    float y[GDN_QLINEAR_GEMV_ROWS] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int c = m + 16 * j;
@@ -182,7 +207,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
         for (int q = 0; q < 4; ++q) pr[i][q] = ((wd >> (4 * q)) & 0x000F000Fu) | 0x43004300u;
       }
 #pragma unroll
-      for (int mm = 0; mm < GDN_QLINEAR_MAX_ROWS; ++mm) {
+      for (int mm = 0; mm < GDN_QLINEAR_GEMV_ROWS; ++mm) {
         if (mm < p.M) {
           float acc = 0.0f;
 #pragma unroll
@@ -196,12 +221,192 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
       }
     }
 #pragma unroll
-    for (int mm = 0; mm < GDN_QLINEAR_MAX_ROWS; ++mm) {
+    for (int mm = 0; mm < GDN_QLINEAR_GEMV_ROWS; ++mm) {
       if (mm < p.M) {
         const float tot = row16_sum(y[mm]);
         if (m == 0 && valid) yseg[((size_t)layer * p.M + mm) * nseg + (row - r0)] = f2bf(tot);
       }
     }
+  }
+}
+
+// MFMA path, step 1: the operand (normalised when NORM) into the workspace's fragment
+// order. Thread = (layer, row, 32-value piece c): the piece is 4 fragment lanes of 8
+// values (blocks 2 (c / 2) + s, lanes 16 (2 (c % 2) + j / 2) + row % 16, s = j % 2). The
+// thread count is a multiple of 4 and pieces run fastest, so a DPP quad is one head.
+template <bool NORM>
+__global__ __launch_bounds__(kThreads) void qprep_kernel(QParams p, int layers) {
+  const int nch = p.K / 32, rows = 16 * p.mtiles;
+  const size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= (size_t)layers * rows * nch) return;  // whole quads (nch is a multiple of 4)
+  const int c = (int)(t % nch);
+  const size_t rg = t / nch;
+  const int mrow = (int)(rg % rows), layer = (int)(rg / rows);
+  float v[32];
+  if (mrow < p.M) {
+    operand_piece<NORM>(p, layer, mrow, c, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) v[e] = 0.0f;
+  }
+  uint16_t* blk = p.xfrag + ((size_t)layer * p.mtiles + mrow / 16) * nch * 512;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = pack_bf2(v[8 * j + e], v[8 * j + e + 4]);
+    const int f = 2 * (c / 2) + (j & 1), ln = 16 * (2 * (c & 1) + j / 2) + (mrow & 15);
+    *reinterpret_cast<u32x4*>(blk + ((size_t)f * 64 + ln) * 8) = q;
+  }
+}
+
+__device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Two nibble words (values k .. k + 7 each) as B fragments: bf16 128 + v, pairs (i, i + 4).
+__device__ __forceinline__ bf8 nibbles_bf16(uint32_t wd) {
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r[q] = ((wd >> (4 * q)) & 0x000F000Fu) | 0x43004300u;
+  return __builtin_bit_cast(bf8, r);
+}
+
+// MFMA path, step 2. Workgroup = 16 NT weight rows (the output columns) x 16 MT operand
+// rows; wave w takes the groups [w G / 4, (w + 1) G / 4) of the G = K / 64 groups. Lane
+// (g4, nn) = (l / 16, l % 16) reads the nibble words 8 g + 2 g4 + s of its row 16 nt + nn
+// (one 8-byte load per row and group) and gets C rows m = 4 g4 + i of column nn.
+template <int MT, int NT>
+__global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
+  __shared__ __attribute__((aligned(16))) f4 red[3][MT * NT][64];  // partial sums of waves 1..3
+  const int layer = blockIdx.x / p.tiles, tile = blockIdx.x % p.tiles;
+  const int mt0 = blockIdx.y * MT;
+  const int lane = threadIdx.x & 63, g4 = lane >> 4, nn = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = p.K, G = K / 64, nch = K / 32;
+  const int g0 = wave * G / 4, g1 = (wave + 1) * G / 4;
+
+  // this lane's weight row for each n-tile
+  const u32x2* wr[NT];
+  const uint16_t *sr[NT], *br[NT];
+  uint16_t* yr[NT];
+  int ystride[NT];
+  bool valid[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int grow = (tile * NT + nt) * 16 + nn;
+    valid[nt] = grow < p.R;
+    const int row = valid[nt] ? grow : p.R - 1;
+    int sg = 0;
+#pragma unroll
+    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= p.row0[q]) ? 1 : 0;
+    const uint32_t* wseg = p.w[0];
+    const uint16_t *sseg = p.s[0], *bseg = p.b[0];
+    uint16_t* yseg = p.y[0];
+    int nseg = p.n[0], r0 = p.row0[0];
+#pragma unroll
+    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) {
+      if (sg == q) {
+        wseg = p.w[q];
+        sseg = p.s[q];
+        bseg = p.b[q];
+        yseg = p.y[q];
+        nseg = p.n[q];
+        r0 = p.row0[q];
+      }
+    }
+    const size_t lrow = (size_t)layer * nseg + (row - r0);
+    wr[nt] = reinterpret_cast<const u32x2*>(wseg + lrow * (K / 8)) + g4;  // + 4 g: words 8 g + 2 g4, +1
+    sr[nt] = sseg + lrow * G;
+    br[nt] = bseg + lrow * G;
+    yr[nt] = yseg + (size_t)layer * p.M * nseg + (row - r0);
+    ystride[nt] = nseg;
+  }
+  const bf8* xa = reinterpret_cast<const bf8*>(p.xfrag + ((size_t)layer * p.mtiles + mt0) * nch * 512) + lane;
+  const bf8 ones = __builtin_bit_cast(bf8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+  f4 y[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // one group ahead: the loads of group g + 1 are in flight while group g is multiplied
+  // (deeper prefetch in registers spilled; this path is functional, not tuned)
+  bf8 a[MT][2] = {}, an[MT][2] = {};
+  u32x2 wv[NT] = {}, wn[NT] = {};
+  uint16_t sv[NT] = {}, bv[NT] = {}, sn[NT] = {}, bn[NT] = {};
+  auto load = [&](int g, bf8 (&aa)[MT][2], u32x2 (&ww)[NT], uint16_t (&ss)[NT], uint16_t (&bb)[NT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) aa[mt][s] = xa[((size_t)mt * nch + 2 * g + s) * 64];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      ww[nt] = __builtin_nontemporal_load(wr[nt] + 4 * g);
+      ss[nt] = sr[nt][g];
+      bb[nt] = br[nt][g];
+    }
+  };
+  if (g0 < g1) load(g0, a, wv, sv, bv);
+  for (int g = g0; g < g1; ++g) {
+    if (g + 1 < g1) load(g + 1, an, wn, sn, bn);
+    f4 xs[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      xs[mt] = mfma(a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
+      xs[mt] = mfma(a[mt][1], ones, xs[mt]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const bf8 b0 = nibbles_bf16(wv[nt][0]), b1 = nibbles_bf16(wv[nt][1]);
+      const float sc = bf2f(sv[nt]);
+      const float off = bf2f(bv[nt]) - 128.0f * sc;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        f4 acc = mfma(a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
+        acc = mfma(a[mt][1], b1, acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      a[mt][0] = an[mt][0];
+      a[mt][1] = an[mt][1];
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      wv[nt] = wn[nt];
+      sv[nt] = sn[nt];
+      bv[nt] = bn[nt];
+    }
+  }
+
+  // the four waves' partial sums (fixed order: wave 0 + 1 + 2 + 3), rounded to bf16 once
+  if (wave > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) red[wave - 1][mt * NT + nt][lane] = y[mt][nt];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f4 t = y[mt][nt];
+#pragma unroll
+        for (int w = 0; w < 3; ++w) t = t + red[w][mt * NT + nt][lane];
+        if (valid[nt]) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = (mt0 + mt) * 16 + 4 * g4 + i;
+            if (m < p.M) yr[nt][(size_t)m * ystride[nt]] = f2bf(t[i]);
+          }
+        }
+      }
   }
 }
 
@@ -223,6 +428,36 @@ hipError_t launch_j(int J, const QParams& p, dim3 grid, size_t smem, hipStream_t
 
 bool qlinear_k_supported(int k) {
   return k == 1024 || k == 2048 || k == 4096 || k == 5120 || k == 6144 || k == 8192;
+}
+
+bool qlinear_uses_gemv(int m, int k) {
+  return m <= GDN_QLINEAR_GEMV_ROWS && (size_t)m * (k / 32) * (4 * 16 + 4) <= 65536;
+}
+
+namespace {
+// MFMA path: m-tiles of 16 rows per workgroup (1..4), the m-tile count rounded up to a
+// multiple of it (the padding rows are zeros in the workspace)
+int qgemm_mt(int m) { return std::min(4, (m + 15) / 16); }
+int qgemm_mtiles(int m) {
+  const int mt = qgemm_mt(m);
+  return ((m + 15) / 16 + mt - 1) / mt * mt;
+}
+
+template <int MT>
+hipError_t launch_gemm_mt(int NT, const QParams& p, dim3 grid, hipStream_t stream) {
+  switch (NT) {
+    case 1: hipLaunchKernelGGL((qgemm_kernel<MT, 1>), grid, dim3(kThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((qgemm_kernel<MT, 2>), grid, dim3(kThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL((qgemm_kernel<MT, 4>), grid, dim3(kThreads), 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+size_t qlinear_workspace_bytes(int n_layers, int m, int k) {
+  if (qlinear_uses_gemv(m, k)) return 0;
+  const size_t b = (size_t)n_layers * qgemm_mtiles(m) * (k / 32) * 1024;
+  return (b + 255) / 256 * 256;
 }
 
 hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
@@ -248,13 +483,37 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   }
   p.R = R;
   const bool norm = a.norm_x != nullptr;
-  // rows per workgroup: 64, or 256 with the norm prologue (every workgroup normalises
-  // the whole operand, so fewer, taller tiles)
-  p.passes = norm ? 16 : 4;
-  p.tiles = (R + kRowsPerPass * p.passes - 1) / (kRowsPerPass * p.passes);
-  const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles));
-  const size_t smem = (size_t)p.M * (a.k / 32) * (4 * 16 + 4);
-  return norm ? launch_j<true>(a.k / 512, p, grid, smem, stream) : launch_j<false>(a.k / 512, p, grid, smem, stream);
+  if (qlinear_uses_gemv(a.m, a.k)) {
+    // rows per workgroup: 64, or 256 with the norm prologue (every workgroup normalises
+    // the whole operand, so fewer, taller tiles)
+    p.passes = norm ? 16 : 4;
+    p.tiles = (R + kRowsPerPass * p.passes - 1) / (kRowsPerPass * p.passes);
+    const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles));
+    const size_t smem = (size_t)p.M * (a.k / 32) * (4 * 16 + 4);
+    return norm ? launch_j<true>(a.k / 512, p, grid, smem, stream) : launch_j<false>(a.k / 512, p, grid, smem, stream);
+  }
+  // MFMA path: the operand into the workspace, then the product
+  const int MT = qgemm_mt(a.m);
+  p.mtiles = qgemm_mtiles(a.m);
+  p.xfrag = static_cast<uint16_t*>(a.workspace);
+  const size_t prep_threads = (size_t)a.n_layers * 16 * p.mtiles * (a.k / 32);
+  const dim3 gp((unsigned)((prep_threads + kThreads - 1) / kThreads));
+  if (norm) hipLaunchKernelGGL(qprep_kernel<true>, gp, dim3(kThreads), 0, stream, p, a.n_layers);
+  else hipLaunchKernelGGL(qprep_kernel<false>, gp, dim3(kThreads), 0, stream, p, a.n_layers);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // weight rows per workgroup: 64, 32 or 16 -- the most that still gives 512 workgroups
+  const int gy = p.mtiles / MT;
+  int NT = 4;
+  while (NT > 1 && (size_t)a.n_layers * ((R + 16 * NT - 1) / (16 * NT)) * gy < 512) NT /= 2;
+  p.tiles = (R + 16 * NT - 1) / (16 * NT);
+  const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles), (unsigned)gy);
+  switch (MT) {
+    case 1: return launch_gemm_mt<1>(NT, p, grid, stream);
+    case 2: return launch_gemm_mt<2>(NT, p, grid, stream);
+    case 3: return launch_gemm_mt<3>(NT, p, grid, stream);
+    default: return launch_gemm_mt<4>(NT, p, grid, stream);
+  }
 }
 
 }  // namespace gdn

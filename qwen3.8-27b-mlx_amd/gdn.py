@@ -32,10 +32,12 @@ HEAD_DIM = 128
 CONV_TAPS = 4
 
 QLINEAR_MAX_SEGS = 4
-QLINEAR_MAX_ROWS = 4
+QLINEAR_GEMV_ROWS = 4
+QLINEAR_MAX_ROWS = 512
 
 EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-           "gdn_qlinear", "gdn_available", "gdn_abi_version", "gdn_last_error")
+           "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_available", "gdn_abi_version",
+           "gdn_last_error")
 
 
 class GdnError(RuntimeError):
@@ -90,6 +92,7 @@ class QLinearArgs(ctypes.Structure):
         ("x", _vp),
         ("norm_x", _vp), ("norm_z", _vp), ("norm_gamma", _vp), ("norm_eps", ctypes.c_float),
         ("n_segs", _int), ("segs", QLinearSeg * QLINEAR_MAX_SEGS),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("stream", _vp),
     ]
 
@@ -114,6 +117,8 @@ def lib() -> ctypes.CDLL:
         L.gdn_commit.restype = _int
         L.gdn_qlinear.argtypes = [ctypes.POINTER(QLinearArgs)]
         L.gdn_qlinear.restype = _int
+        L.gdn_qlinear_workspace_size.argtypes = [ctypes.POINTER(QLinearArgs), ctypes.POINTER(ctypes.c_size_t)]
+        L.gdn_qlinear_workspace_size.restype = _int
         L.gdn_available.argtypes = []
         L.gdn_available.restype = _int
         L.gdn_abi_version.argtypes = []
@@ -152,6 +157,14 @@ def call_commit(args: CommitArgs) -> None:
 
 def call_qlinear(args: QLinearArgs) -> None:
     _check(lib().gdn_qlinear(ctypes.byref(args)))
+
+
+def qlinear_workspace_size(m: int, k: int, n_layers: int = 1) -> int:
+    """Workspace bytes gdn_qlinear needs for m operand rows of k (0 on the GEMV path)."""
+    a = QLinearArgs(n_layers=n_layers, m=m, k=k)
+    n = ctypes.c_size_t(0)
+    _check(lib().gdn_qlinear_workspace_size(ctypes.byref(a), ctypes.byref(n)))
+    return n.value
 
 
 def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48, conv: bool = True) -> int:
@@ -408,10 +421,11 @@ class QuantLinear:
         return self.w.shape[-2]
 
 
-def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
+def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, stream=None):
     """gdn_qlinear_args for y_i = x W_i^T, i over `mats` (1..4 QuantLinear reading the same
     x), or with norm = (o, z, gamma, eps) the layer's GatedRMSNorm of o as the operand.
-    Allocates the outputs; returns (args, [y_i])."""
+    Allocates the outputs, and the workspace when the rows need one and none is given;
+    returns (args, [y_i])."""
     import torch
     src = x if x is not None else norm[0]
     K = src.shape[-1]
@@ -426,13 +440,25 @@ def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
         y = torch.empty(shape, dtype=torch.bfloat16, device=src.device)
         ys.append(y)
         a.segs[i] = QLinearSeg(w=_ptr(q.w), scales=_ptr(q.scales), biases=_ptr(q.biases), y=_ptr(y), n=q.n)
+    try:
+        need = qlinear_workspace_size(M, K, n_layers)
+    except GdnError:
+        need = 0  # a bad shape: gdn_qlinear itself reports it
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=src.device)
+    if workspace is not None:
+        a.workspace = _ptr(workspace)
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    a._keep = workspace  # the workspace lives as long as the args
     return a, ys
 
 
-def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
+def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, stream=None):
     """Linear::operator() for quantized weights (model.cpp:356-372) over 1..4 matrices
     sharing x -- e.g. the layer's in_proj_qkv, in_proj_z, in_proj_a, in_proj_b -- or, with
-    norm = (o, z, gamma, eps), out_proj(GatedRMSNorm(o, z)) (model.cpp:626-641)."""
-    args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, stream=stream)
+    norm = (o, z, gamma, eps), out_proj(GatedRMSNorm(o, z)) (model.cpp:626-641). Up to
+    QLINEAR_GEMV_ROWS rows it is the GEMV kernel; more rows run on MFMA with a workspace
+    (allocated here unless given)."""
+    args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, workspace=workspace, stream=stream)
     call_qlinear(args)
     return ys

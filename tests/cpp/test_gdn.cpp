@@ -283,6 +283,45 @@ void test_qlinear() {
     snprintf(buf, sizeof(buf), "GatedRMSNorm + out_proj (N=%d, K=%d): worst err / limit %.3f", No, Ko, worst);
     check(worst <= 1.0, buf);
   }
+  // a verify block's rows (M = 40): the MFMA path, with a caller workspace
+  {
+    const int Mv = 40, N = ns[0];
+    std::vector<float> xf = normal(901, (size_t)Mv * K);
+    std::vector<uint16_t> xv(xf.size());
+    gdno_round_bf16(xf.data(), xv.data(), (int64_t)xv.size());
+    const size_t ws_bytes = gdn::qlinear_workspace_size(Mv, K);
+    void* ws = nullptr;
+    gdn::check_hip(hipMalloc(&ws, ws_bytes), "hipMalloc");
+    void* yv = nullptr;
+    gdn::check_hip(hipMalloc(&yv, (size_t)Mv * N * 2), "hipMalloc");
+    gdn::linear(W[0], Mv, K, to_dev(xv), yv, nullptr, ws, ws_bytes);
+    gdn::check_hip(hipDeviceSynchronize(), "sync");
+    std::vector<double> ref((size_t)Mv * N);
+    gdno_qlinear_f64(Mv, N, K, xv.data(), hw[0].data(), hs[0].data(), hb[0].data(), ref.data());
+    std::vector<uint16_t> got = to_host(static_cast<uint16_t*>(yv), (size_t)Mv * N);
+    double worst = 0;
+    for (int m = 0; m < Mv; ++m)
+      for (int n = 0; n < N; ++n) {
+        double acc = 0;  // 2^-20 sum |x| (143 |s| + |b|)
+        for (int k = 0; k < K; ++k)
+          acc += std::fabs(gdno_bf16_to_f32(xv[(size_t)m * K + k])) *
+                 (143.0 * std::fabs(gdno_bf16_to_f32(hs[0][(size_t)n * K / 64 + k / 64])) +
+                  std::fabs(gdno_bf16_to_f32(hb[0][(size_t)n * K / 64 + k / 64])));
+        const double r = ref[(size_t)m * N + n];
+        const double lim = std::ldexp(std::fabs(r), -8) + std::ldexp(acc, -20);
+        worst = std::max(worst, std::fabs(gdno_bf16_to_f32(got[(size_t)m * N + n]) - r) / lim);
+      }
+    char buf[128];
+    snprintf(buf, sizeof(buf), "M=%d rows (MFMA path, workspace %zu B): worst err / limit %.3f", Mv, ws_bytes, worst);
+    check(worst <= 1.0, buf);
+    bool threw = false;
+    try {
+      gdn::linear(W[0], Mv, K, to_dev(xv), yv);  // no workspace
+    } catch (const gdn::Error&) {
+      threw = true;
+    }
+    check(threw, "M=40 without a workspace throws");
+  }
 }
 
 int main() {

@@ -22,7 +22,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(
         ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-         "gdn_qlinear", "gdn_available", "gdn_abi_version", "gdn_last_error"])
+         "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_available", "gdn_abi_version",
+         "gdn_last_error"])
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -33,7 +34,7 @@ def test_library_exports_every_declared_symbol(gdn):
                          text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s+(gdn_\w+)", out))
     assert set(declared_functions()) <= exported
-    assert L.gdn_abi_version() == 1
+    assert L.gdn_abi_version() == 2
     assert set(gdn.EXPORTS) == set(declared_functions())
 
 
@@ -229,10 +230,15 @@ def _ql(gdn, **kw):
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(m=0), "bad shape"),
-    (dict(m=5), "bad shape"),
+    (dict(m=513), "bad shape"),
     (dict(n_layers=0), "bad shape"),
     (dict(k=5000), "unsupported"),
-    (dict(m=4, k=8192), "too large"),
+    (dict(m=5), "needs a workspace"),
+    (dict(m=4, k=8192), "needs a workspace"),
+    (dict(m=40, workspace=0x8000000, workspace_bytes=100), "needs a workspace"),
+    (dict(m=40, workspace=0x8000010, workspace_bytes=1 << 30), "256-byte"),
+    (dict(m=40, workspace=0x10000, workspace_bytes=1 << 30), "must not overlap the operand"),
+    (dict(m=40, workspace=0x3ffff00, workspace_bytes=1 << 20), "must not overlap the workspace"),
     (dict(n_segs=5), "n_segs"),
     (dict(x=None), "exactly one"),
     (dict(norm_x=0x20000), "exactly one"),
@@ -250,3 +256,20 @@ def test_qlinear_rejects_bad_arguments(gdn, kw, msg):
     rc = gdn.lib().gdn_qlinear(ctypes.byref(_ql(gdn, **kw)))
     assert rc == gdn.GDN_EINVAL
     assert msg in gdn.last_error(), gdn.last_error()
+
+
+def test_qlinear_workspace_size(gdn):
+    """GEMV path (m <= 4 and m k <= 30720): none. MFMA path: the operand in fragment order,
+    1 KB per (16-row tile, 32 values), the tile count rounded up to the tiles a workgroup
+    takes (up to 4)."""
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert gdn.qlinear_workspace_size(4, 5120) == 0
+    assert gdn.qlinear_workspace_size(1, 8192) == 0
+    assert gdn.qlinear_workspace_size(4, 8192) == al(1 * (8192 // 32) * 1024)
+    assert gdn.qlinear_workspace_size(5, 5120) == 160 * 1024
+    assert gdn.qlinear_workspace_size(40, 5120) == 3 * 160 * 1024
+    assert gdn.qlinear_workspace_size(40, 6144, n_layers=2) == 2 * 3 * 192 * 1024
+    assert gdn.qlinear_workspace_size(65, 5120) == 8 * 160 * 1024  # 5 tiles -> 2 x 4
+    assert gdn.qlinear_workspace_size(512, 1024) == 32 * 32 * 1024
+    with pytest.raises(gdn.GdnError):
+        gdn.qlinear_workspace_size(513, 5120)

@@ -113,3 +113,88 @@ def test_qlinear_rejects_bad_arguments_on_gpu(gdn, dev):
     sb = torch.zeros((8, 78), dtype=torch.bfloat16, device=dev)
     with pytest.raises(gdn.GdnError, match="unsupported"):
         gdn.qlinear([gdn.QuantLinear(w, sb, sb)], x)
+
+
+# ---- more than 4 rows: the MFMA path (operand in fragment order in a workspace) ----
+
+@pytest.mark.parametrize("M,N,K", [(5, 200, 1024), (16, 96, 5120), (17, 130, 6144), (40, 64, 8192),
+                                   (64, 48, 2048), (100, 17, 4096), (4, 72, 8192), (257, 40, 1024)])
+def test_qlinear_mfma_single_matrix(O, gdn, dev, M, N, K):
+    import torch
+    log_case(f"qlinear (MFMA path) M={M} N={N} K={K}")
+    x, w, s, b = quant_inputs(O, 1, M, N, K, seed=7 * N + K + M)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    check(to_np(y), O.qlinear(x[0], w[0], s[0], b[0]), bound(O, x[0], s[0], b[0]), "y")
+
+
+def test_qlinear_mfma_in_proj_verify_block(O, gdn, dev):
+    """The layer's four in_proj matrices on a verify block's 40 rows (B=8, T=5), K=5120."""
+    import torch
+    log_case("qlinear (MFMA path) in_proj 4 segments, M=40, K=5120")
+    M, K = 40, 5120
+    ns = [10240, 6144, 48, 48]
+    mats, host, x = [], [], None
+    for i, n in enumerate(ns):
+        xi, w, s, b = quant_inputs(O, 1, M, n, K, seed=200 + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w[0], s[0], b[0]))
+        host.append((w[0], s[0], b[0]))
+    ys = gdn.qlinear(mats, to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        check(to_np(y), O.qlinear(x[0], w, s, b), bound(O, x[0], s, b), f"segment {i}")
+
+
+def test_qlinear_mfma_two_layers_two_segments(O, gdn, dev):
+    import torch
+    log_case("qlinear (MFMA path) 2 layers x 2 segments, M=24, K=2048")
+    L, M, K = 2, 24, 2048
+    mats, host, x = [], [], None
+    for i, n in enumerate([100, 36]):
+        xi, w, s, b = quant_inputs(O, L, M, n, K, seed=300 + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w, s, b))
+        host.append((w, s, b))
+    ys = gdn.qlinear(mats, to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        got = to_np(y)
+        for l in range(L):
+            check(got[l], O.qlinear(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
+
+
+@pytest.mark.parametrize("M", [5, 40])
+def test_qlinear_mfma_gated_rmsnorm_prologue(O, gdn, dev, M):
+    """out_proj(GatedRMSNorm(o, z)) for M rows on the MFMA path (the norm applied while the
+    operand goes to the workspace), same tolerance as the GEMV path's test."""
+    import torch
+    log_case(f"qlinear (MFMA path) out_proj with GatedRMSNorm, M={M}, K=6144, N=5120")
+    K, N = 6144, 5120
+    rng = np.random.default_rng(900 + M)
+    o = (rng.standard_normal((M, K)) * 0.3).astype(np.float32)
+    z = O.to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    gamma = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    _, w, s, b = quant_inputs(O, 1, M, N, K, seed=901 + M)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])],
+                       norm=(to_dev(o, dev), to_dev(z, dev), to_dev(gamma, dev), 1e-6))
+    torch.cuda.synchronize()
+    xn = O.gated_rmsnorm(o.reshape(M * 48, 128), z.reshape(M * 48, 128), gamma, 1e-6).reshape(M, K)
+    ref = O.qlinear(xn, w[0], s[0], b[0])
+    W = (np.abs(np.repeat(bf16_to_f32(s[0]), 64, axis=1)) * 15 + np.abs(np.repeat(bf16_to_f32(b[0]), 64, axis=1)))
+    flip = 3 * 2.0 ** -8 * (np.abs(bf16_to_f32(xn)).max(axis=1, keepdims=True) * W.max(axis=1)[None, :])
+    check(to_np(y), ref, bound(O, xn, s[0], b[0]) + flip, "y")
+
+
+def test_qlinear_mfma_reuses_a_caller_workspace(O, gdn, dev):
+    """One workspace, two calls in a row with different M; the second's result must not
+    depend on what the first left there."""
+    import torch
+    log_case("qlinear (MFMA path) caller workspace reused, M=40 then M=9")
+    K, N = 5120, 80
+    ws = torch.empty(gdn.qlinear_workspace_size(40, K), dtype=torch.uint8, device=dev)
+    for M, seed in ((40, 11), (9, 12)):
+        x, w, s, b = quant_inputs(O, 1, M, N, K, seed=seed)
+        (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev), workspace=ws)
+        torch.cuda.synchronize()
+        check(to_np(y), O.qlinear(x[0], w[0], s[0], b[0]), bound(O, x[0], s[0], b[0]), f"M={M}")
