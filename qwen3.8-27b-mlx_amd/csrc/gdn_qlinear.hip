@@ -331,56 +331,61 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // one group ahead: the loads of group g + 1 are in flight while group g is multiplied
-  // (deeper prefetch in registers spilled; this path is functional, not tuned)
-  bf8 a[MT][2] = {}, an[MT][2] = {};
-  u32x2 wv[NT] = {}, wn[NT] = {};
-  uint16_t sv[NT] = {}, bv[NT] = {}, sn[NT] = {}, bn[NT] = {};
-  auto load = [&](int g, bf8 (&aa)[MT][2], u32x2 (&ww)[NT], uint16_t (&ss)[NT], uint16_t (&bb)[NT]) {
+  // One group ahead, in two register sets with fixed roles (the loop is unrolled by two,
+  // so no set is copied): the loads of group g + 1 are in flight while group g is
+  // multiplied. Loads are unconditional (past the end they reload the last group, unused):
+  // loads under a condition made the compiler keep old and new sets live together. (Two
+  // groups ahead in three sets needed 285 VGPRs and was slower.)
+  struct Set {
+    bf8 a[MT][2];
+    u32x2 w[NT];
+    uint16_t s[NT], b[NT];
+  };
+  auto load = [&](int g, Set& st) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int s = 0; s < 2; ++s) aa[mt][s] = xa[((size_t)mt * nch + 2 * g + s) * 64];
+      for (int s = 0; s < 2; ++s) st.a[mt][s] = xa[((size_t)mt * nch + 2 * g + s) * 64];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      ww[nt] = __builtin_nontemporal_load(wr[nt] + 4 * g);
-      ss[nt] = sr[nt][g];
-      bb[nt] = br[nt][g];
+      st.w[nt] = wr[nt][4 * g];  // a plain load: the line serves the next three groups too
+      st.s[nt] = sr[nt][g];
+      st.b[nt] = br[nt][g];
     }
   };
-  if (g0 < g1) load(g0, a, wv, sv, bv);
-  for (int g = g0; g < g1; ++g) {
-    if (g + 1 < g1) load(g + 1, an, wn, sn, bn);
+  auto compute = [&](const Set& st) {
     f4 xs[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      xs[mt] = mfma(a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
-      xs[mt] = mfma(a[mt][1], ones, xs[mt]);
+      xs[mt] = mfma(st.a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
+      xs[mt] = mfma(st.a[mt][1], ones, xs[mt]);
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const bf8 b0 = nibbles_bf16(wv[nt][0]), b1 = nibbles_bf16(wv[nt][1]);
-      const float sc = bf2f(sv[nt]);
-      const float off = bf2f(bv[nt]) - 128.0f * sc;
+      const bf8 b0 = nibbles_bf16(st.w[nt][0]), b1 = nibbles_bf16(st.w[nt][1]);
+      const float sc = bf2f(st.s[nt]);
+      const float off = bf2f(st.b[nt]) - 128.0f * sc;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        f4 acc = mfma(a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
-        acc = mfma(a[mt][1], b1, acc);
+        f4 acc = mfma(st.a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
+        acc = mfma(st.a[mt][1], b1, acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      a[mt][0] = an[mt][0];
-      a[mt][1] = an[mt][1];
+  };
+  if (g0 < g1) {
+    Set A, B;
+    const int gl = g1 - 1;
+    load(g0, A);
+    int g = g0;
+    for (; g + 2 <= g1; g += 2) {
+      load(min(g + 1, gl), B);
+      compute(A);
+      load(min(g + 2, gl), A);
+      compute(B);
     }
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      wv[nt] = wn[nt];
-      sv[nt] = sn[nt];
-      bv[nt] = bn[nt];
-    }
+    if (g < g1) compute(A);  // an odd count: the last group is in A
   }
 
   // the four waves' partial sums (fixed order: wave 0 + 1 + 2 + 3), rounded to bf16 once
