@@ -690,13 +690,18 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
   f4 QS[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
+    // the four S^T fragments in flight together, then the products (one LDS latency
+    // instead of four: the register budget left the compiler no room to do it itself)
+    bf8 bs[kD / 32];
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) bs[ks] = frag(s.st, 16 * ct + fr, 32 * ks + fk);
+    __builtin_amdgcn_sched_barrier(0);
     f4 P = {0.f, 0.f, 0.f, 0.f};
     QS[ct] = P;
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) {
-      const bf8 bs = frag(s.st, 16 * ct + fr, 32 * ks + fk);
-      P = mfma(in.w[ks], bs, P);
-      QS[ct] = mfma(in.q[ks], bs, QS[ct]);
+      P = mfma(in.w[ks], bs[ks], P);
+      QS[ct] = mfma(in.q[ks], bs[ks], QS[ct]);
     }
     const f4 vpr = in.u[ct] - P;
     const bf4 hi = to_bf4(vpr);
@@ -716,14 +721,19 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
   // y = e^G . QS + M V' (split operands), staged in LDS
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
+    bf8 bh[kC / 32], bl[kC / 32];  // V' hi and lo fragments in flight together
+#pragma unroll
+    for (int ks = 0; ks < kC / 32; ++ks) {
+      bh[ks] = frag(s.vh, 16 * ct + fr, 32 * ks + fk);
+      bl[ks] = frag(s.vl, 16 * ct + fr, 32 * ks + fk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kC / 32; ++ks) {
-      const bf8 bh = frag(s.vh, 16 * ct + fr, 32 * ks + fk);
-      const bf8 bl = frag(s.vl, 16 * ct + fr, 32 * ks + fk);
-      acc = mfma(in.m[ks][0], bh, acc);
-      acc = mfma(in.m[ks][1], bh, acc);
-      acc = mfma(in.m[ks][0], bl, acc);
+      acc = mfma(in.m[ks][0], bh[ks], acc);
+      acc = mfma(in.m[ks][1], bh[ks], acc);
+      acc = mfma(in.m[ks][0], bl[ks], acc);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) s.y[16 * wave + fq + e][16 * ct + fr] = in.eg[e] * QS[ct][e] + acc[e];
@@ -733,13 +743,19 @@ __device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, 
   __builtin_amdgcn_sched_barrier(0);
   load_part<3>(p, b, g, h, jt, cn, wave, lane, nx);
   __builtin_amdgcn_sched_barrier(0);
+  bf8 bp[2][kC / 32];  // the four e^(G63-G) V' fragments in flight together
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int ks = 0; ks < kC / 32; ++ks) bp[ct][ks] = frag(s.vp, 16 * ct + fr, 32 * ks + fk);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       f4 acc = S[rt][ct] * in.gam;
 #pragma unroll
-      for (int ks = 0; ks < kC / 32; ++ks) acc = mfma(in.kt[rt][ks], frag(s.vp, 16 * ct + fr, 32 * ks + fk), acc);
+      for (int ks = 0; ks < kC / 32; ++ks) acc = mfma(in.kt[rt][ks], bp[ct][ks], acc);
       S[rt][ct] = acc;
     }
 }
