@@ -22,8 +22,9 @@
 // state is in flight (loads retire in order, so the reverse order would make the front
 // end wait for the whole tile).
 //
-// Blocks are mapped XCD-aware: the 6 workgroups that share a k-head (3 v-heads x 2
-// tiles) run on one XCD, whose L2 then serves their shared q/k/x reads.
+// Large grids (more than 16,384 workgroups: batched decode) are mapped XCD-aware: the 6
+// workgroups that share a k-head (3 v-heads x 2 tiles) run on one XCD, whose L2 then serves
+// their shared q/k/x reads; smaller grids keep dispatch order, which measured faster there.
 //
 // Reference semantics: cpp/src/delta.cpp:185-200 (step), 87-94 (collect), the gates of
 // cpp/src/model.cpp:608-612 and the front end of model.cpp:585-606 / 385-395.
