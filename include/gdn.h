@@ -132,9 +132,9 @@ typedef struct gdn_layer_args {
 int gdn_run(const gdn_layer_args* args);
 
 /* Chunked form (chunk 64, WY/UT transform) for prefill; same arguments as gdn_run
- * except that `states` must be NULL, a workspace is required, x and conv_state_in (conv
- * front end) or q, k and v (qkv front end) must be 16-byte aligned, and the qkv front end
- * takes bf16 q, k, v only. Intra-chunk products run on bf16 MFMA with fp32 accumulation;
+ * except that `states` must be NULL, a workspace is required, o and x and conv_state_in
+ * (conv front end) or q, k and v (qkv front end) must be 16-byte aligned, and the qkv
+ * front end takes bf16 q, k, v only. Intra-chunk products run on bf16 MFMA with fp32 accumulation;
  * the state hand-off between chunks stays fp32. The workspace contents are scratch: they
  * need no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);

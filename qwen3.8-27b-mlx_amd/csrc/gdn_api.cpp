@@ -282,6 +282,7 @@ int gdn_prefill_chunked(const gdn_layer_args* a) {
     return fail(GDN_EINVAL, "gdn_prefill_chunked: x and conv_state_in must be 16-byte aligned");
   if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16)))
     return fail(GDN_EINVAL, "gdn_prefill_chunked: q, k and v must be 16-byte aligned");
+  if (!aligned(a->o, 16)) return fail(GDN_EINVAL, "gdn_prefill_chunked: o must be 16-byte aligned");
   const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads,
                                                    a->num_v_heads, a->frontend == GDN_FRONTEND_CONV);
   if (a->seq_len > 0) {

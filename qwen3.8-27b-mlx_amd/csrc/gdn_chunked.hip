@@ -22,12 +22,17 @@
 //                  fragments from T in LDS (T' split into bf16 hi + lo for U). Results go
 //                  to the workspace, already in the register order of the MFMA operands
 //                  that read them.
-//   prefill_scan   one workgroup per (batch, v-head, 32-column Dv tile), serial over the
-//                  chunks; the fp32 state tile lives in MFMA accumulators. Each chunk's
-//                  operands go from the workspace straight into registers, two chunks
-//                  ahead of their use; LDS holds only the operands all four waves share
-//                  (S^T and V'). W S, Q S and K^T V'' use bf16 operands; M V' splits both
-//                  operands into bf16 hi + lo (three MFMAs).
+//   prefill_scan   one workgroup per (batch, v-head, pair of 16-column Dv tiles), serial
+//                  over the chunks. Each of two state waves keeps its tile's fp32 state
+//                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain V' = U - W S,
+//                  S = e^G63 S + K^T V'' with every operand in registers; two output waves
+//                  (positions 0..31 and 32..63 of a chunk) run one chunk behind on the S and
+//                  V' that the state waves leave in a double-buffered LDS mailbox: one
+//                  barrier per chunk. Operands go from the workspace straight into
+//                  registers two chunks ahead of their use, and the output waves touch the
+//                  lines of the chunk four ahead so that they are in L2 when first asked
+//                  for. W S, Q S and K^T V'' use bf16 operands; M V' splits both operands
+//                  into bf16 hi + lo (three MFMAs).
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
@@ -35,6 +40,16 @@
 // keep the 16 rows of a fragment on distinct banks. A matrix stored in "fragment order"
 // is a sequence of 16 x 32 blocks (row block major, then k block), each block being the
 // 64 lanes' 16-byte A fragments in lane order: one 1 KB coalesced load per fragment.
+//
+// Interleaved k order. The scan's B operands are accumulator tiles: two C tiles stacked
+// along k (rows 0..15 and 16..31 of a 32-row k block) give lane l the rows 4(l/16)+i and
+// 16+4(l/16)+i, i < 4, of column l%16 -- eight values of the B fragment when the k block
+// is read in the order k' = 8g + i <-> k = (i < 4 ? 4g + i : 16 + 4g + i - 4), g = l/16.
+// The A operands of those products (W and Q over dk, K^T and M over positions) are stored
+// in fragment order with their k blocks in that same order, so an accumulator tile turns
+// into a B fragment with two conversions and no data movement between lanes.
+#include <type_traits>
+
 #include "../../include/gdn.h"
 #include "gdn_device_math.h"
 #include "gdn_internal.h"
@@ -49,10 +64,10 @@ typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;             // chunk
 constexpr int kPadB = 8;           // bf16 padding per LDS row
-constexpr int kDt = 32;            // Dv columns per scan workgroup
+constexpr int kDt = 16;            // Dv columns per scan wave
 constexpr int kThreads = 256;
 constexpr int kGroup = 3;          // v-heads inverted together (one wave each)
-constexpr int kGStride = 132;      // floats per (v-head, chunk) in the gate workspace
+constexpr int kGStride = 128;      // floats per (v-head, chunk) in the gate workspace
 constexpr int kFrag = 512;         // bf16 elements of one 16 x 32 fragment block
 constexpr int kChunkElems = 8192;  // elements of one chunk's 64 x 128 (or 2 x 64 x 64) matrix
 
@@ -71,10 +86,21 @@ __device__ __forceinline__ f4 from_bf4(bf4 v) { return __builtin_convertvector(v
 // e^x for x <= 0 from the hardware 2^x (the decay factors inside a chunk).
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-// Offset, in a matrix of `kb` 32-column blocks stored in fragment order, of element
-// (row, col); col % 4 == 0 addresses 4 consecutive elements (8 bytes).
-__device__ __forceinline__ int frag_off(int row, int col, int kb) {
-  return ((row >> 4) * kb + (col >> 5)) * kFrag + ((row & 15) + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
+// Offset, in a matrix of `kb` 32-column blocks stored in fragment order with the
+// interleaved k order, of element (row, col); col % 4 == 0 addresses 4 consecutive
+// elements (8 bytes, one half of a lane's fragment).
+__device__ __forceinline__ int ilv_off(int row, int col, int kb) {
+  const int o = col & 31;
+  return ((row >> 4) * kb + (col >> 5)) * kFrag + ((row & 15) + 16 * ((o & 15) >> 2)) * 8 + 4 * (o >> 4) + (col & 3);
+}
+
+// The A fragment of rows row.., k block k0.. in the interleaved k order from an LDS matrix
+// stored [row][k]: lane group g = l/16 takes columns k0 + 4g .. +3 and k0 + 16 + 4g .. +3.
+template <int LD>
+__device__ __forceinline__ bf8 frag_ilv(const __bf16 (*m)[LD], int row, int k0, int g) {
+  const bf4 lo = *reinterpret_cast<const bf4*>(&m[row][k0 + 4 * g]);
+  const bf4 hi = *reinterpret_cast<const bf4*>(&m[row][k0 + 16 + 4 * g]);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 struct PrefillParams {
@@ -97,12 +123,13 @@ struct PrefillParams {
   float* state_out;
   void* o;
   // workspace, per chunk
-  __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128) in fragment order
-  __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64) in fragment order
-  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128) in fragment order
-  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64) in fragment order, hi and lo blocks interleaved
+  // (Q, K^T, W and M in fragment order with the interleaved k order)
+  __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128)
+  __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64)
+  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
+  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating
   float* ws_u;    // (B, Hv, nC): U   (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]
-  float* ws_g;    // (B, Hv, nC, kGStride): e^G [64], e^(G63-G) [64], e^G63
+  float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
   __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
                   // block 2 (dv / 16) + pos / 32, lane 16 ((pos % 32) / 8) + dv % 16, element
                   // pos % 8; positions past T are zeros
@@ -360,7 +387,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) {
-      *reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag) = frag(s.u.fe.q, 16 * wave + fr, 32 * ks + fk);
+      *reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag) = frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg);
     }
     const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
@@ -379,7 +406,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int a = 2 * wave + a2;
-        *reinterpret_cast<bf8*>(wkt + (a * 2 + ks) * kFrag) = frag(s.kt, 16 * a + fr, 32 * ks + fk);
+        *reinterpret_cast<bf8*>(wkt + (a * 2 + ks) * kFrag) = frag_ilv(s.kt, 16 * a + fr, 32 * ks, lg);
       }
   }
 
@@ -413,10 +440,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       const float eg = d_expf(G);
       s.eG[wave][lane] = eg;
       const float Gl = __shfl(G, 63, 64);
-      float* wg = p.ws_g + hc * kGStride;
-      wg[lane] = eg;
-      wg[64 + lane] = d_expf(Gl - G);
-      if (lane == 0) wg[128] = d_expf(Gl);
+      reinterpret_cast<float2*>(p.ws_g + hc * kGStride)[lane] = make_float2(eg, d_expf(Gl - G));
     }
     __syncthreads();
 
@@ -440,11 +464,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         }
         const bf4 hi = to_bf4(mv);
         const bf4 lo = to_bf4(mv - from_bf4(hi));
-        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks interleaved
-        const int blk = ((i >> 4) * 2 + (j0 >> 5)) * 2;
-        const int within = ((i & 15) + 16 * ((j0 & 31) >> 3)) * 8 + (j0 & 7);
-        *reinterpret_cast<bf4*>(wm + blk * kFrag + within) = hi;
-        *reinterpret_cast<bf4*>(wm + (blk + 1) * kFrag + within) = lo;
+        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating
+        const int off = ilv_off(i, j0, 2);
+        const int blk = off / kFrag, within = off % kFrag;
+        *reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within) = hi;
+        *reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within) = lo;
       }
     }
     __syncthreads();
@@ -535,7 +559,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
             f4 acc = {0.f, 0.f, 0.f, 0.f};
             acc = mfma(k0, te[bt][0], acc);
             acc = mfma(k1, te[bt][1], acc);
-            *reinterpret_cast<bf4*>(ww + frag_off(16 * bt + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
+            *reinterpret_cast<bf4*>(ww + ilv_off(16 * bt + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
           }
         }
       }
@@ -581,248 +605,353 @@ __global__ __launch_bounds__(kThreads) void prefill_vfrag_kernel(PrefillParams p
 
 // ============================================================================ scan
 
-struct ScanSmem {
-  __bf16 st[kDt][kD + kPadB];  // S^T (bf16): [dt][dk]
-  __bf16 vh[kDt][kC + kPadB];  // V' hi: [dt][pos]
-  __bf16 vl[kDt][kC + kPadB];  // V' lo
-  __bf16 vp[kDt][kC + kPadB];  // e^(G63-G) V'
-  float y[kC][kDt + 4];        // the chunk's outputs, written to o one chunk later
+constexpr int kScanNt = 2;                  // 16-column MFMA tiles per scan workgroup
+constexpr int kScanGroups = kD / (kDt * kScanNt);  // scan workgroups per v-head
+
+// What the state wave hands the output waves for one chunk, per lane (lane l's entries are
+// written by lane l of the state wave and read by lane l of the output waves): S before
+// the chunk as the B operand of Q S, and V'.
+template <int NT>
+struct ScanMail {
+  bf8 sb[NT][kD / 32][64];
+  f4 vpr[NT][4][64];
 };
 
-// The outputs staged in s.y for the chunk starting at t0 (n positions) to o: thread t
-// stores positions t / 4, columns 8 (t % 4) .. +7 of the tile, 16 or 32 bytes.
-__device__ __forceinline__ void store_outputs(const PrefillParams& p, const ScanSmem& s, int b, int h, int jt, int t0,
-                                              int n, int tid) {
-  const int pos = tid >> 2, c8 = (tid & 3) * 8;
-  if (pos >= n) return;
-  const f4 y0 = *reinterpret_cast<const f4*>(&s.y[pos][c8]);
-  const f4 y1 = *reinterpret_cast<const f4*>(&s.y[pos][c8 + 4]);
-  const size_t oi = (((size_t)b * p.T + t0 + pos) * p.Hv + h) * kD + jt * kDt + c8;
-  if (p.o_bf16) {
-    bf8 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = (__bf16)y0[e];
-      v[4 + e] = (__bf16)y1[e];
-    }
-    *reinterpret_cast<bf8*>(static_cast<__bf16*>(p.o) + oi) = v;
+// The state wave's operands of one chunk, in the register order of the MFMAs that read them.
+template <int NT>
+struct StateOps {
+  bf8 w[4][4];    // W   [pos tile][dk block]   (A of W S)
+  bf8 kt[8][2];   // K^T [dk tile][pos block]   (A of K^T V'')
+  f4 u[NT][4];    // U   [dv tile][pos tile]: positions 16 pt + 4 lg + e, column fr
+  float2 g;       // (e^G, e^(G63-G)) at position `lane`
+};
+
+// An output wave's operands of one chunk: its two position tiles 2 half, 2 half + 1.
+struct OutOps {
+  bf8 q[2][4];     // Q [pos tile][dk block]          (A of Q S)
+  bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V')
+  float eg;        // e^G at position `lane`
+  unsigned touch[2];  // the cache-line touches issued with this set (see touch_lines)
+};
+
+// Chunk operands reach L2 two chunks ahead of their use when the first wave to ask for a
+// line finds it already there: every workgroup of a v-head asks for the same lines at the
+// same time, so a line fetched on demand costs all of them the full memory latency. The
+// output waves therefore touch (one dword per 128-byte line) the lines of the chunk four
+// ahead: the v-head's four workgroups split W, M, Q and K^T between them (group `grp`
+// takes one of the four 16 KB matrices), and each workgroup touches its own U columns and
+// the gate pairs.
+__device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, size_t hc, int grp, int jt, int half,
+                                            int lane, unsigned (&t)[2]) {
+  const unsigned* base;
+  if (half == 0) {
+    const int r = grp & 3;
+    const __bf16* m = r == 0 ? p.ws_w + hc * kChunkElems
+                    : r == 1 ? p.ws_m + hc * kChunkElems
+                    : r == 2 ? p.ws_q + gc * kChunkElems
+                             : p.ws_kt + gc * kChunkElems;
+    base = reinterpret_cast<const unsigned*>(m);
+    t[0] = base[lane * 32];
+    t[1] = base[(64 + lane) * 32];
   } else {
-    *reinterpret_cast<f4*>(static_cast<float*>(p.o) + oi) = y0;
-    *reinterpret_cast<f4*>(static_cast<float*>(p.o) + oi + 4) = y1;
+    base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
+    t[0] = base[lane * 32];
+    t[1] = reinterpret_cast<const unsigned*>(p.ws_g + hc * kGStride)[(lane & 3) * 32];
   }
 }
 
-// One chunk's operands of one wave, in registers.
-struct ChunkIn {
-  bf8 q[4];       // Q rows 16w.., k = dk
-  bf8 w[4];       // W rows 16w.., k = dk
-  bf8 kt[2][2];   // K^T rows 32w + 16rt.., k = pos
-  bf8 m[2][2];    // M rows 16w.., k = pos; [ks][hi, lo]
-  f4 u[2];        // U (pos 16w + 4lg + e, dv 32jt + 16ct + fr)
-  f4 eg, egr;     // e^G, e^(G63-G) at pos 16w + 4lg + e
-  float gam;      // e^G63
-};
-
-// Part PART of one chunk's operands: 0 Q and the gate factors, 1 W, 2 M and U, 3 K^T.
-// The parts are issued at different points of a chunk so that the memory pipeline is
-// fed evenly and the wave is never held at a long run of loads.
-template <int PART>
-__device__ __forceinline__ void load_part(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
-                                          int lane, ChunkIn& in) {
-  const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
-  const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-  if (PART == 0) {
-    const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
+// Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc; jt is the
+// workgroup's first 16-column Dv tile.
+template <int NT>
+__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int lane, StateOps<NT>& op) {
+  const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) in.q[ks] = *reinterpret_cast<const bf8*>(q + (wave * 4 + ks) * kFrag);
-    const float* gg = p.ws_g + hc * kGStride + 16 * wave + 4 * (lane >> 4);
-    in.eg = *reinterpret_cast<const f4*>(gg);
-    in.egr = *reinterpret_cast<const f4*>(gg + 64);
-    in.gam = p.ws_g[hc * kGStride + 128];
-  } else if (PART == 1) {
-    const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
+  for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) in.w[ks] = *reinterpret_cast<const bf8*>(w + (wave * 4 + ks) * kFrag);
-  } else if (PART == 2) {
-    const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
+    for (int ks = 0; ks < 4; ++ks) op.w[pt][ks] = *reinterpret_cast<const bf8*>(w + (pt * 4 + ks) * kFrag);
+  const float* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) in.m[i][j] = *reinterpret_cast<const bf8*>(m + ((wave * 2 + i) * 2 + j) * kFrag);
-    const float* u = p.ws_u + hc * kChunkElems + lane * 4;
+    for (int pt = 0; pt < 4; ++pt) op.u[n][pt] = *reinterpret_cast<const f4*>(u + (n * 4 + pt) * 256);
+  op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
+}
+template <int NT>
+__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int lane, StateOps<NT>& op) {
+  const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) in.u[ct] = *reinterpret_cast<const f4*>(u + ((2 * jt + ct) * 4 + wave) * 256);
-  } else {
-    const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
+  for (int a = 0; a < 8; ++a)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int ks = 0; ks < 2; ++ks) op.kt[a][ks] = *reinterpret_cast<const bf8*>(kt + (a * 2 + ks) * kFrag);
+}
+__device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_t hc, int half, int lane, OutOps& op) {
+  const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
+  const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) in.kt[i][j] = *reinterpret_cast<const bf8*>(kt + ((2 * wave + i) * 2 + j) * kFrag);
+  for (int i = 0; i < 2; ++i) {
+    const int pt = 2 * half + i;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) op.q[i][ks] = *reinterpret_cast<const bf8*>(q + (pt * 4 + ks) * kFrag);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl) op.m[i][ks][hl] = *reinterpret_cast<const bf8*>(m + ((pt * 2 + ks) * 2 + hl) * kFrag);
   }
+  op.eg = p.ws_g[hc * kGStride + 2 * lane];
 }
 
-__device__ __forceinline__ void load_chunk(const PrefillParams& p, int b, int g, int h, int jt, int c, int wave,
-                                           int lane, ChunkIn& in) {
-  load_part<0>(p, b, g, h, jt, c, wave, lane, in);
-  load_part<1>(p, b, g, h, jt, c, wave, lane, in);
-  load_part<2>(p, b, g, h, jt, c, wave, lane, in);
-  load_part<3>(p, b, g, h, jt, c, wave, lane, in);
+// Two accumulator tiles (k rows 0..15 and 16..31 of a block) as one B fragment in the
+// interleaved k order.
+__device__ __forceinline__ bf8 stack_bf8(f4 lo, f4 hi) {
+  return __builtin_shufflevector(to_bf4(lo), to_bf4(hi), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// One chunk: uses `in`, loads chunk c + 2 (the last chunk again at the end) into `nx`.
-__device__ __forceinline__ void scan_chunk(const PrefillParams& p, ScanSmem& s, f4 (&S)[2][2], const ChunkIn& in,
-                                           ChunkIn& nx, int b, int g, int h, int jt, int c, int wave, int lane) {
-  const int fr = lane & 15, fk = (lane >> 4) * 8, fq = (lane >> 4) * 4;
-  // S^T in bf16 for the W S and Q S products
+// The per-position value v (lane t holds position t) at positions 16 pt + 4 (lane / 16) + e,
+// e < 4: the accumulator-row order.
+__device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
+  f4 r;
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-      *reinterpret_cast<bf4*>(&s.st[16 * ct + fr][32 * wave + 16 * rt + fq]) = to_bf4(S[rt][ct]);
-  __syncthreads();
-  const int cn = min(c + 2, p.nC - 1);
-  load_part<0>(p, b, g, h, jt, cn, wave, lane, nx);
-  __builtin_amdgcn_sched_barrier(0);
-  // the previous chunk's outputs (staged before this chunk's first barrier)
-  if (c > 0) store_outputs(p, s, b, h, jt, (c - 1) * kC, kC, threadIdx.x);
+  for (int e = 0; e < 4; ++e) r[e] = __shfl(v, 16 * pt + 4 * (lane >> 4) + e, 64);
+  return r;
+}
 
-  // P = W S, QS = Q S (wave w: positions 16w..); V' = U - P
-  f4 QS[2];
+// The state wave of (batch b, v-head h, Dv tiles jt .. jt + NT - 1): S[n][a] holds the
+// state's rows dk = 16 a + 4 lg + e (lg = lane / 16) of column dv = 16 (jt + n) + lane % 16
+// (S^T as accumulator tiles). Chunk c: V' = U - W S, S = e^G63 S + K^T (e^(G63-G) V');
+// S before the update and V' go to mail[c % 2]. `op` holds chunk c's operands and is
+// reloaded with those of chunk cn (two chunks on) right after their last product.
+template <int NS, int NT>
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, f4 (&S)[NS][kD / 16],
+                                            StateOps<NS>& op, size_t gcn, size_t hcn, int jt, int n0, int lane) {
+  bf8 sb[NS][kD / 32];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    // the four S^T fragments in flight together, then the products (one LDS latency
-    // instead of four: the register budget left the compiler no room to do it itself)
-    bf8 bs[kD / 32];
-#pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) bs[ks] = frag(s.st, 16 * ct + fr, 32 * ks + fk);
-    __builtin_amdgcn_sched_barrier(0);
-    f4 P = {0.f, 0.f, 0.f, 0.f};
-    QS[ct] = P;
+  for (int n = 0; n < NS; ++n)
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) {
-      P = mfma(in.w[ks], bs[ks], P);
-      QS[ct] = mfma(in.q[ks], bs[ks], QS[ct]);
+      sb[n][ks] = stack_bf8(S[n][2 * ks], S[n][2 * ks + 1]);
+      mb.sb[n0 + n][ks][lane] = sb[n][ks];
     }
-    const f4 vpr = in.u[ct] - P;
-    const bf4 hi = to_bf4(vpr);
-    *reinterpret_cast<bf4*>(&s.vh[16 * ct + fr][16 * wave + fq]) = hi;
-    *reinterpret_cast<bf4*>(&s.vl[16 * ct + fr][16 * wave + fq]) = to_bf4(vpr - from_bf4(hi));
-    *reinterpret_cast<bf4*>(&s.vp[16 * ct + fr][16 * wave + fq]) = to_bf4(in.egr * vpr);
-    if (ct == 0) {
-      __builtin_amdgcn_sched_barrier(0);
-      load_part<1>(p, b, g, h, jt, cn, wave, lane, nx);
-      __builtin_amdgcn_sched_barrier(0);
+  f4 egr[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) egr[pt] = rows_of(op.g.y, pt, lane);
+  const float gam = __shfl(op.g.x, 63, 64);
+  f4 vpr[NS][4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      f4 P = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kD / 32; ++ks) P = mfma(op.w[pt][ks], sb[n][ks], P);
+      vpr[n][pt] = op.u[n][pt] - P;
+      mb.vpr[n0 + n][pt][lane] = vpr[n][pt];
     }
-  }
-  __syncthreads();
-  load_part<2>(p, b, g, h, jt, cn, wave, lane, nx);
+  bf8 vb[NS][2];
+#pragma unroll
+  for (int n = 0; n < NS; ++n)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) vb[n][ks] = stack_bf8(egr[2 * ks] * vpr[n][2 * ks], egr[2 * ks + 1] * vpr[n][2 * ks + 1]);
+  // (the reloads stay where they are written: the scheduler would otherwise sink them
+  // to the end of the chunk)
   __builtin_amdgcn_sched_barrier(0);
-
-  // y = e^G . QS + M V' (split operands), staged in LDS
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    bf8 bh[kC / 32], bl[kC / 32];  // V' hi and lo fragments in flight together
-#pragma unroll
-    for (int ks = 0; ks < kC / 32; ++ks) {
-      bh[ks] = frag(s.vh, 16 * ct + fr, 32 * ks + fk);
-      bl[ks] = frag(s.vl, 16 * ct + fr, 32 * ks + fk);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kC / 32; ++ks) {
-      acc = mfma(in.m[ks][0], bh[ks], acc);
-      acc = mfma(in.m[ks][1], bh[ks], acc);
-      acc = mfma(in.m[ks][0], bl[ks], acc);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s.y[16 * wave + fq + e][16 * ct + fr] = in.eg[e] * QS[ct][e] + acc[e];
-  }
-
-  // S = e^G63 S + K^T (e^(G63-G) V')
-  __builtin_amdgcn_sched_barrier(0);
-  load_part<3>(p, b, g, h, jt, cn, wave, lane, nx);
-  __builtin_amdgcn_sched_barrier(0);
-  bf8 bp[2][kC / 32];  // the four e^(G63-G) V' fragments in flight together
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-    for (int ks = 0; ks < kC / 32; ++ks) bp[ct][ks] = frag(s.vp, 16 * ct + fr, 32 * ks + fk);
+  load_wu<NS>(p, hcn, jt, lane, op);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int a = 0; a < kD / 16; ++a)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      f4 acc = S[rt][ct] * in.gam;
+    for (int n = 0; n < NS; ++n) {
+      f4 acc = S[n][a] * gam;
 #pragma unroll
-      for (int ks = 0; ks < kC / 32; ++ks) acc = mfma(in.kt[rt][ks], bp[ct][ks], acc);
-      S[rt][ct] = acc;
+      for (int ks = 0; ks < 2; ++ks) acc = mfma(op.kt[a][ks], vb[n][ks], acc);
+      S[n][a] = acc;
     }
+  __builtin_amdgcn_sched_barrier(0);
+  load_kt<NS>(p, gcn, lane, op);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // mail[c % 2] is complete; the output waves have read mail[(c + 1) % 2]
 }
 
-__global__ __launch_bounds__(kThreads) void prefill_scan_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) ScanSmem s;
+// Operands are loaded two chunks ahead, in two register sets used by alternate chunks (an
+// unrolled pair of chunks per loop trip, so the sets never move between registers), issued
+// in the order the loop reissues them so that the loop is entered with the same loads in
+// flight as at its back edge. One barrier per chunk, and one more at the end, as the
+// output waves.
+template <int NS, int NT>
+__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], int b, int h, int g,
+                                                int jt, int n0, int lane) {
+  const int fr = lane & 15, lg = lane >> 4;
+  const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
+  const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
+  const size_t srow = ((size_t)b * p.Hv + h) * kD * kD + (size_t)(jt * kDt + fr) * kD + 4 * lg;
+  f4 S[NS][kD / 16];
+#pragma unroll
+  for (int n = 0; n < NS; ++n)
+#pragma unroll
+    for (int a = 0; a < kD / 16; ++a)
+      S[n][a] = p.state_in ? *reinterpret_cast<const f4*>(p.state_in + srow + (size_t)n * kDt * kD + 16 * a)
+                           : f4{0.f, 0.f, 0.f, 0.f};
+
+  const int last = p.nC - 1;
+  StateOps<NS> A, B;
+  __builtin_amdgcn_sched_barrier(0);
+  load_wu<NS>(p, hc0, jt, lane, A);
+  __builtin_amdgcn_sched_barrier(0);
+  load_kt<NS>(p, gc0, lane, A);
+  __builtin_amdgcn_sched_barrier(0);
+  load_wu<NS>(p, hc0 + min(1, last), jt, lane, B);
+  __builtin_amdgcn_sched_barrier(0);
+  load_kt<NS>(p, gc0 + min(1, last), lane, B);
+  __builtin_amdgcn_sched_barrier(0);
+  int c = 0;
+  for (; c + 2 <= p.nC; c += 2) {
+    state_chunk<NS, NT>(p, mail[0], S, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, n0, lane);
+    state_chunk<NS, NT>(p, mail[1], S, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, n0, lane);
+  }
+  if (c < p.nC) state_chunk<NS, NT>(p, mail[0], S, A, gc0 + last, hc0 + last, jt, n0, lane);
+  __syncthreads();
+
+  if (p.state_out) {
+#pragma unroll
+    for (int n = 0; n < NS; ++n)
+#pragma unroll
+      for (int a = 0; a < kD / 16; ++a)
+        *reinterpret_cast<f4*>(p.state_out + srow + (size_t)n * kDt * kD + 16 * a) = S[n][a];
+  }
+}
+
+// An output wave's staging tile: its 32 positions x NT * 16 columns of the chunk's outputs,
+// written in accumulator order and read back as 16-byte pieces of one position's columns.
+template <int NT, typename OT>
+struct OutTile {
+  OT y[32][NT * kDt + 16 / sizeof(OT)];
+};
+
+// Output wave `half` (positions 32 half .. 32 half + 31 of each chunk), one chunk behind
+// the state wave (chunk c after its barrier c): y = e^G . (Q S) + M V' (V' split into bf16
+// hi + lo) from mail[c % 2]; `op` is reloaded with chunk cn's operands and touches the
+// lines of chunk c + 4 (gc4, hc4). The touches issued with this set two chunks ago have
+// long arrived: they are folded into `tacc` only so that they stay live.
+template <int NT, bool OBF16>
+__device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
+                                             OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
+                                             OutOps& op, size_t gcn, size_t hcn, size_t gc4, size_t hc4, int b, int h,
+                                             int jt, int half, int c, int lane, unsigned& tacc) {
+  typedef typename std::conditional<OBF16, __bf16, float>::type OT;
+  const int fr = lane & 15, lg = lane >> 4;
+  tacc ^= op.touch[0] ^ op.touch[1];
+  f4 eg[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) eg[i] = rows_of(op.eg, 2 * half + i, lane);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    bf8 sb[kD / 32];
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks) sb[ks] = mb.sb[n][ks][lane];
+    f4 vpr[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) vpr[pt] = mb.vpr[n][pt][lane];
+    bf8 vh[2], vl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf4 h0 = to_bf4(vpr[2 * ks]), h1 = to_bf4(vpr[2 * ks + 1]);
+      vh[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+      vl[ks] = stack_bf8(vpr[2 * ks] - from_bf4(h0), vpr[2 * ks + 1] - from_bf4(h1));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f4 qs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kD / 32; ++ks) qs = mfma(op.q[i][ks], sb[ks], qs);
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        acc = mfma(op.m[i][ks][0], vh[ks], acc);
+        acc = mfma(op.m[i][ks][1], vh[ks], acc);
+        acc = mfma(op.m[i][ks][0], vl[ks], acc);
+      }
+      const f4 y = eg[i] * qs + acc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile.y[16 * i + 4 * lg + e][16 * n + fr] = (OT)y[e];
+    }
+  }
+
+  // lane l stores position 32 half + l / 2, columns 16 (jt + (l % 2) * NT / 2) ..: NT * 8
+  // consecutive columns, 16 bytes at a time (the tile rows were written by this wave)
+  constexpr int kPer = NT * kDt / 2;  // columns per lane
+  constexpr int kVec = 16 / sizeof(OT);
+  const int row = lane >> 1, col = (lane & 1) * kPer;
+  const int t = c * kC + 32 * half + row;
+  if (t < p.T) {
+    OT* o = static_cast<OT*>(p.o) + ((size_t)b * p.T + t) * p.Hv * kD + (size_t)h * kD + jt * kDt + col;
+#pragma unroll
+    for (int v = 0; v < kPer / kVec; ++v)
+      *reinterpret_cast<f4*>(o + v * kVec) = *reinterpret_cast<const f4*>(&tile.y[row][col + v * kVec]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_qm(p, gcn, hcn, half, lane, op);
+  touch_lines(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // done with mail[c % 2]; mail[(c + 1) % 2] is complete
+}
+
+template <int NT, bool OBF16>
+__device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
+                                                 OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
+                                                 int b, int h, int g, int jt, int half, int lane) {
+  const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
+  const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
+  const int last = p.nC - 1;
+  const int grp = jt / NT;
+  unsigned tacc = 0;
+  OutOps A, B;
+  __builtin_amdgcn_sched_barrier(0);
+  load_qm(p, gc0, hc0, half, lane, A);
+  touch_lines(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
+  __builtin_amdgcn_sched_barrier(0);
+  load_qm(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
+  touch_lines(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  int c = 0;
+  for (; c + 2 <= p.nC; c += 2) {
+    output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
+                            gc0 + min(c + 4, last), hc0 + min(c + 4, last), b, h, jt, half, c, lane, tacc);
+    output_chunk<NT, OBF16>(p, mail[1], tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
+                            gc0 + min(c + 5, last), hc0 + min(c + 5, last), b, h, jt, half, c + 1, lane, tacc);
+  }
+  if (c < p.nC)
+    output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half, c,
+                            lane, tacc);
+  // (never true: T >= 1; it keeps the touches from being dropped as unused)
+  if (tacc == 0x9e3779b9u && p.T < 0) static_cast<float*>(p.o)[lane] = 0.0f;
+}
+
+// Workgroup = (batch, v-head, NT 16-column Dv tiles): waves 0 .. NT-1 carry the state of
+// one tile each, waves NT and NT + 1 make the outputs of positions 0..31 and 32..63 of
+// each chunk for all NT tiles. All waves pass nC + 1 barriers.
+template <int NT, bool OBF16>
+__global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
+  typedef typename std::conditional<OBF16, __bf16, float>::type OT;
+  __shared__ __attribute__((aligned(16))) ScanMail<NT> mail[2];
+  __shared__ __attribute__((aligned(16))) OutTile<NT, OT> tiles[2];
   // Workgroups are dispatched to the 8 XCDs round robin (bid % 8); renumber them so that
-  // each XCD gets a contiguous range of (batch, v-head, tile) -- whole k-head groups when
-  // the count divides -- and the chunk operands they share are fetched into one L2.
+  // each XCD gets a contiguous range of (batch, v-head, tiles) -- whole v-heads, and whole
+  // k-head groups when the count divides -- and the chunk operands those waves share are
+  // fetched into one L2.
+  constexpr int kGroups = kD / (kDt * NT);
   int bid = blockIdx.x;
-  if (gridDim.x % 8 == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
-  const int jt = bid % (kD / kDt);
-  const int rest = bid / (kD / kDt);
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int jt = (bid % kGroups) * NT;
+  const int rest = bid / kGroups;
   const int h = rest % p.Hv;
   const int b = rest / p.Hv;
   const int g = h / p.rep;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int fr = lane & 15, fq = (lane >> 4) * 4;
-
-  // S tile (Dk x 32) in accumulators: wave w holds dk rows 32w + 16rt + fq + e, dt 16ct + fr
-  f4 S[2][2];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      S[rt][ct] = f4{0.f, 0.f, 0.f, 0.f};
-      if (p.state_in) {
-        const float* sin = p.state_in + ((size_t)b * p.Hv + h) * kD * kD;
-        S[rt][ct] = *reinterpret_cast<const f4*>(sin + (size_t)(jt * kDt + 16 * ct + fr) * kD + 32 * wave + 16 * rt + fq);
-      }
-    }
-
-  // Operands are loaded two chunks ahead of their use (memory latency under this load
-  // is longer than one chunk's work), in three register sets that rotate. The loop body
-  // is three unconditional chunks and is only reached through three peeled ones, so it
-  // is entered with the same loads in flight, in the same registers, as at its back
-  // edge: the waits for a chunk's operands then never cover the loads issued after them.
-  ChunkIn A, B, C;
-  load_chunk(p, b, g, h, jt, 0, wave, lane, A);
-  load_chunk(p, b, g, h, jt, min(1, p.nC - 1), wave, lane, B);
-  if (p.nC < 3) {
-    scan_chunk(p, s, S, A, C, b, g, h, jt, 0, wave, lane);
-    if (p.nC > 1) scan_chunk(p, s, S, B, A, b, g, h, jt, 1, wave, lane);
+  if (wave < NT) {
+    scan_state_wave<1, NT>(p, mail, b, h, g, jt + wave, wave, lane);
   } else {
-    scan_chunk(p, s, S, A, C, b, g, h, jt, 0, wave, lane);
-    scan_chunk(p, s, S, B, A, b, g, h, jt, 1, wave, lane);
-    scan_chunk(p, s, S, C, B, b, g, h, jt, 2, wave, lane);
-    int c = 3;
-    for (; c + 3 <= p.nC; c += 3) {
-      scan_chunk(p, s, S, A, C, b, g, h, jt, c, wave, lane);
-      scan_chunk(p, s, S, B, A, b, g, h, jt, c + 1, wave, lane);
-      scan_chunk(p, s, S, C, B, b, g, h, jt, c + 2, wave, lane);
-    }
-    if (c < p.nC) scan_chunk(p, s, S, A, C, b, g, h, jt, c, wave, lane);
-    if (c + 1 < p.nC) scan_chunk(p, s, S, B, A, b, g, h, jt, c + 1, wave, lane);
-  }
-  __syncthreads();
-  store_outputs(p, s, b, h, jt, (p.nC - 1) * kC, p.T - (p.nC - 1) * kC, threadIdx.x);
-
-  if (p.state_out) {
-    float* sout = p.state_out + ((size_t)b * p.Hv + h) * kD * kD;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        *reinterpret_cast<f4*>(sout + (size_t)(jt * kDt + 16 * ct + fr) * kD + 32 * wave + 16 * rt + fq) = S[rt][ct];
+    scan_output_wave<NT, OBF16>(p, mail, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
   }
 }
 
@@ -905,7 +1034,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
 
   const dim3 block(kThreads);
   const dim3 g1((unsigned)((size_t)p.B * p.Hk * p.nC));
-  const dim3 g2((unsigned)((size_t)p.B * p.Hv * (kD / kDt)));
+  const dim3 g2((unsigned)((size_t)p.B * p.Hv * kScanGroups));
   if (conv) {
     const size_t nh = ((size_t)2 * p.Hk + p.Hv + kFeHeads - 1) / kFeHeads;
     const dim3 g0((unsigned)((size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
@@ -919,7 +1048,11 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   } else {
     hipLaunchKernelGGL((prefill_intra_kernel<false>), g1, block, 0, stream, p);
   }
-  hipLaunchKernelGGL(prefill_scan_kernel, g2, block, 0, stream, p);
+  if (p.o_bf16) {
+    hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

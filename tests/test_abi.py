@@ -121,18 +121,19 @@ def test_run_rejects_bad_arguments(gdn, kw, msg):
 
 def test_prefill_workspace_size_and_checks(gdn):
     # per chunk: Q, K^T per k-head (bf16 64 x 128); W, M hi/lo, V in fragment order (bf16)
-    # and U (fp32) per v-head; gate scalars; with the conv front end also its bf16 q, k;
+    # and U (fp32) per v-head; two gate factors per position; with the conv front end also
+    # its bf16 q, k;
     # 256-byte aligned pieces
     n_qkv = gdn.prefill_workspace_size(1, 4096, conv=False)
     assert n_qkv == (2 * 16 * 64 * 8192 * 2 + 3 * 48 * 64 * 8192 * 2 + 48 * 64 * 8192 * 4
-                     + 48 * 64 * 132 * 4)
+                     + 48 * 64 * 128 * 4)
     assert gdn.prefill_workspace_size(1, 4096) == n_qkv + 4096 * (16 + 16) * 128 * 2
     # a ragged T: whole chunks for the per-chunk pieces, T rows for the q, k staging
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     nc = (100 + 63) // 64
     assert gdn.prefill_workspace_size(2, 100) == (
         2 * al(2 * 16 * nc * 8192 * 2) + 3 * al(2 * 48 * nc * 8192 * 2) + al(2 * 48 * nc * 8192 * 4)
-        + al(2 * 48 * nc * 132 * 4) + 2 * al(2 * 100 * 16 * 128 * 2))
+        + al(2 * 48 * nc * 128 * 4) + 2 * al(2 * 100 * 16 * 128 * 2))
     L = gdn.lib()
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100)))
     assert rc == gdn.GDN_EINVAL and "workspace" in gdn.last_error()
@@ -141,6 +142,10 @@ def test_prefill_workspace_size_and_checks(gdn):
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, workspace=0x10000010,
                                                   workspace_bytes=1 << 40)))
     assert rc == gdn.GDN_EINVAL and "256-byte" in gdn.last_error()
+    # the outputs are written as 16-byte pieces of a position's columns
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, o=0x9000002, workspace=0x10000000,
+                                                  workspace_bytes=1 << 40)))
+    assert rc == gdn.GDN_EINVAL and "o must be 16-byte aligned" in gdn.last_error()
 
 
 def test_null_args_and_prefill_states(gdn):

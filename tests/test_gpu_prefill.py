@@ -122,12 +122,14 @@ def test_prefill_then_decode_continues(O, gdn, dev):
 
 
 def _from_fragments(blocks, rows: int, cols: int):
-    """A matrix stored in MFMA A-fragment order -- 16 x 32 blocks, row block major; in a
-    block, lane l = 16 lg + fr holds row fr, columns 8 lg .. 8 lg + 7 -- to row-major."""
+    """A matrix stored in MFMA A-fragment order with the interleaved k order -- 16 x 32
+    blocks, row block major; in a block, lane l = 16 lg + fr holds row fr, columns
+    4 lg .. 4 lg + 3 (elements 0..3) and 16 + 4 lg .. 16 + 4 lg + 3 (elements 4..7) -- to
+    row-major."""
     lead = blocks.shape[:-1]
-    a = blocks.reshape(*lead, rows // 16, cols // 32, 4, 16, 8)   # [rt][ks][lg][fr][i]
-    nd = a.ndim
-    a = np.moveaxis(a, nd - 2, nd - 4)                              # [rt][fr][ks][lg][i]
+    a = blocks.reshape(*lead, rows // 16, cols // 32, 4, 16, 2, 4)   # [rt][ks][lg][fr][half][e]
+    n = len(lead)
+    a = a.transpose(*range(n), n, n + 3, n + 1, n + 4, n + 2, n + 5)  # [rt][fr][ks][half][lg][e]
     return a.reshape(*lead, rows, cols)
 
 
