@@ -617,13 +617,15 @@ struct ScanMail {
   f4 vpr[NT][4][64];
 };
 
-// The state wave's operands of one chunk, in the register order of the MFMAs that read them.
-template <int NT>
+// A state wave's share of one chunk's operands, in the register order of the MFMAs that
+// read them. The two state waves of a workgroup need all of W and K^T; each loads half
+// (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles 4i .. 4i + 3) and passes it
+// to the other through LDS (ScanShared).
 struct StateOps {
-  bf8 w[4][4];    // W   [pos tile][dk block]   (A of W S)
-  bf8 kt[8][2];   // K^T [dk tile][pos block]   (A of K^T V'')
-  f4 u[NT][4];    // U   [dv tile][pos tile]: positions 16 pt + 4 lg + e, column fr
-  float2 g;       // (e^G, e^(G63-G)) at position `lane`
+  bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
+  bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
+  f4 u[4];       // U   [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile
+  float2 g;      // (e^G, e^(G63-G)) at position `lane`
 };
 
 // An output wave's operands of one chunk: its two position tiles 2 half, 2 half + 1.
@@ -660,29 +662,25 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
   }
 }
 
-// Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc; jt is the
-// workgroup's first 16-column Dv tile.
-template <int NT>
-__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int lane, StateOps<NT>& op) {
+// Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc: state wave
+// i's halves of W (with its tile jt's U and the gates) and of K^T.
+__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int i, int lane, StateOps& op) {
   const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt)
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) op.w[pt][ks] = *reinterpret_cast<const bf8*>(w + (pt * 4 + ks) * kFrag);
+    for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
   const float* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
-  for (int n = 0; n < NT; ++n)
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) op.u[n][pt] = *reinterpret_cast<const f4*>(u + (n * 4 + pt) * 256);
+  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const f4*>(u + pt * 256);
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
-template <int NT>
-__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int lane, StateOps<NT>& op) {
+__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int i, int lane, StateOps& op) {
   const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
-  for (int a = 0; a < 8; ++a)
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) op.kt[a][ks] = *reinterpret_cast<const bf8*>(kt + (a * 2 + ks) * kFrag);
+    for (int ks = 0; ks < 2; ++ks) op.kt[r][ks] = *reinterpret_cast<const bf8*>(kt + ((4 * i + r) * 2 + ks) * kFrag);
 }
 __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_t hc, int half, int lane, OutOps& op) {
   const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
@@ -715,107 +713,142 @@ __device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
   return r;
 }
 
-// The state wave of (batch b, v-head h, Dv tiles jt .. jt + NT - 1): S[n][a] holds the
-// state's rows dk = 16 a + 4 lg + e (lg = lane / 16) of column dv = 16 (jt + n) + lane % 16
-// (S^T as accumulator tiles). Chunk c: V' = U - W S, S = e^G63 S + K^T (e^(G63-G) V');
-// S before the update and V' go to mail[c % 2]. `op` holds chunk c's operands and is
-// reloaded with those of chunk cn (two chunks on) right after their last product.
-template <int NS, int NT>
-__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, f4 (&S)[NS][kD / 16],
-                                            StateOps<NS>& op, size_t gcn, size_t hcn, int jt, int n0, int lane) {
-  bf8 sb[NS][kD / 32];
+// The W and K^T halves the two state waves exchange, per lane, in two slots: slot c % 2
+// holds chunk c's, written during chunk c - 1.
+struct ScanShared {
+  bf8 w[2][2][2][4][64];   // [slot][wave][own pos tile][dk block][lane]
+  bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
+};
+
+// State wave i of (batch b, v-head h, Dv tile jt): S[a] holds the state's rows dk = 16 a +
+// 4 lg + e (lg = lane / 16) of column dv = 16 jt + lane % 16 (S^T as accumulator tiles).
+// Chunk c: V' = U - W S, S = e^G63 S + K^T (e^(G63-G) V'); S before the update and V' go to
+// mail slot i. `op` holds this wave's share of chunk c's operands and is reloaded with
+// chunk cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk
+// ago) is written to the exchange slot of chunk c + 1.
+template <int NT, int i>
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared& sh, f4 (&S)[kD / 16],
+                                            StateOps& op, const StateOps& nx, size_t gcn, size_t hcn, int jt, int slot,
+                                            int lane) {
+  constexpr int o = i ^ 1;
+  // the other wave's halves of this chunk's W and K^T
+  bf8 wo[2][4], kto[4][2];
 #pragma unroll
-  for (int n = 0; n < NS; ++n)
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) {
-      sb[n][ks] = stack_bf8(S[n][2 * ks], S[n][2 * ks + 1]);
-      mb.sb[n0 + n][ks][lane] = sb[n][ks];
-    }
+    for (int ks = 0; ks < 4; ++ks) wo[r][ks] = sh.w[slot][o][r][ks][lane];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
+  bf8 sb[kD / 32];
+#pragma unroll
+  for (int ks = 0; ks < kD / 32; ++ks) {
+    sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
+    mb.sb[i][ks][lane] = sb[ks];
+  }
   f4 egr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) egr[pt] = rows_of(op.g.y, pt, lane);
   const float gam = __shfl(op.g.x, 63, 64);
-  f4 vpr[NS][4];
+  f4 vpr[4];
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt)
+  for (int pt = 0; pt < 4; ++pt) {
+    // position tiles 2i, 2i + 1 are this wave's (registers), the others came through LDS
+    const int r = pt & 1;
+    const bool own = (pt >> 1) == i;  // (compile-time after unrolling)
+    f4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      f4 P = {0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < kD / 32; ++ks) P = mfma(own ? op.w[r][ks] : wo[r][ks], sb[ks], P);
+    vpr[pt] = op.u[pt] - P;
+    mb.vpr[i][pt][lane] = vpr[pt];
+  }
+  bf8 vb[2];
 #pragma unroll
-      for (int ks = 0; ks < kD / 32; ++ks) P = mfma(op.w[pt][ks], sb[n][ks], P);
-      vpr[n][pt] = op.u[n][pt] - P;
-      mb.vpr[n0 + n][pt][lane] = vpr[n][pt];
-    }
-  bf8 vb[NS][2];
-#pragma unroll
-  for (int n = 0; n < NS; ++n)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) vb[n][ks] = stack_bf8(egr[2 * ks] * vpr[n][2 * ks], egr[2 * ks + 1] * vpr[n][2 * ks + 1]);
-  // (the reloads stay where they are written: the scheduler would otherwise sink them
-  // to the end of the chunk)
+  for (int ks = 0; ks < 2; ++ks) vb[ks] = stack_bf8(egr[2 * ks] * vpr[2 * ks], egr[2 * ks + 1] * vpr[2 * ks + 1]);
+  // S = e^G63 S + K^T V'', with the reloads of chunk cn's share spread between its MFMAs
+  // (one load after each): loads issued in a burst queue up in the CU's address unit
+  // behind the other waves' and hold this wave at the issue.
   __builtin_amdgcn_sched_barrier(0);
-  load_wu<NS>(p, hcn, jt, lane, op);
-  __builtin_amdgcn_sched_barrier(0);
+  load_wu(p, hcn, jt, i, lane, op);
 #pragma unroll
-  for (int a = 0; a < kD / 16; ++a)
+  for (int a = 0; a < kD / 16; ++a) {
+    const int r = a & 3;
+    const bool own = (a >> 2) == i;
+    f4 acc = S[a] * gam;
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      f4 acc = S[n][a] * gam;
+    for (int ks = 0; ks < 2; ++ks) acc = mfma(own ? op.kt[r][ks] : kto[r][ks], vb[ks], acc);
+    S[a] = acc;
+  }
+  load_kt(p, gcn, i, lane, op);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) acc = mfma(op.kt[a][ks], vb[n][ks], acc);
-      S[n][a] = acc;
-    }
+  for (int k = 0; k < 16; ++k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+  }
+  __builtin_amdgcn_sched_group_barrier(0x020, 5, 0);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt<NS>(p, gcn, lane, op);
-  __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();  // mail[c % 2] is complete; the output waves have read mail[(c + 1) % 2]
+  // chunk c + 1's share for the other wave (the slot was last read in chunk c - 1)
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sh.w[slot ^ 1][i][r][ks][lane] = nx.w[r][ks];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sh.kt[slot ^ 1][i][r][ks][lane] = nx.kt[r][ks];
+  __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
+                    // have read mail[(c + 1) % 2]
 }
 
 // Operands are loaded two chunks ahead, in two register sets used by alternate chunks (an
 // unrolled pair of chunks per loop trip, so the sets never move between registers), issued
 // in the order the loop reissues them so that the loop is entered with the same loads in
-// flight as at its back edge. One barrier per chunk, and one more at the end, as the
-// output waves.
-template <int NS, int NT>
-__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], int b, int h, int g,
-                                                int jt, int n0, int lane) {
+// flight as at its back edge. Barriers: one after chunk 0's shares are exchanged, one per
+// chunk, one at the end, as the output waves.
+template <int NT, int i>
+__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared& sh,
+                                                int b, int h, int g, int jt, int lane) {
   const int fr = lane & 15, lg = lane >> 4;
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
   const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
   const size_t srow = ((size_t)b * p.Hv + h) * kD * kD + (size_t)(jt * kDt + fr) * kD + 4 * lg;
-  f4 S[NS][kD / 16];
+  f4 S[kD / 16];
 #pragma unroll
-  for (int n = 0; n < NS; ++n)
-#pragma unroll
-    for (int a = 0; a < kD / 16; ++a)
-      S[n][a] = p.state_in ? *reinterpret_cast<const f4*>(p.state_in + srow + (size_t)n * kDt * kD + 16 * a)
-                           : f4{0.f, 0.f, 0.f, 0.f};
+  for (int a = 0; a < kD / 16; ++a)
+    S[a] = p.state_in ? *reinterpret_cast<const f4*>(p.state_in + srow + 16 * a) : f4{0.f, 0.f, 0.f, 0.f};
 
   const int last = p.nC - 1;
-  StateOps<NS> A, B;
+  StateOps A, B;
   __builtin_amdgcn_sched_barrier(0);
-  load_wu<NS>(p, hc0, jt, lane, A);
+  load_wu(p, hc0, jt, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt<NS>(p, gc0, lane, A);
+  load_kt(p, gc0, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_wu<NS>(p, hc0 + min(1, last), jt, lane, B);
+  load_wu(p, hc0 + min(1, last), jt, i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt<NS>(p, gc0 + min(1, last), lane, B);
+  load_kt(p, gc0 + min(1, last), i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sh.w[0][i][r][ks][lane] = A.w[r][ks];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sh.kt[0][i][r][ks][lane] = A.kt[r][ks];
+  __syncthreads();
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
-    state_chunk<NS, NT>(p, mail[0], S, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, n0, lane);
-    state_chunk<NS, NT>(p, mail[1], S, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, n0, lane);
+    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
+    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
   }
-  if (c < p.nC) state_chunk<NS, NT>(p, mail[0], S, A, gc0 + last, hc0 + last, jt, n0, lane);
+  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
   __syncthreads();
 
   if (p.state_out) {
 #pragma unroll
-    for (int n = 0; n < NS; ++n)
-#pragma unroll
-      for (int a = 0; a < kD / 16; ++a)
-        *reinterpret_cast<f4*>(p.state_out + srow + (size_t)n * kDt * kD + 16 * a) = S[n][a];
+    for (int a = 0; a < kD / 16; ++a) *reinterpret_cast<f4*>(p.state_out + srow + 16 * a) = S[a];
   }
 }
 
@@ -826,11 +859,32 @@ struct OutTile {
   OT y[32][NT * kDt + 16 / sizeof(OT)];
 };
 
+// The outputs of chunk c staged in an output wave's tile to o: lane l stores position
+// 64 c + 32 half + l / 2, columns 16 (jt + (l % 2) * NT / 2) ..: NT * 8 consecutive columns,
+// 16 bytes at a time (the tile rows were written by this wave).
+template <int NT, typename OT>
+__device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile<NT, OT>& tile, int b, int h, int jt,
+                                           int half, int c, int lane) {
+  constexpr int kPer = NT * kDt / 2;  // columns per lane
+  constexpr int kVec = 16 / sizeof(OT);
+  const int row = lane >> 1, col = (lane & 1) * kPer;
+  const int t = c * kC + 32 * half + row;
+  if (t < p.T) {
+    OT* o = static_cast<OT*>(p.o) + ((size_t)b * p.T + t) * p.Hv * kD + (size_t)h * kD + jt * kDt + col;
+#pragma unroll
+    for (int v = 0; v < kPer / kVec; ++v)
+      *reinterpret_cast<f4*>(o + v * kVec) = *reinterpret_cast<const f4*>(&tile.y[row][col + v * kVec]);
+  }
+}
+
 // Output wave `half` (positions 32 half .. 32 half + 31 of each chunk), one chunk behind
 // the state wave (chunk c after its barrier c): y = e^G . (Q S) + M V' (V' split into bf16
-// hi + lo) from mail[c % 2]; `op` is reloaded with chunk cn's operands and touches the
-// lines of chunk c + 4 (gc4, hc4). The touches issued with this set two chunks ago have
-// long arrived: they are folded into `tacc` only so that they stay live.
+// hi + lo) from mail[c % 2] into the tile, after the previous chunk's outputs have been
+// stored from it (the stores are issued before the reloads, so a wait for a reloaded
+// operand never has to count stores that may not have been issued). `op` is reloaded with
+// chunk cn's operands and touches the lines of chunk c + 4 (gc4, hc4). The touches issued
+// with this set two chunks ago have long arrived: they are folded into `tacc` only so that
+// they stay live.
 template <int NT, bool OBF16>
 __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
                                              OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
@@ -838,6 +892,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
                                              int jt, int half, int c, int lane, unsigned& tacc) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const int fr = lane & 15, lg = lane >> 4;
+  if (c > 0) store_tile<NT, OT>(p, tile, b, h, jt, half, c - 1, lane);
   tacc ^= op.touch[0] ^ op.touch[1];
   f4 eg[2];
 #pragma unroll
@@ -874,19 +929,6 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
       for (int e = 0; e < 4; ++e) tile.y[16 * i + 4 * lg + e][16 * n + fr] = (OT)y[e];
     }
   }
-
-  // lane l stores position 32 half + l / 2, columns 16 (jt + (l % 2) * NT / 2) ..: NT * 8
-  // consecutive columns, 16 bytes at a time (the tile rows were written by this wave)
-  constexpr int kPer = NT * kDt / 2;  // columns per lane
-  constexpr int kVec = 16 / sizeof(OT);
-  const int row = lane >> 1, col = (lane & 1) * kPer;
-  const int t = c * kC + 32 * half + row;
-  if (t < p.T) {
-    OT* o = static_cast<OT*>(p.o) + ((size_t)b * p.T + t) * p.Hv * kD + (size_t)h * kD + jt * kDt + col;
-#pragma unroll
-    for (int v = 0; v < kPer / kVec; ++v)
-      *reinterpret_cast<f4*>(o + v * kVec) = *reinterpret_cast<const f4*>(&tile.y[row][col + v * kVec]);
-  }
   __builtin_amdgcn_sched_barrier(0);
   load_qm(p, gcn, hcn, half, lane, op);
   touch_lines(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
@@ -898,6 +940,7 @@ template <int NT, bool OBF16>
 __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                                  int b, int h, int g, int jt, int half, int lane) {
+  typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
   const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
   const int last = p.nC - 1;
@@ -911,7 +954,8 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
   load_qm(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
   touch_lines(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
   __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();
+  __syncthreads();  // the state waves' exchange of chunk 0's shares
+  __syncthreads();  // chunk 0's mail
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
     output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
@@ -922,18 +966,21 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
   if (c < p.nC)
     output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half, c,
                             lane, tacc);
+  store_tile<NT, OT>(p, tile, b, h, jt, half, p.nC - 1, lane);
   // (never true: T >= 1; it keeps the touches from being dropped as unused)
   if (tacc == 0x9e3779b9u && p.T < 0) static_cast<float*>(p.o)[lane] = 0.0f;
 }
 
 // Workgroup = (batch, v-head, NT 16-column Dv tiles): waves 0 .. NT-1 carry the state of
 // one tile each, waves NT and NT + 1 make the outputs of positions 0..31 and 32..63 of
-// each chunk for all NT tiles. All waves pass nC + 1 barriers.
+// each chunk for all NT tiles. All waves pass nC + 2 barriers.
 template <int NT, bool OBF16>
 __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
+  static_assert(NT == 2, "two state waves exchange halves of W and K^T");
   __shared__ __attribute__((aligned(16))) ScanMail<NT> mail[2];
   __shared__ __attribute__((aligned(16))) OutTile<NT, OT> tiles[2];
+  __shared__ __attribute__((aligned(16))) ScanShared shared_ops;
   // Workgroups are dispatched to the 8 XCDs round robin (bid % 8); renumber them so that
   // each XCD gets a contiguous range of (batch, v-head, tiles) -- whole v-heads, and whole
   // k-head groups when the count divides -- and the chunk operands those waves share are
@@ -948,8 +995,10 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
   const int g = h / p.rep;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (wave < NT) {
-    scan_state_wave<1, NT>(p, mail, b, h, g, jt + wave, wave, lane);
+  if (wave == 0) {
+    scan_state_wave<NT, 0>(p, mail, shared_ops, b, h, g, jt, lane);
+  } else if (wave == 1) {
+    scan_state_wave<NT, 1>(p, mail, shared_ops, b, h, g, jt + 1, lane);
   } else {
     scan_output_wave<NT, OBF16>(p, mail, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
   }
