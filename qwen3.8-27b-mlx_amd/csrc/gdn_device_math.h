@@ -119,28 +119,24 @@ __device__ __forceinline__ float silu_bf(float y) {
 // hardware 2^x and reciprocal give sigmoid(y) within 0.83 (5 + |y|) ulp of d_sigmoidf(y)
 // on every bf16 y >= -60 (all 65536 inputs checked on the device); when that fast value
 // lies more than 16 + 2|y| ulp from a bf16 rounding midpoint (bits 0x8000 of its low
-// half), both round to the same bf16. Other values -- near a midpoint, y < -60, NaN,
-// about 0.1% of inputs with |y| < 10 -- take the exact path, in one branch per batch
-// so that the fast paths of the batch interleave.
+// half), both round to the same bf16. The check used here is stricter and cheap: |y| < 8
+// and more than 32 ulp from the midpoint (one v_sad_u16 on the low half), folded into one
+// lane mask for the batch. A lane whose batch fails anywhere -- near a midpoint, |y| >= 8,
+// NaN -- recomputes the whole batch on the exact path.
 template <int N>
 __device__ __forceinline__ void silu_bf_batch(float (&y)[N]) {
   float sg[N];
-  uint32_t ok_mask = 0;  // bitwise, not short-circuit: the checks stay straight-line code
+  bool ok = true;
 #pragma unroll
   for (int e = 0; e < N; ++e) {
     const float ex = __builtin_amdgcn_exp2f(-y[e] * 1.44269504088896341f);
     const float s = __builtin_amdgcn_rcpf(1.0f + ex);
-    const int lo = (int)(f_bits(s) & 0xffffu) - 0x8000;
-    const float dist = (float)(lo < 0 ? -lo : lo);
-    const uint32_t ok = (uint32_t)(y[e] >= -60.0f) & (uint32_t)(dist > 16.0f + 2.0f * __builtin_fabsf(y[e]));
+    ok = ok & (__builtin_fabsf(y[e]) < 8.0f) & (__builtin_amdgcn_sad_u16(f_bits(s), 0x8000u, 0u) > 32u);
     sg[e] = rbf(s);
-    ok_mask |= ok << e;
   }
-  if (__builtin_expect(ok_mask != (1u << N) - 1u, 0)) {
+  if (__builtin_expect(!ok, 0)) {
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-      if (!((ok_mask >> e) & 1u)) sg[e] = rbf(d_sigmoidf(y[e]));
-    }
+    for (int e = 0; e < N; ++e) sg[e] = rbf(d_sigmoidf(y[e]));
   }
 #pragma unroll
   for (int e = 0; e < N; ++e) y[e] = rbf(y[e] * sg[e]);

@@ -165,3 +165,47 @@ def test_prefill_frontend_is_bit_exact(O, gdn, dev):
     print(f"  q mismatches {(q_got != qr).sum()}, k mismatches {(k_got != kr).sum()}", flush=True)
     assert np.array_equal(q_got, qr)
     assert np.array_equal(k_got, kr)
+
+
+def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
+    """The front end's SiLU (hardware 2^x and reciprocal with an exact fallback) on every
+    finite bf16 value, bit for bit against the oracle: conv weights (0, 0, 0, 1) make the
+    conv output equal to x, the v channels of T = 16 positions hold all 65,280 finite bf16
+    patterns, and v is read back from the workspace (its fragment order: block
+    2 (dv / 16) + position / 32, lane 16 ((position % 32) / 8) + dv % 16, element
+    position % 8)."""
+    import torch
+    log_case("prefill front end silu on every finite bf16, B=1 T=16")
+    B, T, Hk, Hv = 1, 16, 16, 48
+    C = 2 * Hk * D + Hv * D
+    pats = np.arange(1 << 16, dtype=np.uint32)
+    finite = pats[((pats >> 7) & 0xFF) != 0xFF].astype(np.uint16)
+    rng = np.random.default_rng(11)
+    x = O.to_bf16(rng.standard_normal((B, T, C)).astype(np.float32))
+    nv = T * Hv * D
+    x[:, :, 2 * Hk * D:] = np.resize(finite, nv).reshape(1, T, Hv * D).view(x.dtype)
+    w = np.zeros((4, C), np.float32)
+    w[3] = 1.0
+    w = O.to_bf16(w)
+    _, _, v_ref, _ = O.conv_frontend(x, None, w, Hk, Hv)
+    a = O.to_bf16(rng.standard_normal((B, T, Hv)).astype(np.float32))
+    ws = torch.empty(gdn.prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device=dev)
+    gdn.prefill_chunked(x=to_dev(x, dev), conv_weight=to_dev(w, dev), a=to_dev(a, dev), b=to_dev(a, dev),
+                        A_log=torch.zeros(Hv, device=dev), dt_bias=torch.zeros(Hv, device=dev),
+                        Hk=Hk, Hv=Hv, workspace=ws)
+    torch.cuda.synchronize()
+    raw = to_np(ws).view(np.uint16)
+    al = lambda n: -(-n // 256) * 256  # noqa: E731  (byte sizes of the workspace pieces)
+    nC = 1
+    qk, wm = B * Hk * nC * 8192 * 2, B * Hv * nC * 8192 * 2
+    uu, gg = B * Hv * nC * 8192 * 4, B * Hv * nC * 128 * 4
+    vf_off = (2 * al(qk) + 2 * al(wm) + al(uu) + al(gg)) // 2
+    vf = raw[vf_off:vf_off + Hv * 8192].reshape(Hv, 8192)
+    pos = np.arange(T)[:, None]
+    dv = np.arange(D)[None, :]
+    idx = (2 * (dv >> 4) + (pos >> 5)) * 512 + (16 * ((pos & 31) >> 3) + (dv & 15)) * 8 + (pos & 7)
+    v_got = vf[:, idx].transpose(1, 0, 2)                      # (T, Hv, D)
+    v_want = v_ref.view(np.uint16)[0]
+    bad = int((v_got != v_want).sum())
+    print(f"  {finite.size} finite inputs, mismatches {bad}", flush=True)
+    assert bad == 0
