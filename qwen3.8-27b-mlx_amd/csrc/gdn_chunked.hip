@@ -321,22 +321,88 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   }
 }
 
-// Column j (this lane) of T = (I + A)^-1 by forward substitution, right-looking: once x_m
-// is final, x_i += (-A_im) x_m for every later row i. All lanes read the same LDS words.
-__device__ __forceinline__ void invert_column(const float (*nat)[kC + 4], int j, float (&x)[kC]) {
+// T = (I + A)^-1 of one v-head's strictly lower A (64 x 64), by 16 x 16 blocks, in one
+// wave. The buffer holds -A transposed in its upper triangle (nat[j][i] = -A_ij, j < i) and
+// receives T in its lower triangle (nat[i][j] = T_ij, i >= j): the two never overlap, so
+// -A stays readable while T is written. (1) The four diagonal blocks together, lane = (block
+// kb, column c), forward substitution in fp32 (x_r += (-A_rm) x_m for r > m, 120 FMAs a
+// lane); their rows are then written whole, zeros above the diagonal. (2) The blocks below,
+// a diagonal at a time: T_ij = -T_ii S_ij with S_ij = sum_{k=j}^{i-1} A_ik T_kj, on
+// v_mfma_f32_16x16x32_bf16 with both operands split into bf16 hi + lo (three products:
+// about 2^-16 relative error). K runs in the interleaved order k' = 8 lg + e <-> row/column
+// 4 lg + (e & 3) of the first (e < 4) or second (e >= 4) block of the pair, so the
+// accumulator tile S is the B operand of T_ii S as it stands. The blocks above the diagonal
+// keep -A^T: the readers of T mask them.
+__device__ __forceinline__ void split_bf16(const float (&v)[8], bf8& hi, bf8& lo) {
 #pragma unroll
-  for (int i = 0; i < kC; ++i) x[i] = i == j ? 1.0f : 0.0f;
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)v[e];
+    hi[e] = h;
+    lo[e] = (__bf16)(v[e] - (float)h);
+  }
+}
+
+__device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
+  const int lg = lane >> 4, fr = lane & 15;
+  {
+    float x[16];
 #pragma unroll
-  for (int m = 0; m < kC - 1; ++m) {
+    for (int r = 0; r < 16; ++r) x[r] = r == fr ? 1.0f : 0.0f;
 #pragma unroll
-    for (int i4 = (m + 1) & ~3; i4 < kC; i4 += 4) {
-      const f4 a = *reinterpret_cast<const f4*>(&nat[m][i4]);
+    for (int m = 0; m < 15; ++m) {
+      const float* row = &nat[16 * lg + m][16 * lg];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (i4 + e > m) x[i4 + e] = __builtin_fmaf(a[e], x[m], x[i4 + e]);
+      for (int r4 = (m + 1) & ~3; r4 < 16; r4 += 4) {
+        const f4 a = *reinterpret_cast<const f4*>(row + r4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (r4 + e > m) x[r4 + e] = __builtin_fmaf(a[e], x[m], x[r4 + e]);
+        }
       }
     }
+    // (every lane has read its block's -A before any lane writes: one wave, in order)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) nat[16 * lg + r][16 * lg + fr] = x[r];
   }
+  // S += [A_{i,k1} | A_{i,k2}] [T_{k1,j} ; T_{k2,j}] (k2 < 0: one block)
+  auto prod = [&](int i, int k1, int k2, int j, f4 acc) -> f4 {
+    float av[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kk = e < 4 ? k1 : k2;
+      const int row = 16 * kk + 4 * lg + (e & 3);
+      av[e] = kk < 0 ? 0.0f : -nat[row][16 * i + fr];
+      bv[e] = kk < 0 ? 0.0f : nat[row][16 * j + fr];
+    }
+    bf8 ah, al, bh, bl;
+    split_bf16(av, ah, al);
+    split_bf16(bv, bh, bl);
+    acc = mfma(ah, bh, acc);
+    acc = mfma(al, bh, acc);
+    acc = mfma(ah, bl, acc);
+    return acc;
+  };
+  // T_ij = -T_ii S, written to the lower triangle
+  auto finish = [&](int i, int j, f4 S) {
+    const f4 d = *reinterpret_cast<const f4*>(&nat[16 * i + fr][16 * i + 4 * lg]);
+    const float av[8] = {d[0], d[1], d[2], d[3], 0.0f, 0.0f, 0.0f, 0.0f};
+    const float bv[8] = {S[0], S[1], S[2], S[3], 0.0f, 0.0f, 0.0f, 0.0f};
+    bf8 ah, al, bh, bl;
+    split_bf16(av, ah, al);
+    split_bf16(bv, bh, bl);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc = mfma(ah, bh, acc);
+    acc = mfma(al, bh, acc);
+    acc = mfma(ah, bl, acc);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) nat[16 * i + 4 * lg + t][16 * j + fr] = -acc[t];
+  };
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 3; ++j) finish(j + 1, j, prod(j + 1, j, -1, j, zero));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) finish(j + 2, j, prod(j + 2, j, j + 1, j, zero));
+  finish(3, 0, prod(3, 2, -1, 0, prod(3, 0, 1, 0, zero)));
 }
 
 // q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output.
@@ -481,14 +547,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
     __syncthreads();
 
-    // T = (I + A)^-1: wave r inverts v-head r0 + r, lane j = column j, and writes T over
-    // its own -A^T as [i][j] (only this wave has read that slot)
-    if (wave < gs) {
-      float x[kC];
-      invert_column(s.u.nat[wave], lane, x);
-#pragma unroll
-      for (int i = 0; i < kC; ++i) s.u.nat[wave][i][lane] = x[i];
-    }
+    // T = (I + A)^-1: wave r inverts v-head r0 + r in its own slot (T below the diagonal,
+    // -A^T left above it)
+    if (wave < gs) invert_blocked(s.u.nat[wave], lane);
     __syncthreads();
 
     for (int r = 0; r < gs; ++r) {
@@ -520,8 +581,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         bf8 ah[2], al[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
+          // (column blocks above row block `wave` still hold -A^T: T is zero there)
+          const bool above = 2 * kh + (lane >> 5) > wave;
           const float* xr = &s.u.nat[r][16 * wave + fr][32 * kh + fk];
-          const f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
+          f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
+          if (above) x0 = x1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
@@ -549,8 +613,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         for (int bt = 0; bt < 4; ++bt)
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh) {
+            const bool above = 2 * kh + (lane >> 5) > bt;
             const float* xr = &s.u.nat[r][16 * bt + fr][32 * kh + fk];
-            const f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
+            f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
+            if (above) x0 = x1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
