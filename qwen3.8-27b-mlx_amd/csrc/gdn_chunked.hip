@@ -576,9 +576,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           bj[kh][e] = s.beta[r][32 * kh + fk + e];
           ej[kh][e] = s.eG[r][32 * kh + fk + e];
         }
-      // U = T' V: wave w takes position tile w, all eight dv tiles; T' split into hi + lo
+      // U = T' V and W^T = K^T (T' e^G)^T: wave w takes position tile w (rows i = 16 w + fr
+      // of T'), all eight dv tiles of U and all eight dk tiles of W; T' split into hi + lo for U
       {
-        bf8 ah[2], al[2];
+        bf8 ah[2], al[2], te[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           // (column blocks above row block `wave` still hold -A^T: T is zero there)
@@ -592,6 +593,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
             const __bf16 hi = (__bf16)tv;
             ah[kh][e] = hi;
             al[kh][e] = (__bf16)(tv - (float)hi);
+            te[kh][e] = (__bf16)(tv * ej[kh][e]);
           }
         }
         float* wu = p.ws_u + hc * kChunkElems + lane * 4;
@@ -604,37 +606,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           acc = mfma(al[1], vb[d][1], acc);
           *reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256) = acc;
         }
-      }
-      // W^T = K^T (T' e^G)^T: wave w takes dk tiles 2w, 2w+1, all position tiles; lane
-      // gets W[i = 16 bt + fr][dk = 16 a + 4 lg .. +3]
-      {
-        bf8 te[4][2];
-#pragma unroll
-        for (int bt = 0; bt < 4; ++bt)
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh) {
-            const bool above = 2 * kh + (lane >> 5) > bt;
-            const float* xr = &s.u.nat[r][16 * bt + fr][32 * kh + fk];
-            f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
-            if (above) x0 = x1 = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
-              te[bt][kh][e] = (__bf16)(tv * ej[kh][e]);
-            }
-          }
+        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]
         __bf16* ww = p.ws_w + hc * kChunkElems;
 #pragma unroll
-        for (int a2 = 0; a2 < 2; ++a2) {
-          const int a = 2 * wave + a2;
+        for (int a = 0; a < kD / 16; ++a) {
           const bf8 k0 = frag(s.kt, 16 * a + fr, fk), k1 = frag(s.kt, 16 * a + fr, 32 + fk);
-#pragma unroll
-          for (int bt = 0; bt < 4; ++bt) {
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = mfma(k0, te[bt][0], acc);
-            acc = mfma(k1, te[bt][1], acc);
-            *reinterpret_cast<bf4*>(ww + ilv_off(16 * bt + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
-          }
+          f4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma(k0, te[0], acc);
+          acc = mfma(k1, te[1], acc);
+          *reinterpret_cast<bf4*>(ww + ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
         }
       }
     }
