@@ -202,11 +202,12 @@ static_assert(kC == 2 * kFePos, "a chunk is two front-end position blocks");
 // four pairs as ((p0 + p1) + (p2 + p3)) (the first two butterfly steps), then the DPP
 // row sum does the remaining four. The workgroup holding position T-1 also writes the
 // conv state hand-off (rows T-3..T-1 of [conv_in ; x]) for its heads.
-// A v head's lane holds eight positions of each of its eight channels, so it writes each
-// channel's positions as one 16-byte piece of the fragment order straight from registers
-// (the q/k and v paths share the conv and SiLU code and their registers). At most 128
+// A v head's outputs go through the wave's LDS tile ([channel][position]), so that each
+// lane then writes eight positions of one channel as one 16-byte piece of the fragment
+// order (the q/k and v paths share the conv and SiLU code and their registers). At most 128
 // VGPRs: four waves per SIMD for this VALU-bound kernel.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void prefill_frontend_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_frontend_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) __bf16 vtile[kFeHeads][kD][kFePos + 8];
   const int nheads = 2 * p.Hk + p.Hv;
   const int hgroups = (nheads + kFeHeads - 1) / kFeHeads;
   const int pblocks = (p.T + kFePos - 1) / kFePos;
@@ -248,14 +249,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const size_t pstride = (size_t)p.Hk * kD;
   const float scale_b = rbf(1.0f / sqrtf((float)kD));
   const float eps_b = rbf(1e-6f);
-  // v: channel e's eight positions as four bf16 pairs (the values are bf16 already, so the
-  // pair conversion is exact); positions at or past T are zeros
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-  const bool vfull = (pb + 1) * kFePos <= p.T;
-  u4v vpiece[8];
-  float vprev[8];
+  auto& vt = vtile[wave];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     float u[8];  // channels 4m + e (e < 4) and 64 + 4m + (e - 4)
@@ -289,28 +283,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
         *reinterpret_cast<bf4*>(o + 64 + 4 * m) = to_bf4(y1);
       }
     } else {
+      const int tp = 8 * (lane >> 4) + t;  // position within the block
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float val = (vfull || pos < p.T) ? u[e] : 0.0f;
-        if (t & 1) {
-          vpiece[e][t >> 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){vprev[e], val}, bf2));
-        } else {
-          vprev[e] = val;
-        }
+      for (int e = 0; e < 4; ++e) {
+        vt[4 * m + e][tp] = pos < p.T ? (__bf16)u[e] : (__bf16)0.0f;
+        vt[64 + 4 * m + e][tp] = pos < p.T ? (__bf16)u[4 + e] : (__bf16)0.0f;
       }
     }
   }
   if (!norm) {
     // v: the B operand of U = T' V in fragment order (block 2 (dv / 16) + half chunk, lane
-    // 16 (position / 8) + dv % 16, element position % 8)
+    // 16 (position / 8) + dv % 16); this wave's LDS tile, written above by this wave only
     const int hv = hh - 2 * p.Hk;
     const int kh = pb & 1;  // which half of the 64-position chunk (kFePos = kC / 2)
-    const int pg = lane >> 4;
     __bf16* vf = p.ws_vf + (((size_t)b * p.Hv + hv) * p.nC + pb / 2) * kChunkElems;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int dv = e < 4 ? 4 * m + e : 64 + 4 * m + (e - 4);
-      *reinterpret_cast<u4v*>(vf + (2 * (dv >> 4) + kh) * kFrag + (16 * pg + (dv & 15)) * 8) = vpiece[e];
+    for (int i = 0; i < 8; ++i) {
+      const int piece = 64 * i + lane;          // (dv tile, lane of the fragment)
+      const int dv = 16 * (piece >> 6) + (lane & 15), pg = lane >> 4;
+      *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + kh) * kFrag + lane * 8) =
+          *reinterpret_cast<const bf8*>(&vt[dv][8 * pg]);
     }
   }
   if (p.conv_out && pb == pblocks - 1) {
