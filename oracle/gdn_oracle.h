@@ -2,7 +2,7 @@
  * CPU oracle for the gated-delta recurrence -- TEST INFRASTRUCTURE ONLY.
  *
  * This library restates, op for op, the reference's unfused MLX sequence for the
- * Gated-DeltaNet path. It is the checker that the HIP kernels are compared with,
+ * Gated-DeltaNet path. It is what the HIP kernels are compared with in the tests,
  * and the CPU baseline that bench.py times next to them. Nothing in the product
  * (the HIP library and its host code) may link, load or call it.
  *

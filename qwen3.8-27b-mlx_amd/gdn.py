@@ -270,7 +270,8 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
 def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
           conv_weight=None, conv_state=None, collect: bool = False, in_place: bool = True,
           o_dtype=None, Hk: int = 16, stream=None):
-    """The north-star per-layer call: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
+    """The per-layer call of GatedDeltaNet::operator() (cpp/src/model.cpp:585-641) at the
+    recurrence: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
     (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
     v (B,T,Hv,128). Returns dict(o, state, states, conv_state)."""
     import torch

@@ -1,4 +1,4 @@
-"""Shared test setup: the `gpu` marker, the package loader and the oracle (the checker)."""
+"""Shared test setup: the `gpu` marker, the package loader and the oracle."""
 from __future__ import annotations
 
 import os

@@ -2,7 +2,7 @@
 // reference's self-test (cpp/src/tests.cpp:36-56 rel_err/check, 196-243 test_delta):
 // gdn::run vs the oracle's run_reference restatement on the reference's shapes and input
 // distributions, with and without collect, bound 2e-5; then DeltaCache record/commit
-// against plain decoding; then the quantized projections (gdn::linears, norm_out_proj). The oracle (oracle/gdn_oracle.h) is the checker only.
+// against plain decoding; then the quantized projections (gdn::linears, norm_out_proj). The oracle (oracle/gdn_oracle.h) is used for comparison only.
 #include <hip/hip_runtime.h>
 
 #include <cmath>

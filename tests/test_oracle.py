@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (the checker) without trusting it: known-answer vectors for the
+"""Pins the CPU oracle without trusting it: known-answer vectors for the
 generator, independent implementations (torch's bf16 cast, fp64 libm, numpy fp64 matrix
 algebra), closed forms and invariants of the recurrence, and the reference's own
 criterion for the chunked form (equality with the per-token recurrence)."""
