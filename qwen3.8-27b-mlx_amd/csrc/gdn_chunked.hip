@@ -127,7 +127,8 @@ struct PrefillParams {
   __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128)
   __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64)
   __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
-  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating
+  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
+                  // blocks above the diagonal are left unwritten)
   float* ws_u;    // (B, Hv, nC): U   (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]
   float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
   __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
@@ -530,11 +531,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         }
         const bf4 hi = to_bf4(mv);
         const bf4 lo = to_bf4(mv - from_bf4(hi));
-        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating
+        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating.
+        // Blocks (0, 1) and (1, 1) lie above the diagonal: zero, neither stored nor read.
         const int off = ilv_off(i, j0, 2);
         const int blk = off / kFrag, within = off % kFrag;
-        *reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within) = hi;
-        *reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within) = lo;
+        if (ct >= 2 || wave < 2) {
+          *reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within) = hi;
+          *reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within) = lo;
+        }
       }
     }
     __syncthreads();
@@ -674,10 +678,15 @@ struct StateOps {
   float2 g;      // (e^G, e^(G63-G)) at position `lane`
 };
 
-// An output wave's operands of one chunk: its two position tiles 2 half, 2 half + 1.
+// Output wave `half` makes position tiles half and 3 - half of each chunk: M is lower
+// triangular, so the first tile (rows < 32) has one nonzero 32-column block and the second
+// two, and both waves get three of the six.
+__device__ __forceinline__ int out_tile(int half, int i) { return i == 0 ? half : 3 - half; }
+
+// An output wave's operands of one chunk: its two position tiles out_tile(half, 0 / 1).
 struct OutOps {
   bf8 q[2][4];     // Q [pos tile][dk block]          (A of Q S)
-  bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V')
+  bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V'); [0][1] is zero, never loaded
   float eg;        // e^G at position `lane`
   unsigned touch[2];  // the cache-line touches issued with this set (see touch_lines)
 };
@@ -733,11 +742,11 @@ __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_
   const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int pt = 2 * half + i;
+    const int pt = out_tile(half, i);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.q[i][ks] = *reinterpret_cast<const bf8*>(q + (pt * 4 + ks) * kFrag);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks <= i; ++ks)
 #pragma unroll
       for (int hl = 0; hl < 2; ++hl) op.m[i][ks][hl] = *reinterpret_cast<const bf8*>(m + ((pt * 2 + ks) * 2 + hl) * kFrag);
   }
@@ -905,16 +914,17 @@ struct OutTile {
   OT y[32][NT * kDt + 16 / sizeof(OT)];
 };
 
-// The outputs of chunk c staged in an output wave's tile to o: lane l stores position
-// 64 c + 32 half + l / 2, columns 16 (jt + (l % 2) * NT / 2) ..: NT * 8 consecutive columns,
-// 16 bytes at a time (the tile rows were written by this wave).
+// The outputs of chunk c staged in an output wave's tile to o: lane l stores tile row
+// r = l / 2 (position 64 c + 16 out_tile(half, r / 16) + r % 16), columns
+// 16 (jt + (l % 2) * NT / 2) ..: NT * 8 consecutive columns, 16 bytes at a time (the tile
+// rows were written by this wave).
 template <int NT, typename OT>
 __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile<NT, OT>& tile, int b, int h, int jt,
                                            int half, int c, int lane) {
   constexpr int kPer = NT * kDt / 2;  // columns per lane
   constexpr int kVec = 16 / sizeof(OT);
   const int row = lane >> 1, col = (lane & 1) * kPer;
-  const int t = c * kC + 32 * half + row;
+  const int t = c * kC + 16 * out_tile(half, row >> 4) + (row & 15);
   if (t < p.T) {
     OT* o = static_cast<OT*>(p.o) + ((size_t)b * p.T + t) * p.Hv * kD + (size_t)h * kD + jt * kDt + col;
 #pragma unroll
@@ -923,7 +933,7 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile
   }
 }
 
-// Output wave `half` (positions 32 half .. 32 half + 31 of each chunk), one chunk behind
+// Output wave `half` (position tiles out_tile(half, 0 / 1) of each chunk), one chunk behind
 // the state wave (chunk c after its barrier c): y = e^G . (Q S) + M V' (V' split into bf16
 // hi + lo) from mail[c % 2] into the tile, after the previous chunk's outputs have been
 // stored from it (the stores are issued before the reloads, so a wait for a reloaded
@@ -942,7 +952,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   tacc ^= op.touch[0] ^ op.touch[1];
   f4 eg[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) eg[i] = rows_of(op.eg, 2 * half + i, lane);
+  for (int i = 0; i < 2; ++i) eg[i] = rows_of(op.eg, out_tile(half, i), lane);
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     bf8 sb[kD / 32];
@@ -965,7 +975,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
       for (int ks = 0; ks < kD / 32; ++ks) qs = mfma(op.q[i][ks], sb[ks], qs);
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks <= i; ++ks) {  // (M's block (tile 0 or 1, columns 32..63) is zero)
         acc = mfma(op.m[i][ks][0], vh[ks], acc);
         acc = mfma(op.m[i][ks][1], vh[ks], acc);
         acc = mfma(op.m[i][ks][0], vl[ks], acc);
