@@ -26,7 +26,7 @@
 //                  over the chunks. Each of two state waves keeps its tile's fp32 state
 //                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain V' = U - W S,
 //                  S = e^G63 S + K^T V'' with every operand in registers; two output waves
-//                  (positions 0..31 and 32..63 of a chunk) run one chunk behind on the S and
+//                  (position tiles {0, 3} and {1, 2} of a chunk) run one chunk behind on the S and
 //                  V' that the state waves leave in a double-buffered LDS mailbox: one
 //                  barrier per chunk. Operands go from the workspace straight into
 //                  registers two chunks ahead of their use, and the output waves touch the
@@ -1028,8 +1028,8 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
 }
 
 // Workgroup = (batch, v-head, NT 16-column Dv tiles): waves 0 .. NT-1 carry the state of
-// one tile each, waves NT and NT + 1 make the outputs of positions 0..31 and 32..63 of
-// each chunk for all NT tiles. All waves pass nC + 2 barriers.
+// one tile each, waves NT and NT + 1 make the outputs of position tiles {0, 3} and {1, 2}
+// of each chunk for all NT tiles. All waves pass nC + 2 barriers.
 template <int NT, bool OBF16>
 __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
