@@ -85,6 +85,21 @@ def test_prefill_qkv_precomputed_gates_equal_heads(O, gdn, dev):
     check(O, S, rS, "state")
 
 
+@pytest.mark.parametrize("Hk,Hv", [(8, 16), (4, 16), (2, 12), (4, 20)])
+def test_prefill_other_head_ratios(O, gdn, dev, Hk, Hv):
+    """Other sizes of the family: two v-heads per k-head (one group of two), four (groups of
+    three and one: the intra kernel's general form), six (two full groups) and five (three
+    and two); conv front end, carried state and conv state, ragged last chunk."""
+    log_case(f"prefill conv Hk={Hk} Hv={Hv} T=150 B=1 with state")
+    inp = O.make_inputs(config=4, layer=100 * Hk + Hv, B=1, L=150, Hk=Hk, Hv=Hv, conv=True,
+                        state_std=0.05)
+    ref = O.reference_layer(inp)
+    o, S, conv = run_prefill(gdn, dev, inp, Hk=Hk, o_dtype="f32")
+    check(O, o, ref["o"], "o")
+    check(O, S, ref["state"], "state")
+    assert np.array_equal(conv, ref["xp"][:, -3:])
+
+
 def test_prefill_4096_full(O, gdn, dev):
     """The benchmark configuration: B=1, T=4096, conv front end, zero state."""
     log_case("prefill conv T=4096 B=1 (benchmark shape)")

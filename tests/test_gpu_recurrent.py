@@ -303,6 +303,20 @@ def test_ragged_steps_conv_and_zero_inputs(O, gdn, dev, T):
     assert np.array_equal(out2["conv"][0], ref2["xp"][:, -3:])
 
 
+@pytest.mark.parametrize("Hk,Hv,T", [(8, 16, 1), (4, 16, 5), (2, 10, 3)])
+def test_conv_layer_other_head_ratios(O, gdn, dev, Hk, Hv, T):
+    """Other sizes of the family: two, four and five v-heads per k-head (the v-head ->
+    k-head map h / (Hv / Hk), model.cpp:603-605), decode and a verify-length block, with
+    the conv front end and a carried conv state."""
+    log_case(f"conv layer Hk={Hk} Hv={Hv} T={T} B=2")
+    inp = O.make_inputs(config=3, layer=10 * Hk + Hv + T, B=2, L=T, Hk=Hk, Hv=Hv, conv=True)
+    ref = O.reference_layer(inp)
+    out = run_layers(gdn, dev, [inp], o_dtype="f32", Hk=Hk)
+    check_state(O, out["state"][0], ref["state"], "state")
+    check_o(O, out["o"][0], ref["o"], "f32", "o")
+    assert np.array_equal(out["conv"][0], ref["xp"][:, -3:])
+
+
 def test_empty_block_copies_state_and_conv(O, gdn, dev):
     import torch
     log_case("T=0 block")
