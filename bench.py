@@ -217,11 +217,13 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
     r = timer.time_calls(lambda it: gdn.call_prefill(args), steps, warmup, host_us_per_call=80.0)
     intra, inter = prefill_flops(T)
     sec = r["ms_per_step"] * 1e-3
+    traffic = load_traffic("prefill_t4096_b1_conv") if T == 4096 else None
     return dict(tokens_per_s=T / sec, us_per_call=r["ms_per_step"] * 1e3,
                 intra_TFLOPs=intra / sec / 1e12,
                 intra_frac_mfma=intra / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 all_products_frac_mfma=(intra + inter) / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
-                intra_flop=intra, inter_flop=inter)
+                intra_flop=intra, inter_flop=inter,
+                hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9)
 
 
 def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str, M: int = 1):
@@ -380,8 +382,9 @@ def main() -> int:
     if want("prefill"):
         r = bench_prefill(torch, gdn, dev, timer, steps=max(5, args.steps // 10), warmup=3)
         sec["prefill_t4096"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        hbm = "" if r["hbm_GBps"] is None else f", HBM {r['hbm_GBps']:.0f} GB/s (counted bytes)"
         print(f"# prefill T=4096: {r['us_per_call']:.1f} us, {r['tokens_per_s'] / 1e6:.2f} M tok/s, "
-              f"intra MFMA frac {r['intra_frac_mfma']:.4f}", flush=True)
+              f"intra MFMA frac {r['intra_frac_mfma']:.4f}{hbm}", flush=True)
     for which in ("in_proj", "out_proj"):
         if want(which):
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)
