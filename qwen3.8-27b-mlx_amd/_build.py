@@ -21,7 +21,8 @@ HIPCC_FLAGS = [
 # Per-source additions. The chunked prefill's scan keeps its state and every MFMA result in
 # VGPRs (the default heuristic puts them in AGPRs, and each elementwise step on them then
 # costs a copy out and back).
-SOURCE_FLAGS = {"gdn_chunked.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"gdn_chunked.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "gdn_qlinear.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:

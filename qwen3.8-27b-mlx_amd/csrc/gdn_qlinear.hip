@@ -39,6 +39,10 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// global-memory pointers: a plain pointer that passed through a struct can lose its
+// address space and compile to flat loads, which also count against the LDS wait counter
+typedef const u32x2 __attribute__((address_space(1))) g_u32x2;
+typedef const uint16_t __attribute__((address_space(1))) g_u16;
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = 16;  // 4 waves x 4 DPP rows
@@ -264,31 +268,100 @@ __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Two nibble words (values k .. k + 7 each) as B fragments: bf16 128 + v, pairs (i, i + 4).
-__device__ __forceinline__ bf8 nibbles_bf16(uint32_t wd) {
+// (a & m) | c in one instruction. VOP3 takes no literal constant on this target and at
+// most one SGPR, so m and c come in VGPRs (set once per kernel by nibble_consts); written
+// out, the compiler emits a separate AND and OR with literals instead.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+struct NibbleConsts {
+  uint32_t mask, bias;  // 0x000F000F, 0x43004300
+};
+__device__ __forceinline__ NibbleConsts nibble_consts() {
+  NibbleConsts k;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(k.mask));
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.bias));
+  return k;
+}
+
+// A nibble word (values k .. k + 7) as a B fragment: bf16 128 + v, pairs (i, i + 4).
+__device__ __forceinline__ bf8 nibbles_bf16(uint32_t wd, NibbleConsts k) {
   u32x4 r;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) r[q] = ((wd >> (4 * q)) & 0x000F000Fu) | 0x43004300u;
+  for (int q = 0; q < 4; ++q) r[q] = and_or(wd >> (4 * q), k.mask, k.bias);
   return __builtin_bit_cast(bf8, r);
 }
 
+// A weight row's segment (the unrolled compare-and-select keeps the argument arrays out of
+// run-time indexing): its nibble words, scales, biases and output column.
+struct RowPtrs {
+  const uint32_t* w;
+  const uint16_t *s, *b;
+  uint16_t* y;
+  int ystride;
+};
+__device__ __forceinline__ RowPtrs row_ptrs(const QParams& p, int layer, int row) {
+  int sg = 0;
+#pragma unroll
+  for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= p.row0[q]) ? 1 : 0;
+  const uint32_t* wseg = p.w[0];
+  const uint16_t *sseg = p.s[0], *bseg = p.b[0];
+  uint16_t* yseg = p.y[0];
+  int nseg = p.n[0], r0 = p.row0[0];
+#pragma unroll
+  for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) {
+    if (sg == q) {
+      wseg = p.w[q];
+      sseg = p.s[q];
+      bseg = p.b[q];
+      yseg = p.y[q];
+      nseg = p.n[q];
+      r0 = p.row0[q];
+    }
+  }
+  const int G = p.K / 64;
+  const size_t lrow = (size_t)layer * nseg + (row - r0);
+  RowPtrs r;
+  r.w = wseg + lrow * (p.K / 8);
+  r.s = sseg + lrow * G;
+  r.b = bseg + lrow * G;
+  r.y = yseg + (size_t)layer * p.M * nseg + (row - r0);
+  r.ystride = nseg;
+  return r;
+}
+
 // MFMA path, step 2. Workgroup = 16 NT weight rows (the output columns) x 16 MT operand
-// rows; wave w takes the groups [w G / 4, (w + 1) G / 4) of the G = K / 64 groups. Lane
-// (g4, nn) = (l / 16, l % 16) reads the nibble words 8 g + 2 g4 + s of its row 16 nt + nn
-// (one 8-byte load per row and group) and gets C rows m = 4 g4 + i of column nn.
+// rows; wave w takes the groups [w G / 4, (w + 1) G / 4) of the G = K / 64 groups (a
+// multiple of 4 for every supported K). Lane (g4, nn) = (l / 16, l % 16) reads the nibble
+// words 8 g + 2 g4 + s of its row 16 nt + nn (one 8-byte load per row and group) and gets
+// C rows m = 4 g4 + i of column nn.
+// Memory: the weight stream comes from HBM once, so what bounds the kernel is how many of
+// its bytes each wave keeps in flight: every load is issued kRing groups ahead (the ring
+// below), and the workgroup's scale and bias pairs are staged in LDS once at the start
+// (they would otherwise be two more loads per row tile and group at the same depth).
+constexpr int kRing = 2;  // groups in flight per wave (G / 4 is a multiple of it)
 template <int MT, int NT>
 __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
-  __shared__ __attribute__((aligned(16))) f4 red[3][MT * NT][64];  // partial sums of waves 1..3
+  constexpr int kRows = 16 * NT;
+  constexpr int kMaxG = 8192 / 64;
+  // scale | bias << 16 per (row, group), rows kMaxG + 1 words apart at most (a row stride
+  // of G + 1 words puts the 16 rows a wave reads at once on distinct banks); at the end the
+  // partial sums of waves 1..3
+  __shared__ __attribute__((aligned(16))) union {
+    uint32_t sb[kRows * (kMaxG + 1)];
+    f4 red[3][MT * NT][64];
+  } sm;
   const int layer = blockIdx.x / p.tiles, tile = blockIdx.x % p.tiles;
   const int mt0 = blockIdx.y * MT;
   const int lane = threadIdx.x & 63, g4 = lane >> 4, nn = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int K = p.K, G = K / 64, nch = K / 32;
+  const int K = p.K, G = K / 64, nch = K / 32, sbs = G + 1;
   const int g0 = wave * G / 4, g1 = (wave + 1) * G / 4;
 
   // this lane's weight row for each n-tile
-  const u32x2* wr[NT];
-  const uint16_t *sr[NT], *br[NT];
+  g_u32x2* wr[NT];
   uint16_t* yr[NT];
   int ystride[NT];
   bool valid[NT];
@@ -296,34 +369,56 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   for (int nt = 0; nt < NT; ++nt) {
     const int grow = (tile * NT + nt) * 16 + nn;
     valid[nt] = grow < p.R;
-    const int row = valid[nt] ? grow : p.R - 1;
-    int sg = 0;
-#pragma unroll
-    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= p.row0[q]) ? 1 : 0;
-    const uint32_t* wseg = p.w[0];
-    const uint16_t *sseg = p.s[0], *bseg = p.b[0];
-    uint16_t* yseg = p.y[0];
-    int nseg = p.n[0], r0 = p.row0[0];
-#pragma unroll
-    for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) {
-      if (sg == q) {
-        wseg = p.w[q];
-        sseg = p.s[q];
-        bseg = p.b[q];
-        yseg = p.y[q];
-        nseg = p.n[q];
-        r0 = p.row0[q];
-      }
-    }
-    const size_t lrow = (size_t)layer * nseg + (row - r0);
-    wr[nt] = reinterpret_cast<const u32x2*>(wseg + lrow * (K / 8)) + g4;  // + 4 g: words 8 g + 2 g4, +1
-    sr[nt] = sseg + lrow * G;
-    br[nt] = bseg + lrow * G;
-    yr[nt] = yseg + (size_t)layer * p.M * nseg + (row - r0);
-    ystride[nt] = nseg;
+    const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
+    wr[nt] = (g_u32x2*)(rp.w) + g4;  // + 4 g: words 8 g + 2 g4, +1
+    yr[nt] = rp.y;
+    ystride[nt] = rp.ystride;
   }
   const bf8* xa = reinterpret_cast<const bf8*>(p.xfrag + ((size_t)layer * p.mtiles + mt0) * nch * 512) + lane;
   const bf8 ones = __builtin_bit_cast(bf8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const NibbleConsts nk = nibble_consts();
+
+  // A ring of kRing slots, one group each (operand fragments and nibble words): slot j
+  // holds groups j, j + kRing, ... and is reloaded with the group kRing ahead right after
+  // its products, so every load is issued kRing groups before its use. (Loads complete in
+  // issue order: a nearer load issued after a farther one would wait for it.) Loads past
+  // the wave's last group reload that group, unused.
+  struct Slot {
+    bf8 a[MT][2];
+    u32x2 w[NT];
+  };
+  auto load = [&](int g, Slot& sl) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) sl.a[mt][s] = xa[((size_t)mt * nch + 2 * g + s) * 64];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) sl.w[nt] = wr[nt][4 * g];
+  };
+  Slot R[kRing];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) load(g0 + j, R[j]);  // (g1 - g0 >= kRing)
+
+  // the scale and bias pairs of the workgroup's rows, all groups: thread t takes row
+  // t / (256 / kRows), four groups at a time (8-byte loads: G and the block starts are
+  // multiples of 4)
+  {
+    constexpr int tpr = kThreads / kRows;
+    const int r = threadIdx.x / tpr, j = threadIdx.x % tpr;
+    const int grow = tile * kRows + r;
+    const RowPtrs rp = row_ptrs(p, layer, grow < p.R ? grow : p.R - 1);
+    for (int g = 4 * j; g < G; g += 4 * tpr) {
+      const u32x2 sv = *(g_u32x2*)(rp.s + g);
+      const u32x2 bv = *(g_u32x2*)(rp.b + g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t s16 = (sv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        const uint32_t b16 = (bv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        sm.sb[r * sbs + g + e] = s16 | (b16 << 16);
+      }
+    }
+  }
+  __syncthreads();
 
   f4 y[MT][NT];
 #pragma unroll
@@ -331,69 +426,42 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // One group ahead, in two register sets with fixed roles (the loop is unrolled by two,
-  // so no set is copied): the loads of group g + 1 are in flight while group g is
-  // multiplied. Loads are unconditional (past the end they reload the last group, unused):
-  // loads under a condition made the compiler keep old and new sets live together. (Two
-  // groups ahead in three sets needed 285 VGPRs and was slower.)
-  struct Set {
-    bf8 a[MT][2];
-    u32x2 w[NT];
-    uint16_t s[NT], b[NT];
-  };
-  auto load = [&](int g, Set& st) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) st.a[mt][s] = xa[((size_t)mt * nch + 2 * g + s) * 64];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      st.w[nt] = wr[nt][4 * g];  // a plain load: the line serves the next three groups too
-      st.s[nt] = sr[nt][g];
-      st.b[nt] = br[nt][g];
-    }
-  };
-  auto compute = [&](const Set& st) {
+  // group g from slot sl, then sl reloaded with group g + kRing
+  auto step = [&](int g, Slot& sl) {
     f4 xs[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      xs[mt] = mfma(st.a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
-      xs[mt] = mfma(st.a[mt][1], ones, xs[mt]);
+      xs[mt] = mfma(sl.a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
+      xs[mt] = mfma(sl.a[mt][1], ones, xs[mt]);
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const bf8 b0 = nibbles_bf16(st.w[nt][0]), b1 = nibbles_bf16(st.w[nt][1]);
-      const float sc = bf2f(st.s[nt]);
-      const float off = bf2f(st.b[nt]) - 128.0f * sc;
+      const uint32_t sbv = sm.sb[(16 * nt + nn) * sbs + g];
+      const float sc = __builtin_bit_cast(float, sbv << 16);
+      const float off = __builtin_bit_cast(float, sbv & 0xFFFF0000u) - 128.0f * sc;
+      const bf8 b0 = nibbles_bf16(sl.w[nt][0], nk), b1 = nibbles_bf16(sl.w[nt][1], nk);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        f4 acc = mfma(st.a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
-        acc = mfma(st.a[mt][1], b1, acc);
+        f4 acc = mfma(sl.a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
+        acc = mfma(sl.a[mt][1], b1, acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
       }
     }
+    load(min(g + kRing, g1 - 1), sl);
   };
-  if (g0 < g1) {
-    Set A, B;
-    const int gl = g1 - 1;
-    load(g0, A);
-    int g = g0;
-    for (; g + 2 <= g1; g += 2) {
-      load(min(g + 1, gl), B);
-      compute(A);
-      load(min(g + 2, gl), A);
-      compute(B);
-    }
-    if (g < g1) compute(A);  // an odd count: the last group is in A
+  for (int gb = g0; gb < g1; gb += kRing) {
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) step(gb + j, R[j]);
   }
 
   // the four waves' partial sums (fixed order: wave 0 + 1 + 2 + 3), rounded to bf16 once
+  __syncthreads();  // every wave is done with the scale and bias pairs
   if (wave > 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) red[wave - 1][mt * NT + nt][lane] = y[mt][nt];
+      for (int nt = 0; nt < NT; ++nt) sm.red[wave - 1][mt * NT + nt][lane] = y[mt][nt];
   }
   __syncthreads();
   if (wave == 0) {
@@ -403,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
       for (int nt = 0; nt < NT; ++nt) {
         f4 t = y[mt][nt];
 #pragma unroll
-        for (int w = 0; w < 3; ++w) t = t + red[w][mt * NT + nt][lane];
+        for (int w = 0; w < 3; ++w) t = t + sm.red[w][mt * NT + nt][lane];
         if (valid[nt]) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
