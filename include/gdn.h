@@ -190,8 +190,8 @@ int gdn_commit(const gdn_commit_args* args);
 
 typedef struct gdn_qlinear_seg {
   const void* w;      /* (N, K/8) uint32, 16-byte aligned */
-  const void* scales; /* (N, K/64) bf16 */
-  const void* biases; /* (N, K/64) bf16 */
+  const void* scales; /* (N, K/64) bf16, 8-byte aligned */
+  const void* biases; /* (N, K/64) bf16, 8-byte aligned */
   void* y;            /* (M, N) bf16; must not overlap any input */
   int n;              /* N >= 1 */
 } gdn_qlinear_seg;

@@ -401,8 +401,8 @@ int gdn_qlinear(const gdn_qlinear_args* a) {
     const gdn_qlinear_seg& g = a->segs[i];
     if (!g.w || !g.scales || !g.biases || !g.y || g.n < 1)
       return fail(GDN_EINVAL, "gdn_qlinear: segment %d needs w, scales, biases, y and n >= 1", i);
-    if (!aligned(g.w, 16) || !aligned(g.scales, 2) || !aligned(g.biases, 2) || !aligned(g.y, 2))
-      return fail(GDN_EINVAL, "gdn_qlinear: segment %d: w must be 16-byte and scales, biases, y 2-byte aligned", i);
+    if (!aligned(g.w, 16) || !aligned(g.scales, 8) || !aligned(g.biases, 8) || !aligned(g.y, 2))
+      return fail(GDN_EINVAL, "gdn_qlinear: segment %d: w must be 16-byte, scales and biases 8-byte and y 2-byte aligned", i);
     rows += g.n;
   }
   if (rows * L > (int64_t)1 << 31) return fail(GDN_EINVAL, "gdn_qlinear: too many rows");

@@ -294,8 +294,10 @@ __device__ __forceinline__ bf8 nibbles_bf16(uint32_t wd, NibbleConsts k) {
   return __builtin_bit_cast(bf8, r);
 }
 
-// A weight row's segment (the unrolled compare-and-select keeps the argument arrays out of
-// run-time indexing): its nibble words, scales, biases and output column.
+// A weight row's segment: its nibble words, scales, biases and output column. Every
+// candidate is read as a value first and held opaque (the empty asm), then selected: a
+// select between loads of the argument arrays is otherwise folded into one load at a
+// run-time index, for which the compiler copies the kernel arguments to scratch.
 struct RowPtrs {
   const uint32_t* w;
   const uint16_t *s, *b;
@@ -303,22 +305,36 @@ struct RowPtrs {
   int ystride;
 };
 __device__ __forceinline__ RowPtrs row_ptrs(const QParams& p, int layer, int row) {
+  const uint32_t* wv[GDN_QLINEAR_MAX_SEGS];
+  const uint16_t *sv[GDN_QLINEAR_MAX_SEGS], *bv[GDN_QLINEAR_MAX_SEGS];
+  uint16_t* yv[GDN_QLINEAR_MAX_SEGS];
+  int nv[GDN_QLINEAR_MAX_SEGS], rv[GDN_QLINEAR_MAX_SEGS];
+#pragma unroll
+  for (int q = 0; q < GDN_QLINEAR_MAX_SEGS; ++q) {
+    wv[q] = p.w[q];
+    sv[q] = p.s[q];
+    bv[q] = p.b[q];
+    yv[q] = p.y[q];
+    nv[q] = p.n[q];
+    rv[q] = p.row0[q];
+    asm volatile("" : "+s"(wv[q]), "+s"(sv[q]), "+s"(bv[q]), "+s"(yv[q]), "+s"(nv[q]), "+s"(rv[q]));
+  }
   int sg = 0;
 #pragma unroll
-  for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= p.row0[q]) ? 1 : 0;
-  const uint32_t* wseg = p.w[0];
-  const uint16_t *sseg = p.s[0], *bseg = p.b[0];
-  uint16_t* yseg = p.y[0];
-  int nseg = p.n[0], r0 = p.row0[0];
+  for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) sg += (q < p.nseg && row >= rv[q]) ? 1 : 0;
+  const uint32_t* wseg = wv[0];
+  const uint16_t *sseg = sv[0], *bseg = bv[0];
+  uint16_t* yseg = yv[0];
+  int nseg = nv[0], r0 = rv[0];
 #pragma unroll
   for (int q = 1; q < GDN_QLINEAR_MAX_SEGS; ++q) {
     if (sg == q) {
-      wseg = p.w[q];
-      sseg = p.s[q];
-      bseg = p.b[q];
-      yseg = p.y[q];
-      nseg = p.n[q];
-      r0 = p.row0[q];
+      wseg = wv[q];
+      sseg = sv[q];
+      bseg = bv[q];
+      yseg = yv[q];
+      nseg = nv[q];
+      r0 = rv[q];
     }
   }
   const int G = p.K / 64;
