@@ -251,6 +251,8 @@ def _ql(gdn, **kw):
     (dict(x=0x10008), "16-byte"),
     (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0, y=0x4000000, n=64)]), "segment 0"),
     (dict(segs=[dict(w=0x1000008, scales=0x2000000, biases=0x3000000, y=0x4000000, n=64)]), "16-byte"),
+    (dict(segs=[dict(w=0x1000000, scales=0x2000004, biases=0x3000000, y=0x4000000, n=64)]), "8-byte"),
+    (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000002, y=0x4000000, n=64)]), "8-byte"),
     (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x10000 + 64, n=64)]), "operand"),
     (dict(segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x1000000 + 64, n=64)]), "weight"),
     (dict(n_segs=2, segs=[dict(w=0x1000000, scales=0x2000000, biases=0x3000000, y=0x4000000, n=64),
