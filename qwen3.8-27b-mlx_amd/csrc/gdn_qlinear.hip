@@ -268,14 +268,12 @@ __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// (a & m) | c in one instruction. VOP3 takes no literal constant on this target and at
-// most one SGPR, so m and c come in VGPRs (set once per kernel by nibble_consts); written
-// out, the compiler emits a separate AND and OR with literals instead.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
-  return r;
-}
+// (a & m) | c: with m and c in VGPRs (opaque values from nibble_consts) the compiler selects
+// one v_and_or_b32 for it -- with literal constants it cannot (a VOP3 takes no literal on
+// this target and at most one SGPR) and emits a separate AND and OR. Written out in C, not
+// as inline asm, so that the compiler also sees the instruction and keeps the wait states
+// an MFMA reading its result needs.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 struct NibbleConsts {
   uint32_t mask, bias;  // 0x000F000F, 0x43004300
 };
