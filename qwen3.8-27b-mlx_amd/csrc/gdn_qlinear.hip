@@ -279,8 +279,9 @@ struct NibbleConsts {
 };
 __device__ __forceinline__ NibbleConsts nibble_consts() {
   NibbleConsts k;
-  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(k.mask));
-  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.bias));
+  k.mask = 0x000F000Fu;
+  k.bias = 0x43004300u;
+  asm volatile("" : "+v"(k.mask), "+v"(k.bias));  // (emits nothing: keeps them opaque VGPR values)
   return k;
 }
 
