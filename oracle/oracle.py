@@ -237,6 +237,28 @@ def qlinear(x_bf16, w_u32, scales_bf16, biases_bf16):
     return y
 
 
+def qlinear_blocked(x_bf16, w_u32, scales_bf16, biases_bf16, rows: int = 2048):
+    """The same product as qlinear for large shapes: W dequantized to fp64 with numpy bit
+    ops (value i of a word in nibble i, python/mlp_kernel.py:54-56) a block of rows at a
+    time, then an fp64 matrix product -> (M, N) fp64. Equal to qlinear up to fp64 summation
+    order (tests/test_oracle.py pins it)."""
+    x = from_bf16(np.ascontiguousarray(x_bf16, np.uint16)).astype(np.float64)
+    w = np.ascontiguousarray(w_u32, dtype=np.uint32)
+    s = from_bf16(np.ascontiguousarray(scales_bf16, np.uint16)).astype(np.float64)
+    b = from_bf16(np.ascontiguousarray(biases_bf16, np.uint16)).astype(np.float64)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape == (N, K // 8) and s.shape == (N, K // 64) and b.shape == (N, K // 64)
+    shifts = 4 * np.arange(8, dtype=np.uint32)
+    y = np.empty((M, N), np.float64)
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        q = ((w[r0:r1, :, None] >> shifts) & 0xF).reshape(r1 - r0, K).astype(np.float64)
+        Wd = (q.reshape(r1 - r0, K // 64, 64) * s[r0:r1, :, None] + b[r0:r1, :, None]).reshape(r1 - r0, K)
+        y[:, r0:r1] = x @ Wd.T
+    return y
+
+
 def gated_rmsnorm(o, z_bf16, gamma, eps: float = 1e-6):
     """GatedRMSNorm: rows of o (..., D) fp32, z bf16 bits, gamma (D) fp32 -> bf16 bits."""
     o, z, g = _f32(o), _u16(z_bf16), _f32(gamma)

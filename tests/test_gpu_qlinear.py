@@ -198,3 +198,41 @@ def test_qlinear_mfma_reuses_a_caller_workspace(O, gdn, dev):
         (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev), workspace=ws)
         torch.cuda.synchronize()
         check(to_np(y), O.qlinear(x[0], w[0], s[0], b[0]), bound(O, x[0], s[0], b[0]), f"M={M}")
+
+
+# ---- the widest MFMA tiles: 64 weight rows per workgroup (NT = 4) ----
+# The host picks the most weight rows per workgroup (64, 32, 16) that still gives >= 512
+# workgroups: n_layers * ceil(R / 64) * (m-tiles / MT) >= 512 selects 64.
+
+@pytest.mark.parametrize("M", [40, 64])
+def test_qlinear_mfma_in_proj_two_layers_64_row_tiles(O, gdn, dev, M):
+    """The whole in_proj (R = 16480 rows, K = 5120) of two layers: 2 x 258 tiles of 64 rows =
+    516 workgroups, so the 64-row form runs, with 3 (M = 40) and 4 (M = 64) m-tiles."""
+    import torch
+    log_case(f"qlinear (MFMA path, 64-row tiles) in_proj 4 segments x 2 layers, M={M}, K=5120")
+    L, K = 2, 5120
+    ns = [10240, 6144, 48, 48]
+    mats, host, x = [], [], None
+    for i, n in enumerate(ns):
+        xi, w, s, b = quant_inputs(O, L, M, n, K, seed=600 + 10 * M + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w, s, b))
+        host.append((w, s, b))
+    ys = gdn.qlinear(mats, to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        got = to_np(y)
+        for l in range(L):
+            check(got[l], O.qlinear_blocked(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
+
+
+def test_qlinear_mfma_512_rows(O, gdn, dev):
+    """The most rows the quantized path takes (512 = 32 m-tiles in 8 groups of 4), N = 4096:
+    64 tiles of 64 rows x 8 = 512 workgroups, so the 64-row form with 4 m-tiles runs."""
+    import torch
+    log_case("qlinear (MFMA path, 64-row tiles) M=512, N=4096, K=1024")
+    M, N, K = 512, 4096, 1024
+    x, w, s, b = quant_inputs(O, 1, M, N, K, seed=700)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    check(to_np(y), O.qlinear_blocked(x[0], w[0], s[0], b[0]), bound(O, x[0], s[0], b[0]), "y")

@@ -402,6 +402,15 @@ def test_qlinear_matches_numpy_dequantize(O):
     assert np.abs(O.qlinear(x, w, s, b) - ref).max() <= 1e-12 * np.abs(ref).max()
 
 
+def test_qlinear_blocked_equals_qlinear(O):
+    """The blocked numpy form (used for large GPU checks) equals the C oracle, with row blocks
+    that split the matrix unevenly."""
+    x, w, s, b = _qlin_inputs(O, 5, 300, 1024, 6)
+    ref = O.qlinear(x, w, s, b)
+    got = O.qlinear_blocked(x, w, s, b, rows=128)
+    assert np.abs(got - ref).max() <= 1e-12 * np.abs(ref).max()
+
+
 def test_qlinear_nibble_order_known_answers(O):
     """A single nonzero nibble at value position i of word j selects x[8j + i]; scale 1,
     bias 0; an all-zero w with bias b gives b * sum(x) per group."""
