@@ -30,7 +30,8 @@
  *
  * Conventions
  *   - Every pointer is device memory owned by the caller; the library allocates no
- *     device memory on any entry point and keeps no per-call state.
+ *     device memory on any entry point and keeps no per-call state. (gdn_qlinear_noalloc
+ *     uses a fixed scratch array the library holds per device, see there.)
  *   - All tensors are dense, row-major, with a leading n_layers dimension: layer l of
  *     a tensor of per-layer size N starts at element l*N. n_layers > 1 runs that many
  *     independent layers in one launch (the layers of a model evaluated together, or
@@ -51,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 2
+#define GDN_ABI_VERSION 3
 #define GDN_HEAD_DIM 128 /* Dk = Dv */
 #define GDN_CONV_TAPS 4  /* conv kernel size; the conv state holds GDN_CONV_TAPS-1 rows */
 
@@ -220,6 +221,18 @@ int gdn_qlinear(const gdn_qlinear_args* args);
 /* Workspace bytes gdn_qlinear needs for these arguments' n_layers, m and k (0 on the
  * GEMV path); the other fields are not read. */
 int gdn_qlinear_workspace_size(const gdn_qlinear_args* args, size_t* bytes);
+
+/* gdn_qlinear without a workspace argument and without any allocation. No counterpart in
+ * the reference (MLX allocates inside quantized_matmul): for callers that cannot allocate
+ * device memory -- code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc. Same arguments, kernels and results as gdn_qlinear, except that `workspace`
+ * must be NULL and `workspace_bytes` 0: the MFMA path's operand goes to a scratch array
+ * the library holds on each device (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES, kept until the
+ * process ends), so calls whose gdn_qlinear_workspace_size() exceeds that are GDN_EINVAL
+ * (one layer at any m and k fits). Every call on a device shares that device's scratch:
+ * calls that overlap in time on one device (different streams or threads) race. */
+#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int gdn_qlinear_noalloc(const gdn_qlinear_args* args);
 
 /* 1 if the current HIP device is a gfx950 the kernels were built for, else 0. */
 int gdn_available(void);

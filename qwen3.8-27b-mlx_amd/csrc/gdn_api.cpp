@@ -196,6 +196,82 @@ int run_empty(const gdn_layer_args* a, hipStream_t stream) {
   return ok();
 }
 
+// Shared validation of gdn_qlinear / gdn_qlinear_noalloc. With `noalloc` the workspace
+// fields must be empty and the MFMA path's operand must fit the library's scratch (which no
+// caller buffer can overlap: its address is not exposed).
+int validate_qlinear(const gdn_qlinear_args* a, const char* fn, bool noalloc) {
+  if (!a) return fail(GDN_EINVAL, "%s: args is NULL", fn);
+  if (a->n_layers < 1 || a->m < 1 || a->m > GDN_QLINEAR_MAX_ROWS)
+    return fail(GDN_EINVAL, "%s: bad shape (n_layers=%d m=%d; m must be 1..%d)", fn, a->n_layers, a->m,
+                GDN_QLINEAR_MAX_ROWS);
+  if (!gdn::qlinear_k_supported(a->k))
+    return fail(GDN_EINVAL, "%s: k=%d unsupported (1024, 2048, 4096, 5120, 6144, 8192)", fn, a->k);
+  if (a->n_segs < 1 || a->n_segs > GDN_QLINEAR_MAX_SEGS)
+    return fail(GDN_EINVAL, "%s: n_segs must be 1..%d", fn, GDN_QLINEAR_MAX_SEGS);
+  const int64_t L = a->n_layers, M = a->m, K = a->k;
+  const size_t ws_need = gdn::qlinear_workspace_bytes(a->n_layers, a->m, a->k);
+  if (noalloc) {
+    if (a->workspace || a->workspace_bytes)
+      return fail(GDN_EINVAL, "%s: takes no workspace (workspace must be NULL, workspace_bytes 0)", fn);
+    if (ws_need > GDN_QLINEAR_NOALLOC_SCRATCH_BYTES)
+      return fail(GDN_EINVAL, "%s: n_layers=%d m=%d k=%d needs %zu bytes of scratch, more than the %zu the library holds",
+                  fn, a->n_layers, a->m, a->k, ws_need, (size_t)GDN_QLINEAR_NOALLOC_SCRATCH_BYTES);
+  } else if (ws_need > 0) {  // MFMA path: the operand in fragment order goes to the workspace
+    if (!a->workspace || a->workspace_bytes < ws_need)
+      return fail(GDN_EINVAL, "%s: m=%d k=%d needs a workspace of %zu bytes (got %zu)", fn, a->m, a->k, ws_need,
+                  a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(GDN_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+  }
+  const bool norm = a->norm_x != nullptr;
+  if (norm == (a->x != nullptr))
+    return fail(GDN_EINVAL, "%s: exactly one of x and norm_x is required", fn);
+  Range in[3];
+  if (norm) {
+    if (!a->norm_z || !a->norm_gamma) return fail(GDN_EINVAL, "%s: the norm needs norm_z and norm_gamma", fn);
+    if (!(a->norm_eps >= 0.0f)) return fail(GDN_EINVAL, "%s: norm_eps must be >= 0", fn);
+    if (!aligned(a->norm_x, 16) || !aligned(a->norm_z, 16) || !aligned(a->norm_gamma, 16))
+      return fail(GDN_EINVAL, "%s: norm_x, norm_z and norm_gamma must be 16-byte aligned", fn);
+    in[0] = range_of(a->norm_x, L * M * K * 4);
+    in[1] = range_of(a->norm_z, L * M * K * 2);
+    in[2] = range_of(a->norm_gamma, L * 128 * 4);
+  } else {
+    if (!aligned(a->x, 16)) return fail(GDN_EINVAL, "%s: x must be 16-byte aligned", fn);
+    in[0] = range_of(a->x, L * M * K * 2);
+  }
+  int64_t rows = 0;
+  for (int i = 0; i < a->n_segs; ++i) {
+    const gdn_qlinear_seg& g = a->segs[i];
+    if (!g.w || !g.scales || !g.biases || !g.y || g.n < 1)
+      return fail(GDN_EINVAL, "%s: segment %d needs w, scales, biases, y and n >= 1", fn, i);
+    if (!aligned(g.w, 16) || !aligned(g.scales, 8) || !aligned(g.biases, 8) || !aligned(g.y, 2))
+      return fail(GDN_EINVAL, "%s: segment %d: w must be 16-byte, scales and biases 8-byte and y 2-byte aligned", fn, i);
+    rows += g.n;
+  }
+  if (rows * L > (int64_t)1 << 31) return fail(GDN_EINVAL, "%s: too many rows", fn);
+  const Range ws = range_of(ws_need > 0 && !noalloc ? a->workspace : nullptr, (int64_t)ws_need);
+  for (const Range& r : in)
+    if (overlap(ws, r)) return fail(GDN_EINVAL, "%s: the workspace must not overlap the operand", fn);
+  for (int i = 0; i < a->n_segs; ++i) {
+    const gdn_qlinear_seg& g = a->segs[i];
+    const Range y = range_of(g.y, L * M * g.n * 2);
+    if (overlap(y, ws)) return fail(GDN_EINVAL, "%s: segment %d: y must not overlap the workspace", fn, i);
+    if (overlap(ws, range_of(g.w, L * g.n * K / 2)) || overlap(ws, range_of(g.scales, L * g.n * K / 32)) ||
+        overlap(ws, range_of(g.biases, L * g.n * K / 32)))
+      return fail(GDN_EINVAL, "%s: the workspace must not overlap segment %d's weights", fn, i);
+    for (const Range& r : in)
+      if (overlap(y, r)) return fail(GDN_EINVAL, "%s: segment %d: y must not overlap the operand", fn, i);
+    for (int j = 0; j < a->n_segs; ++j) {
+      const gdn_qlinear_seg& h = a->segs[j];
+      if (overlap(y, range_of(h.w, L * h.n * K / 2)) || overlap(y, range_of(h.scales, L * h.n * K / 32)) ||
+          overlap(y, range_of(h.biases, L * h.n * K / 32)))
+        return fail(GDN_EINVAL, "%s: segment %d: y must not overlap a weight tensor", fn, i);
+      if (j != i && overlap(y, range_of(h.y, L * M * h.n * 2)))
+        return fail(GDN_EINVAL, "%s: outputs of segments %d and %d overlap", fn, i, j);
+    }
+  }
+  return GDN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -364,73 +440,28 @@ int gdn_commit(const gdn_commit_args* a) {
 }
 
 int gdn_qlinear(const gdn_qlinear_args* a) {
-  if (!a) return fail(GDN_EINVAL, "gdn_qlinear: args is NULL");
-  if (a->n_layers < 1 || a->m < 1 || a->m > GDN_QLINEAR_MAX_ROWS)
-    return fail(GDN_EINVAL, "gdn_qlinear: bad shape (n_layers=%d m=%d; m must be 1..%d)", a->n_layers, a->m,
-                GDN_QLINEAR_MAX_ROWS);
-  if (!gdn::qlinear_k_supported(a->k))
-    return fail(GDN_EINVAL, "gdn_qlinear: k=%d unsupported (1024, 2048, 4096, 5120, 6144, 8192)", a->k);
-  if (a->n_segs < 1 || a->n_segs > GDN_QLINEAR_MAX_SEGS)
-    return fail(GDN_EINVAL, "gdn_qlinear: n_segs must be 1..%d", GDN_QLINEAR_MAX_SEGS);
-  const int64_t L = a->n_layers, M = a->m, K = a->k;
-  const size_t ws_need = gdn::qlinear_workspace_bytes(a->n_layers, a->m, a->k);
-  if (ws_need > 0) {  // MFMA path: the operand in fragment order goes to the workspace
-    if (!a->workspace || a->workspace_bytes < ws_need)
-      return fail(GDN_EINVAL, "gdn_qlinear: m=%d k=%d needs a workspace of %zu bytes (got %zu)", a->m, a->k, ws_need,
-                  a->workspace ? a->workspace_bytes : (size_t)0);
-    if (!aligned(a->workspace, 256)) return fail(GDN_EINVAL, "gdn_qlinear: workspace must be 256-byte aligned");
-  }
-  const bool norm = a->norm_x != nullptr;
-  if (norm == (a->x != nullptr))
-    return fail(GDN_EINVAL, "gdn_qlinear: exactly one of x and norm_x is required");
-  Range in[3];
-  if (norm) {
-    if (!a->norm_z || !a->norm_gamma) return fail(GDN_EINVAL, "gdn_qlinear: the norm needs norm_z and norm_gamma");
-    if (!(a->norm_eps >= 0.0f)) return fail(GDN_EINVAL, "gdn_qlinear: norm_eps must be >= 0");
-    if (!aligned(a->norm_x, 16) || !aligned(a->norm_z, 16) || !aligned(a->norm_gamma, 16))
-      return fail(GDN_EINVAL, "gdn_qlinear: norm_x, norm_z and norm_gamma must be 16-byte aligned");
-    in[0] = range_of(a->norm_x, L * M * K * 4);
-    in[1] = range_of(a->norm_z, L * M * K * 2);
-    in[2] = range_of(a->norm_gamma, L * 128 * 4);
-  } else {
-    if (!aligned(a->x, 16)) return fail(GDN_EINVAL, "gdn_qlinear: x must be 16-byte aligned");
-    in[0] = range_of(a->x, L * M * K * 2);
-  }
-  int64_t rows = 0;
-  for (int i = 0; i < a->n_segs; ++i) {
-    const gdn_qlinear_seg& g = a->segs[i];
-    if (!g.w || !g.scales || !g.biases || !g.y || g.n < 1)
-      return fail(GDN_EINVAL, "gdn_qlinear: segment %d needs w, scales, biases, y and n >= 1", i);
-    if (!aligned(g.w, 16) || !aligned(g.scales, 8) || !aligned(g.biases, 8) || !aligned(g.y, 2))
-      return fail(GDN_EINVAL, "gdn_qlinear: segment %d: w must be 16-byte, scales and biases 8-byte and y 2-byte aligned", i);
-    rows += g.n;
-  }
-  if (rows * L > (int64_t)1 << 31) return fail(GDN_EINVAL, "gdn_qlinear: too many rows");
-  const Range ws = range_of(ws_need > 0 ? a->workspace : nullptr, (int64_t)ws_need);
-  for (const Range& r : in)
-    if (overlap(ws, r)) return fail(GDN_EINVAL, "gdn_qlinear: the workspace must not overlap the operand");
-  for (int i = 0; i < a->n_segs; ++i) {
-    const gdn_qlinear_seg& g = a->segs[i];
-    const Range y = range_of(g.y, L * M * g.n * 2);
-    if (overlap(y, ws)) return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap the workspace", i);
-    if (overlap(ws, range_of(g.w, L * g.n * K / 2)) || overlap(ws, range_of(g.scales, L * g.n * K / 32)) ||
-        overlap(ws, range_of(g.biases, L * g.n * K / 32)))
-      return fail(GDN_EINVAL, "gdn_qlinear: the workspace must not overlap segment %d's weights", i);
-    for (const Range& r : in)
-      if (overlap(y, r)) return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap the operand", i);
-    for (int j = 0; j < a->n_segs; ++j) {
-      const gdn_qlinear_seg& h = a->segs[j];
-      if (overlap(y, range_of(h.w, L * h.n * K / 2)) || overlap(y, range_of(h.scales, L * h.n * K / 32)) ||
-          overlap(y, range_of(h.biases, L * h.n * K / 32)))
-        return fail(GDN_EINVAL, "gdn_qlinear: segment %d: y must not overlap a weight tensor", i);
-      if (j != i && overlap(y, range_of(h.y, L * M * h.n * 2)))
-        return fail(GDN_EINVAL, "gdn_qlinear: outputs of segments %d and %d overlap", i, j);
-    }
-  }
-  int rc = check_device();
+  int rc = validate_qlinear(a, "gdn_qlinear", false);
+  if (rc != GDN_OK) return rc;
+  rc = check_device();
   if (rc != GDN_OK) return rc;
   hipError_t e = gdn::launch_qlinear(*a, static_cast<hipStream_t>(a->stream));
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear launch");
+  return ok();
+}
+
+int gdn_qlinear_noalloc(const gdn_qlinear_args* a) {
+  int rc = validate_qlinear(a, "gdn_qlinear_noalloc", true);
+  if (rc != GDN_OK) return rc;
+  rc = check_device();
+  if (rc != GDN_OK) return rc;
+  gdn_qlinear_args b = *a;
+  if (gdn::qlinear_workspace_bytes(a->n_layers, a->m, a->k) > 0) {
+    hipError_t e = gdn::qlinear_scratch(&b.workspace);
+    if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_noalloc: hipGetSymbolAddress of the scratch");
+    b.workspace_bytes = GDN_QLINEAR_NOALLOC_SCRATCH_BYTES;
+  }
+  hipError_t e = gdn::launch_qlinear(b, static_cast<hipStream_t>(a->stream));
+  if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_noalloc launch");
   return ok();
 }
 

@@ -68,5 +68,8 @@ bool qlinear_k_supported(int k);
 bool qlinear_uses_gemv(int m, int k);
 size_t qlinear_workspace_bytes(int n_layers, int m, int k);
 hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream);
+// Device address of this device's gdn_qlinear_noalloc scratch
+// (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES, 256-byte aligned), looked up once per device.
+hipError_t qlinear_scratch(void** ptr);
 
 }  // namespace gdn

@@ -29,6 +29,7 @@
 #include "gdn_internal.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace gdn {
 namespace {
@@ -541,6 +542,33 @@ hipError_t launch_gemm_mt(int NT, const QParams& p, dim3 grid, hipStream_t strea
   return hipGetLastError();
 }
 }  // namespace
+
+// The no-allocation entry point's workspace: one array per device, held until the process
+// ends. Host code never passes `scratch` itself to a kernel (on the host it names a
+// stand-in, not device memory): its device address comes from hipGetSymbolAddress, once per
+// device with that device current, and only that address is used.
+static __device__ __align__(256) unsigned char scratch[GDN_QLINEAR_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+void* g_scratch_ptr[kMaxScratchDevices];
+hipError_t g_scratch_err[kMaxScratchDevices];
+}  // namespace
+
+hipError_t qlinear_scratch(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  *ptr = g_scratch_ptr[dev];
+  return g_scratch_err[dev];
+}
 
 size_t qlinear_workspace_bytes(int n_layers, int m, int k) {
   if (qlinear_uses_gemv(m, k)) return 0;

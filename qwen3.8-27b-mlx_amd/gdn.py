@@ -34,10 +34,11 @@ CONV_TAPS = 4
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
 QLINEAR_MAX_ROWS = 512
+QLINEAR_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-           "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_available", "gdn_abi_version",
-           "gdn_last_error")
+           "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_qlinear_noalloc", "gdn_available",
+           "gdn_abi_version", "gdn_last_error")
 
 
 class GdnError(RuntimeError):
@@ -119,6 +120,8 @@ def lib() -> ctypes.CDLL:
         L.gdn_qlinear.restype = _int
         L.gdn_qlinear_workspace_size.argtypes = [ctypes.POINTER(QLinearArgs), ctypes.POINTER(ctypes.c_size_t)]
         L.gdn_qlinear_workspace_size.restype = _int
+        L.gdn_qlinear_noalloc.argtypes = [ctypes.POINTER(QLinearArgs)]
+        L.gdn_qlinear_noalloc.restype = _int
         L.gdn_available.argtypes = []
         L.gdn_available.restype = _int
         L.gdn_abi_version.argtypes = []
@@ -157,6 +160,10 @@ def call_commit(args: CommitArgs) -> None:
 
 def call_qlinear(args: QLinearArgs) -> None:
     _check(lib().gdn_qlinear(ctypes.byref(args)))
+
+
+def call_qlinear_noalloc(args: QLinearArgs) -> None:
+    _check(lib().gdn_qlinear_noalloc(ctypes.byref(args)))
 
 
 def qlinear_workspace_size(m: int, k: int, n_layers: int = 1) -> int:
@@ -422,11 +429,12 @@ class QuantLinear:
         return self.w.shape[-2]
 
 
-def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, stream=None):
+def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, stream=None,
+                 alloc_workspace: bool = True):
     """gdn_qlinear_args for y_i = x W_i^T, i over `mats` (1..4 QuantLinear reading the same
     x), or with norm = (o, z, gamma, eps) the layer's GatedRMSNorm of o as the operand.
-    Allocates the outputs, and the workspace when the rows need one and none is given;
-    returns (args, [y_i])."""
+    Allocates the outputs, and (with alloc_workspace) the workspace when the rows need one
+    and none is given; returns (args, [y_i])."""
     import torch
     src = x if x is not None else norm[0]
     K = src.shape[-1]
@@ -445,7 +453,7 @@ def qlinear_args(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, 
         need = qlinear_workspace_size(M, K, n_layers)
     except GdnError:
         need = 0  # a bad shape: gdn_qlinear itself reports it
-    if need and workspace is None:
+    if need and workspace is None and alloc_workspace:
         workspace = torch.empty(need, dtype=torch.uint8, device=src.device)
     if workspace is not None:
         a.workspace = _ptr(workspace)
@@ -462,4 +470,13 @@ def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, strea
     (allocated here unless given)."""
     args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, workspace=workspace, stream=stream)
     call_qlinear(args)
+    return ys
+
+
+def qlinear_noalloc(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
+    """qlinear through gdn_qlinear_noalloc: no workspace, the library's per-device scratch
+    instead (one layer at any rows fits; calls overlapping on one device race on it). Only
+    the outputs are allocated here; the library call itself allocates nothing."""
+    args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, stream=stream, alloc_workspace=False)
+    call_qlinear_noalloc(args)
     return ys

@@ -22,8 +22,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(
         ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
-         "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_available", "gdn_abi_version",
-         "gdn_last_error"])
+         "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_qlinear_noalloc", "gdn_available",
+         "gdn_abi_version", "gdn_last_error"])
 
 
 def test_library_exports_every_declared_symbol(gdn):
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(gdn):
                          text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s+(gdn_\w+)", out))
     assert set(declared_functions()) <= exported
-    assert L.gdn_abi_version() == 2
+    assert L.gdn_abi_version() == 3
     assert set(gdn.EXPORTS) == set(declared_functions())
 
 
@@ -280,3 +280,28 @@ def test_qlinear_workspace_size(gdn):
     assert gdn.qlinear_workspace_size(512, 1024) == 32 * 32 * 1024
     with pytest.raises(gdn.GdnError):
         gdn.qlinear_workspace_size(513, 5120)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(m=40, workspace=0x8000000, workspace_bytes=1 << 30), "takes no workspace"),
+    (dict(m=4, workspace_bytes=16), "takes no workspace"),
+    (dict(n_layers=2, m=512, k=8192), "more than the 8388608"),
+    (dict(n_layers=48, m=40, k=5120), "more than the 8388608"),
+    (dict(m=513), "bad shape"),
+    (dict(x=None), "exactly one"),
+])
+def test_qlinear_noalloc_rejects_bad_arguments(gdn, kw, msg):
+    """The no-allocation variant takes no workspace and refuses shapes whose operand does not
+    fit the library's scratch (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES); its other checks are
+    gdn_qlinear's."""
+    rc = gdn.lib().gdn_qlinear_noalloc(ctypes.byref(_ql(gdn, **kw)))
+    assert rc == gdn.GDN_EINVAL
+    assert msg in gdn.last_error(), gdn.last_error()
+    assert gdn.last_error().startswith("gdn_qlinear_noalloc:")
+
+
+def test_qlinear_noalloc_scratch_fits_one_layer(gdn):
+    """One layer at the largest rows and k fits the scratch exactly."""
+    assert gdn.qlinear_workspace_size(512, 8192) == gdn.QLINEAR_NOALLOC_SCRATCH_BYTES
+    text = open(HEADER).read()
+    assert "#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)" in text
