@@ -369,6 +369,36 @@ int gdn_prefill_chunked(const gdn_layer_args* a) {
       return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace must be 256-byte aligned");
     const int64_t L = a->n_layers;
     if (L != 1) return fail(GDN_EINVAL, "gdn_prefill_chunked: one layer per call (n_layers = 1)");
+    // the workspace is written while every other buffer is read or written
+    const int64_t B = a->batch, T = a->seq_len, Hk = a->num_k_heads, Hv = a->num_v_heads,
+                  D = GDN_HEAD_DIM, C = 2 * Hk * D + Hv * D;
+    const bool conv = a->frontend == GDN_FRONTEND_CONV, raw = a->gate_mode == GDN_GATES_RAW;
+    const struct {
+      const void* p;
+      int64_t bytes;
+      const char* name;
+    } bufs[] = {
+        {a->o, B * T * Hv * D * (a->o_dtype == GDN_DTYPE_BF16 ? 2 : 4), "o"},
+        {a->state_in, B * Hv * D * D * 4, "state_in"},
+        {a->state_out, B * Hv * D * D * 4, "state_out"},
+        {conv ? a->x : nullptr, B * T * C * 2, "x"},
+        {conv ? a->conv_weight : nullptr, 4 * C * 2, "conv_weight"},
+        {conv ? a->conv_state_in : nullptr, B * 3 * C * 2, "conv_state_in"},
+        {conv ? a->conv_state_out : nullptr, B * 3 * C * 2, "conv_state_out"},
+        {conv ? nullptr : a->q, B * T * Hk * D * 2, "q"},
+        {conv ? nullptr : a->k, B * T * Hk * D * 2, "k"},
+        {conv ? nullptr : a->v, B * T * Hv * D * 2, "v"},
+        {raw ? a->a : nullptr, B * T * Hv * 2, "a"},
+        {raw ? a->b : nullptr, B * T * Hv * 2, "b"},
+        {raw ? a->A_log : nullptr, Hv * 4, "A_log"},
+        {raw ? a->dt_bias : nullptr, Hv * 4, "dt_bias"},
+        {raw ? nullptr : a->alpha, B * T * Hv * 4, "alpha"},
+        {raw ? nullptr : a->beta, B * T * Hv * 4, "beta"},
+    };
+    const Range ws = range_of(a->workspace, (int64_t)need);
+    for (const auto& buf : bufs)
+      if (overlap(ws, range_of(buf.p, buf.bytes)))
+        return fail(GDN_EINVAL, "gdn_prefill_chunked: the workspace must not overlap %s", buf.name);
   }
   rc = check_device();
   if (rc != GDN_OK) return rc;

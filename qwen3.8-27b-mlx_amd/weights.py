@@ -18,7 +18,7 @@ import os
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
-from .gdn import QuantLinear
+from .gdn import CONV_TAPS, HEAD_DIM, QuantLinear
 
 _PREFIXES = ("model.language_model.", "model.")
 
@@ -165,6 +165,14 @@ class Checkpoint:
         path = f"layers.{i}.linear_attn"
         nk, nv = c.linear_num_key_heads, c.linear_num_value_heads
         dk, dv, K, h = c.linear_key_head_dim, c.linear_value_head_dim, c.linear_conv_kernel_dim, c.hidden_size
+        # the kernels implement 4 conv taps, 128-wide heads and an integer number of v-heads
+        # per k-head (include/gdn.h): anything else would load and then be misread
+        if K != CONV_TAPS:
+            raise ValueError(f"linear_conv_kernel_dim = {K}; the kernels take {CONV_TAPS} taps")
+        if dk != HEAD_DIM or dv != HEAD_DIM:
+            raise ValueError(f"linear key/value head dims = {dk}/{dv}; the kernels take {HEAD_DIM}")
+        if nk < 1 or nv < 1 or nv % nk != 0:
+            raise ValueError(f"linear_num_value_heads = {nv} is not a multiple of linear_num_key_heads = {nk}")
         qkv_dim, z_dim = 2 * nk * dk + nv * dv, nv * dv
         conv = self._take(path + ".conv1d.weight", (qkv_dim, 1, K))
         return DeltaNetLayerWeights(

@@ -148,6 +148,26 @@ def test_prefill_workspace_size_and_checks(gdn):
     assert rc == gdn.GDN_EINVAL and "o must be 16-byte aligned" in gdn.last_error()
 
 
+@pytest.mark.parametrize("kw,name", [
+    (dict(o=0x10000000 + 4096), "o"),
+    (dict(state_in=0x10000000 + 4096, state_out=0x10000000 + 4096), "state_in"),
+    (dict(state_out=0x10000000 - 4096), "state_out"),   # ends inside the workspace
+    (dict(a=0x10000000 + 256), "a"),
+    (dict(A_log=0x10000000 + 512), "A_log"),
+    (dict(v=0x10000000 - 256), "v"),
+    (dict(frontend=1, x=0x10000000 + 4096, conv_weight=0x8000), "x"),
+    (dict(frontend=1, x=0xA000000, conv_weight=0x8000, conv_state_out=0x10000000), "conv_state_out"),
+    (dict(gate_mode=1, a=None, b=None, alpha=0x8000000, beta=0x10000000 + 1024), "beta"),
+])
+def test_prefill_rejects_a_workspace_that_overlaps(gdn, kw, name):
+    """The workspace is written while every other buffer is live: any overlap is an error."""
+    base = dict(seq_len=100, workspace=0x10000000, workspace_bytes=1 << 28)
+    base.update(kw)
+    rc = gdn.lib().gdn_prefill_chunked(ctypes.byref(_args(gdn, **base)))
+    assert rc == gdn.GDN_EINVAL, gdn.last_error()
+    assert f"the workspace must not overlap {name}" in gdn.last_error(), gdn.last_error()
+
+
 def test_null_args_and_prefill_states(gdn):
     L = gdn.lib()
     assert L.gdn_run(None) == gdn.GDN_EINVAL and "NULL" in gdn.last_error()

@@ -18,7 +18,7 @@ PFX = "model.language_model.layers.0.linear_attn."
 
 
 def write_checkpoint(path, rng, out_proj_quantized=False, drop=None, bad_shape=None,
-                     hk=HK, hv=HV):
+                     hk=HK, hv=HV, cfg_override=None):
     import torch
     from safetensors.torch import save_file
     os.makedirs(path, exist_ok=True)
@@ -62,6 +62,7 @@ def write_checkpoint(path, rng, out_proj_quantized=False, drop=None, bad_shape=N
                            "linear_key_head_dim": D, "linear_value_head_dim": D,
                            "linear_conv_kernel_dim": KC, "rms_norm_eps": 1e-6},
            "quantization": {"group_size": 64, "bits": 4, "quantized_modules": mods}}
+    cfg["text_config"].update(cfg_override or {})
     json.dump(cfg, open(os.path.join(path, "config.json"), "w"))
     return t
 
@@ -101,6 +102,20 @@ def test_reader_errors(gdn, tmp_path):
     write_checkpoint(str(tmp_path / "c"), rng)
     with pytest.raises(ValueError, match="full_attention"):
         gdn.weights.Checkpoint(str(tmp_path / "c")).deltanet_layer(1, device="cpu")
+
+
+@pytest.mark.parametrize("override,msg", [
+    (dict(linear_conv_kernel_dim=3), "linear_conv_kernel_dim = 3"),
+    (dict(linear_key_head_dim=64), "head dims = 64/128"),
+    (dict(linear_value_head_dim=256), "head dims = 128/256"),
+    (dict(linear_num_value_heads=5), "not a multiple"),
+])
+def test_reader_rejects_shapes_the_kernels_do_not_take(gdn, tmp_path, override, msg):
+    """A config the kernels cannot run (other conv taps, head dims, a fractional v-head to
+    k-head ratio) is refused at load, before any tensor is read."""
+    write_checkpoint(str(tmp_path), np.random.default_rng(3), cfg_override=override)
+    with pytest.raises(ValueError, match=msg):
+        gdn.weights.Checkpoint(str(tmp_path)).deltanet_layer(0, device="cpu")
 
 
 @pytest.mark.gpu
