@@ -15,7 +15,7 @@
 #include "gdn_internal.h"
 
 namespace gdn {
-int recurrent_tile_rows();
+int recurrent_tile_rows(long long heads);
 size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv);
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream);
 }  // namespace gdn
@@ -309,7 +309,8 @@ int gdn_run(const gdn_layer_args* a) {
   p.gate_raw = a->gate_mode == GDN_GATES_RAW;
   p.o_bf16 = a->o_dtype == GDN_DTYPE_BF16;
   p.states_tbh = a->states_layout == GDN_STATES_TBH;
-  const int64_t tiles = GDN_HEAD_DIM / gdn::recurrent_tile_rows();
+  const int64_t tiles =
+      GDN_HEAD_DIM / gdn::recurrent_tile_rows((long long)a->n_layers * a->batch * a->num_v_heads);
   const int64_t nblocks = (int64_t)a->n_layers * a->batch * a->num_v_heads * tiles;
   p.nblocks = static_cast<int>(nblocks);
   // XCD-aware order (the 6 workgroups of a k-head on one XCD, whose L2 serves their shared

@@ -1,12 +1,14 @@
 // Recurrent gated-delta kernel for gfx950: decode (T = 1), speculative verify
 // (T steps, every per-step state written) and any other T.
 //
-// Work decomposition. One workgroup = 4 wave64s = one (layer, batch, v-head,
-// 64-row Dv tile): 32 KB of fp32 state, read once and written once per call whatever T
-// is. Each wave owns 16 state rows; inside a wave each 16-lane DPP row owns one state
-// row at a time and a lane holds 4 rows ("slots") x 8 fp32 elements: [4j, 4j+4) and
-// [64+4j, 64+4j+4) for lane j of the group, so one float4 load instruction of the wave
-// reads 4 rows x 256 contiguous bytes. State traffic is non-temporal: it is streamed
+// Work decomposition. One workgroup = 4 wave64s = one (layer, batch, v-head, Dv tile of
+// 16 x SLOTS rows): 64 rows (SLOTS = 4, 32 KB of fp32 state) when the grid is large, 16
+// rows (SLOTS = 1) when it is small -- a single-layer call, whose 96 tiles of 64 rows
+// would leave most CUs idle. The state is read once and written once per call whatever
+// T is. Each wave owns 4 x SLOTS state rows; inside a wave each 16-lane DPP row owns one
+// state row at a time and a lane holds SLOTS rows ("slots") x 8 fp32 elements: [4j, 4j+4)
+// and [64+4j, 64+4j+4) for lane j of the group, so one float4 load instruction of the
+// wave reads 4 rows x 256 contiguous bytes. State traffic is non-temporal: it is streamed
 // once per step and would only evict the small shared inputs from the caches.
 //
 // q, k, the tile's v rows and the gates of up to 8 steps are staged in LDS by the
@@ -37,14 +39,18 @@ namespace {
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef int i4v __attribute__((ext_vector_type(4)));
 
-// cache-policy operand of the buffer store builtins: bit 4 = sc1 (device scope)
-constexpr int kCachePolicySc1 = 16;
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kTC = 8;         // steps staged in LDS per pass
 
-constexpr int kTileRows = 64;                 // Dv rows per workgroup
-constexpr int kTilesPerHead = kD / kTileRows; // 2
-constexpr int kThreads = 256;                 // 4 waves
-constexpr int kSlots = 4;                     // rows per 16-lane group
-constexpr int kTC = 8;                        // steps staged in LDS per pass
+// Dv tile of 16 x SLOTS rows (SLOTS rows per 16-lane group, 4 groups per wave, 4 waves)
+template <int SLOTS>
+struct Geom {
+  static constexpr int kSlots = SLOTS;
+  static constexpr int kTileRows = 16 * SLOTS;
+  static constexpr int kTilesPerHead = kD / kTileRows;
+};
+constexpr int kBigSlots = 4;    // 64-row tiles
+constexpr int kSmallSlots = 1;  // 16-row tiles
 
 // Butterfly sum over a whole wave64 in the fixed order p[l] += p[l ^ m],
 // m = 1, 2, 4, 8, 16, 32: the l2norm sum order, fixed so that its bf16 rounding is
@@ -92,6 +98,7 @@ struct Tile {
   size_t lb, head;
 };
 
+template <int SLOTS>
 __device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
   int bid = blockIdx.x;
   if (p.remap) {
@@ -99,28 +106,30 @@ __device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
     bid = (bid & 7) * per + (bid >> 3);
   }
   Tile t;
-  t.tile = bid % kTilesPerHead;
-  int rest = bid / kTilesPerHead;
+  t.tile = bid % Geom<SLOTS>::kTilesPerHead;
+  int rest = bid / Geom<SLOTS>::kTilesPerHead;
   t.h = rest % p.Hv;
   rest /= p.Hv;
   t.bb = rest % p.B;
   t.layer = rest / p.B;
   t.g = t.h / p.rep;
-  t.r0 = t.tile * kTileRows;
+  t.r0 = t.tile * Geom<SLOTS>::kTileRows;
   t.lb = (size_t)t.layer * p.B + t.bb;
   t.head = t.lb * p.Hv + t.h;
   return t;
 }
 
-__device__ __forceinline__ int row_of(int wave, int i, int grp) { return wave * 4 * kSlots + i * 4 + grp; }
+template <int SLOTS>
+__device__ __forceinline__ int row_of(int wave, int i, int grp) { return wave * 4 * SLOTS + i * 4 + grp; }
 
+template <int SLOTS>
 __device__ __forceinline__ void load_state(const RecurrentParams& p, const Tile& t, int wave,
-                                           int grp, int j16, f4v (&s)[kSlots][2]) {
+                                           int grp, int j16, f4v (&s)[SLOTS][2]) {
   if (p.state_in) {
     const float* base = p.state_in + t.head * kD * kD;
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int row = t.r0 + row_of(wave, i, grp);
+    for (int i = 0; i < SLOTS; ++i) {
+      const int row = t.r0 + row_of<SLOTS>(wave, i, grp);
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         s[i][hf] = __builtin_nontemporal_load(
@@ -129,52 +138,21 @@ __device__ __forceinline__ void load_state(const RecurrentParams& p, const Tile&
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < SLOTS; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-// State stores come in two cache policies. Non-temporal stores are written back: the
-// lines stay in the L2 of the XCD that wrote them until evicted, and what is still there
-// when the kernel ends is written back after its last wave (the 8 XCDs' L2s are not
-// coherent with each other), which lengthens a launch by up to the L2s' 32 MB at HBM
-// speed. Device-scope stores (sc1) write through instead, at a somewhat lower streaming
-// rate. So the bulk of a large grid writes back and its tail writes through: the
-// workgroups dispatched last (highest block ids) write the final kWtTailBytes of state.
-// Measured on MI355X, 48-layer B=1 decode: 56.0 -> 53.0 us. Small grids (a single-layer
-// decode: 3 MB) write back throughout -- there write-through is slower.
-constexpr unsigned kWtTailBytes = 40u << 20;
-constexpr unsigned kWtTailGroups = kWtTailBytes / (kTileRows * kD * 4);  // 1280 workgroups
-constexpr unsigned kWtMinGroups = 1024;
-// A collecting launch whose whole grid is resident at once (256 CUs x 8 workgroups) writes
-// all its per-step states through (the verify block B = 8, T = 5, 126 MB of per-step
-// states: 32.1 -> 30.5 us); a larger one writes back throughout (through was slower there:
-// the last step through, 4 layers: 122.5 -> 127 us).
-constexpr unsigned kResidentGroups = 2048;
-constexpr unsigned long long kWtMinCollectBytes = 16ull << 20;
-
-// The grid-size conditions are taken on the host (kernels are instantiated with a WT flag,
-// so a grid that never writes through keeps the plain store code and its registers); the
-// tail's per-workgroup test is taken here.
-__device__ __forceinline__ bool tail_write_through() { return blockIdx.x + kWtTailGroups >= gridDim.x; }
-
+// State stores are non-temporal and written back. Writing the grid's last 40 MB through
+// (device scope) instead, or every per-step state of a verify block, measured faster only
+// while the benchmark's rotating state sets partly fitted the 256 MB last-level cache (4
+// sets, 604 MB); with 8 sets (1.2 GB) it made the 48-layer B=1 step slower (53.7 -> 55.5
+// us) and verify no faster, so every store writes back.
+template <int SLOTS>
 __device__ __forceinline__ void store_rows(float* base, const Tile& t, int wave, int grp, int j16,
-                                           const f4v (&s)[kSlots][2], bool write_through) {
-  if (write_through) {
-    // buffer stores with sc1 (device scope); every offset is inside the 64 KB state
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, kD * kD * 4, 0x00020000);
+                                           const f4v (&s)[SLOTS][2]) {
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int row = t.r0 + row_of(wave, i, grp);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4v, s[i][hf]), rs,
-                                               (row * kD + hf * 64 + j16 * 4) * 4, 0, kCachePolicySc1);
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
-    const int row = t.r0 + row_of(wave, i, grp);
+  for (int i = 0; i < SLOTS; ++i) {
+    const int row = t.r0 + row_of<SLOTS>(wave, i, grp);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       __builtin_nontemporal_store(s[i][hf],
@@ -186,11 +164,13 @@ __device__ __forceinline__ void store_rows(float* base, const Tile& t, int wave,
 // The conv state hand-off: rows T..T+2 of [conv_in ; x] for this tile's v channels,
 // plus the q (first tile) or k (second tile) channels of the k-head when h is its
 // k-head's first v-head. Every channel has exactly one writer.
+template <int SLOTS>
 __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const Tile& t,
                                                const uint16_t* x_b, const uint16_t* cin_b) {
+  constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
   const int vbase = 2 * p.Hk * kD + t.h * kD + t.r0;
-  const bool qk_writer = (t.h % p.rep) == 0;
+  const bool qk_writer = (t.h % p.rep) == 0 && t.tile < 2;
   const int qkbase = (t.tile == 0 ? 0 : p.Hk * kD) + t.g * kD;
   const int nch = kTileRows + (qk_writer ? kD : 0);
   for (int e = threadIdx.x; e < nch * kConvRows; e += kThreads) {
@@ -208,19 +188,19 @@ __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const T
   }
 }
 
-template <bool COLLECT, bool WT>
+template <int SLOTS, bool COLLECT>
 __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
                                            float al, float be, const float* kk, const float* qq,
                                            const float* vv, int wave, int grp, int j16,
-                                           f4v (&s)[kSlots][2]) {
+                                           f4v (&s)[SLOTS][2]) {
   const f4v k0 = *reinterpret_cast<const f4v*>(kk + j16 * 4);
   const f4v k1 = *reinterpret_cast<const f4v*>(kk + 64 + j16 * 4);
   const f4v q0 = *reinterpret_cast<const f4v*>(qq + j16 * 4);
   const f4v q1 = *reinterpret_cast<const f4v*>(qq + 64 + j16 * 4);
-  float ov[kSlots];
+  float ov[SLOTS];
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
-    const float vr = vv[row_of(wave, i, grp)];
+  for (int i = 0; i < SLOTS; ++i) {
+    const float vr = vv[row_of<SLOTS>(wave, i, grp)];
     f4v& a0 = s[i][0];
     f4v& a1 = s[i][1];
     float pk = k0.x * a0.x;
@@ -252,14 +232,14 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
     float* dst = p.states_tbh
                      ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
                      : p.states + (t.head * p.T + step) * kD * kD;
-    store_rows(dst, t, wave, grp, j16, s, WT);
+    store_rows<SLOTS>(dst, t, wave, grp, j16, s);
   }
-  // lane j (< kSlots) of each group writes the output of slot j
-  if (j16 < kSlots) {
+  // lane j (< SLOTS) of each group writes the output of slot j
+  if (j16 < SLOTS) {
     float val = ov[0];
 #pragma unroll
-    for (int i = 1; i < kSlots; ++i) val = (j16 == i) ? ov[i] : val;
-    const int row = t.r0 + row_of(wave, j16, grp);
+    for (int i = 1; i < SLOTS; ++i) val = (j16 == i) ? ov[i] : val;
+    const int row = t.r0 + row_of<SLOTS>(wave, j16, grp);
     const size_t oi = ((t.lb * p.T + step) * p.Hv + t.h) * kD + row;
     if (p.o_bf16) {
       static_cast<uint16_t*>(p.o)[oi] = f2bf(val);
@@ -323,24 +303,27 @@ __device__ __forceinline__ float qkv_value(uint32_t raw, int bf16) {
 }
 
 // Front-end channel of a wave in the conv front end: wave 0 -> q channels (lane,
-// lane+64) of k-head g, wave 1 -> k channels, wave 2 -> the tile's v channels.
+// lane+64) of k-head g, wave 1 -> k channels, wave 2 -> the tile's v channels (lanes past
+// the tile's rows repeat its last channel: their values go unused).
+template <int SLOTS>
 __device__ __forceinline__ int fe_channel(const RecurrentParams& p, const Tile& t, int wave,
                                           int lane) {
   return wave == 0 ? t.g * kD + lane
        : wave == 1 ? p.Hk * kD + t.g * kD + lane
-                   : 2 * p.Hk * kD + t.h * kD + t.r0 + lane;
+                   : 2 * p.Hk * kD + t.h * kD + t.r0 + min(lane, Geom<SLOTS>::kTileRows - 1);
 }
 
 // ---------------------------------------------------------------- decode, T = 1
 
-template <int FE, bool WT>
+template <int SLOTS, int FE>
 __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
+  constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   __shared__ float sm_q[kD];
   __shared__ float sm_k[kD];
   __shared__ float sm_v[kTileRows];
   __shared__ float sm_ab[2];
 
-  const Tile t = decode_block(p);
+  const Tile t = decode_block<SLOTS>(p);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4, j16 = lane & 15;
@@ -358,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
     const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
     // Every wave issues the same loads (no branch, so nothing waits on them early);
     // waves 2 and 3 read their one channel twice, wave 3's values go unused.
-    c0 = fe_channel(p, t, wave < 3 ? wave : 2, lane);
+    c0 = fe_channel<SLOTS>(p, t, wave < 3 ? wave : 2, lane);
     const int c1 = wave < 2 ? c0 + 64 : c0;
 #pragma unroll
     for (int j = 0; j < kTaps; ++j) {
@@ -373,8 +356,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
     if (tid < kTileRows) v_raw = qkv_raw(p.v, (row0 * p.Hv + t.h) * kD + t.r0 + tid, p.qkv_bf16);
   }
   // 2. the tile's state; then the gate inputs, which only wave 3 waits for
-  f4v s[kSlots][2];
-  load_state(p, t, wave, grp, j16, s);
+  f4v s[SLOTS][2];
+  load_state<SLOTS>(p, t, wave, grp, j16, s);
   GateRaw gr;
   if (wave == 3) gr = gate_load(p, t.layer, t.h, row0 * p.Hv + t.h);
   __builtin_amdgcn_sched_barrier(0);  // keep the front-end arithmetic below the loads
@@ -399,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
         float* dst = wave == 0 ? sm_q : sm_k;
         dst[lane] = y0;
         dst[lane + 64] = y1;
-      } else {
+      } else if (lane < kTileRows) {
         sm_v[lane] = u[0];
       }
     }
@@ -420,8 +403,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   __syncthreads();
 
   // 4. the step, then the state goes back
-  apply_step<false, false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
-  if (p.state_out) store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s, WT && tail_write_through());
+  apply_step<SLOTS, false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
+  if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
 
   // 5. conv state hand-off from the rows already in registers: new rows 0..2 are xp
   // rows 1..3. This tile's v channels; the q (tile 0) or k (tile 1) channels of the
@@ -429,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   if (FE == 1 && p.conv_out) {
     uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
     const bool qk_writer = (t.h % p.rep) == 0 && wave == t.tile;
-    const int nm = wave == 2 ? 1 : (wave < 2 && qk_writer ? 2 : 0);
+    const int nm = wave == 2 ? (lane < kTileRows ? 1 : 0) : (wave < 2 && qk_writer ? 2 : 0);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       if (m < nm) {
@@ -445,15 +428,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
 
 // ---------------------------------------------------------------- any T (verify, prefill-size L)
 
-template <int FE, bool COLLECT, bool WT>
+template <int SLOTS, int FE, bool COLLECT>
 __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
+  constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   __shared__ float sm_q[kTC][kD];
   __shared__ float sm_k[kTC][kD];
   __shared__ float sm_v[kTC][kTileRows];
   __shared__ float sm_a[kTC];
   __shared__ float sm_b[kTC];
 
-  const Tile t = decode_block(p);
+  const Tile t = decode_block<SLOTS>(p);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4, j16 = lane & 15;
@@ -469,11 +453,11 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     x_b = p.x + t.lb * (size_t)T * p.C;
     cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
     w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
-    c0 = fe_channel(p, t, wave, lane);
+    c0 = fe_channel<SLOTS>(p, t, wave, lane);
   }
   const int nm = wave < 2 ? 2 : 1;  // conv channels per lane (waves 0..2)
 
-  f4v s[kSlots][2];
+  f4v s[SLOTS][2];
   for (int t0 = 0; t0 < T; t0 += kTC) {
     const int tc = min(kTC, T - t0);
     if (t0 > 0) __syncthreads();  // the previous pass is done reading LDS
@@ -500,7 +484,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     const int gt = tid - (kThreads - kTC);  // the last 8 threads: one step each
     if (gt >= 0 && gt < tc) gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gt)) * p.Hv + t.h);
 
-    if (t0 == 0) load_state(p, t, wave, grp, j16, s);
+    if (t0 == 0) load_state<SLOTS>(p, t, wave, grp, j16, s);
 
     if (FE == 0) {
       const int per = 2 * kD + kTileRows;
@@ -543,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
             float* dst = wave == 0 ? sm_q[tt] : sm_k[tt];
             dst[lane] = y0;
             dst[lane + 64] = y1;
-          } else {
+          } else if (lane < kTileRows) {
             sm_v[tt][lane] = u[0];
           }
         }
@@ -553,15 +537,13 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     __syncthreads();
 
     for (int tt = 0; tt < tc; ++tt) {
-      apply_step<COLLECT, WT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave,
-                          grp, j16, s);
+      apply_step<SLOTS, COLLECT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave, grp,
+                                 j16, s);
     }
   }
 
-  if (p.state_out)
-    store_rows(p.state_out + t.head * kD * kD, t, wave, grp, j16, s,
-               WT && (COLLECT || tail_write_through()));
-  if (FE == 1 && p.conv_out) write_conv_out(p, t, x_b, cin_b);
+  if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+  if (FE == 1 && p.conv_out) write_conv_out<SLOTS>(p, t, x_b, cin_b);
 }
 
 __global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t n) {
@@ -579,40 +561,43 @@ __global__ void copy_u16_kernel(uint16_t* __restrict__ dst, const uint16_t* __re
   }
 }
 
+// The 16-row tiles serve grids whose 64-row form would be small: up to this many
+// (layer, batch, v-head) units, i.e. at most 2 x kSmallTileMaxHeads 64-row workgroups.
+#ifndef GDN_SMALL_TILE_MAX_HEADS
+#define GDN_SMALL_TILE_MAX_HEADS 96
+#endif
+constexpr long long kSmallTileMaxHeads = GDN_SMALL_TILE_MAX_HEADS;
+
+template <int SLOTS, int FE>
+void launch_steps(const RecurrentParams& p, bool collect, dim3 grid, dim3 block, hipStream_t stream) {
+  if (collect) hipLaunchKernelGGL((steps_kernel<SLOTS, FE, true>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((steps_kernel<SLOTS, FE, false>), grid, block, 0, stream, p);
+}
+
+template <int SLOTS>
+void launch_slots(const RecurrentParams& p, int frontend, bool collect, hipStream_t stream) {
+  const dim3 grid(p.nblocks), block(kThreads);
+  if (p.T == 1 && !collect) {
+    if (frontend == 0) hipLaunchKernelGGL((decode_kernel<SLOTS, 0>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((decode_kernel<SLOTS, 1>), grid, block, 0, stream, p);
+  } else if (frontend == 0) {
+    launch_steps<SLOTS, 0>(p, collect, grid, block, stream);
+  } else {
+    launch_steps<SLOTS, 1>(p, collect, grid, block, stream);
+  }
+}
+
 }  // namespace
 
-template <int FE>
-static void launch_steps(const RecurrentParams& p, bool collect, bool wt, dim3 grid, dim3 block, hipStream_t stream) {
-  if (collect) {
-    if (wt) hipLaunchKernelGGL((steps_kernel<FE, true, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((steps_kernel<FE, true, false>), grid, block, 0, stream, p);
-  } else {
-    if (wt) hipLaunchKernelGGL((steps_kernel<FE, false, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((steps_kernel<FE, false, false>), grid, block, 0, stream, p);
-  }
+int recurrent_tile_rows(long long heads) {
+  return heads <= kSmallTileMaxHeads ? Geom<kSmallSlots>::kTileRows : Geom<kBigSlots>::kTileRows;
 }
 
 hipError_t launch_recurrent(const RecurrentParams& p, int frontend, bool collect,
                             hipStream_t stream) {
-  const dim3 grid(p.nblocks), block(kThreads);
-  // write-through: a large grid's tail, or every per-step state of a collecting launch that
-  // is resident at once and writes enough of them
-  const bool wt = collect ? (unsigned long long)p.nblocks * p.T * (kTileRows * kD * 4) >= kWtMinCollectBytes &&
-                                p.nblocks <= (int)kResidentGroups
-                          : p.nblocks >= (int)kWtMinGroups;
-  if (p.T == 1 && !collect) {
-    if (frontend == 0) {
-      if (wt) hipLaunchKernelGGL((decode_kernel<0, true>), grid, block, 0, stream, p);
-      else hipLaunchKernelGGL((decode_kernel<0, false>), grid, block, 0, stream, p);
-    } else {
-      if (wt) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, 0, stream, p);
-      else hipLaunchKernelGGL((decode_kernel<1, false>), grid, block, 0, stream, p);
-    }
-  } else if (frontend == 0) {
-    launch_steps<0>(p, collect, wt, grid, block, stream);
-  } else {
-    launch_steps<1>(p, collect, wt, grid, block, stream);
-  }
+  const long long heads = (long long)p.n_layers * p.B * p.Hv;
+  if (recurrent_tile_rows(heads) == Geom<kSmallSlots>::kTileRows) launch_slots<kSmallSlots>(p, frontend, collect, stream);
+  else launch_slots<kBigSlots>(p, frontend, collect, stream);
   return hipGetLastError();
 }
 
@@ -629,7 +614,5 @@ hipError_t launch_copy_u16(uint16_t* dst, const uint16_t* src, int64_t n, hipStr
   hipLaunchKernelGGL(copy_u16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, dst, src, n);
   return hipGetLastError();
 }
-
-int recurrent_tile_rows() { return kTileRows; }
 
 }  // namespace gdn

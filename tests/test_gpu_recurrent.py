@@ -131,6 +131,41 @@ def test_decode_48_layers_conv(O, gdn, dev):
     assert worst <= STATE_TOL
 
 
+def _concat_batches(O, a, b):
+    """The sequences of a followed by those of b, as one batch (same layer weights: a's)."""
+    cat = lambda u, v: None if u is None else np.ascontiguousarray(np.concatenate([u, v], axis=0))  # noqa: E731
+    return O.LayerInputs(None, None, None, cat(a.x, b.x), a.conv_w, cat(a.conv_state, b.conv_state),
+                         cat(a.a, b.a), cat(a.b, b.b), a.A_log, a.dt_bias, cat(a.state, b.state))
+
+
+@pytest.mark.parametrize("B,T", [(1, 1), (2, 1), (1, 5), (2, 5)])
+def test_small_tiles_one_layer_conv(O, gdn, dev, B, T):
+    """The reference's per-layer call shape (model.cpp:622-624) at B <= 2: at most 96
+    (layer, batch, v-head) units, which run on 16-row Dv tiles (8 workgroups per v-head)
+    instead of 64-row ones. Against the oracle (state, o, conv hand-off; with T = 5 also
+    every per-step state of a recording call), and bit for bit against the 64-row tiles
+    that the same sequences get inside a batch of B + 2 (more than 96 units)."""
+    log_case(f"16-row tiles: one layer B={B} T={T} conv")
+    inp = O.make_inputs(config=1 if T == 1 else 3, layer=40 + 10 * B + T, B=B, L=T, conv=True)
+    extra = O.make_inputs(config=1 if T == 1 else 3, layer=90 + 10 * B + T, B=2, L=T, conv=True)
+    ref = O.reference_layer(inp, collect=T > 1)
+    out = run_layers(gdn, dev, [inp], o_dtype="bf16")
+    check_state(O, out["state"][0], ref["state"], "state")
+    check_o(O, out["o"][0], ref["o"], "bf16", "o")
+    assert np.array_equal(out["conv"][0], ref["xp"][:, -3:]), "conv state hand-off"
+    big = run_layers(gdn, dev, [_concat_batches(O, inp, extra)], o_dtype="bf16")
+    assert np.array_equal(big["state"][0][:B], out["state"][0]), "16-row vs 64-row tiles: state"
+    assert np.array_equal(big["o"][0][:B], out["o"][0]), "16-row vs 64-row tiles: o"
+    assert np.array_equal(big["conv"][0][:B], out["conv"][0]), "16-row vs 64-row tiles: conv"
+    if T > 1:
+        rec = run_layers(gdn, dev, [inp], o_dtype="bf16", collect=True, conv_out=False)
+        for t in range(T):
+            check_state(O, rec["states"][0][:, :, t], ref["states"][:, :, t], f"step {t} state")
+        rec_big = run_layers(gdn, dev, [_concat_batches(O, inp, extra)], o_dtype="bf16", collect=True,
+                             conv_out=False)
+        assert np.array_equal(rec_big["states"][0][:B], rec["states"][0]), "16-row vs 64-row tiles: states"
+
+
 def test_decode_frontend_is_bit_exact(O, gdn, dev):
     """With a zero state and beta from the gates, o = beta v (k.q): the front end's bf16
     q,k,v must round exactly as the oracle's (checked through a zero-state step)."""
