@@ -226,6 +226,40 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
                 hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9)
 
 
+def bench_crossover(torch, gdn, dev, timer, steps: int, warmup: int, Ts=(16, 32, 64, 128, 256, 512, 1024),
+                    Bs=(1, 4)):
+    """One layer with the conv front end over T tokens, B sequences: the recurrent kernel
+    (gdn_run, serial in T) against the chunked prefill (gdn_prefill_chunked), us per call.
+    The crossover is where a non-recording call switches forms (the reference makes the same
+    choice by length, python/qwen35.py:606-626)."""
+    out = {}
+    for B in Bs:
+        for T in Ts:
+            i = make_layer_inputs(torch, dev, 1, B, T, True, seed=800 + T + B)
+            x = i["x"][0].contiguous()
+            cw = i["conv_weight"][0].contiguous()
+            a, b = i["a"][0].contiguous(), i["b"][0].contiguous()
+            A_log, dt_bias = i["A_log"][0].contiguous(), i["dt_bias"][0].contiguous()
+            state = torch.randn((B, HV, D, D), device=dev) * 0.02
+            o = torch.empty((B, T, HV, D), dtype=torch.bfloat16, device=dev)
+            conv_out = torch.empty((B, 3, C), dtype=torch.bfloat16, device=dev)
+            st_out = torch.empty_like(state)
+            ws = torch.empty(gdn.prefill_workspace_size(B, T), dtype=torch.uint8, device=dev)
+            common = dict(B=B, T=T, x=x, conv_weight=cw, conv_state_in=i["conv_state"][0].contiguous(),
+                          conv_state_out=conv_out, a=a, b=b, A_log=A_log, dt_bias=dt_bias, state_in=state,
+                          state_out=st_out, o=o)
+            rec = gdn.layer_args(**common)
+            chk = gdn.layer_args(**common, workspace=ws)
+            n = max(5, steps // 4)
+            r1 = timer.time_calls(lambda it: gdn.call_run(rec), n, warmup, host_us_per_call=80.0)
+            r2 = timer.time_calls(lambda it: gdn.call_prefill(chk), n, warmup, host_us_per_call=80.0)
+            out[f"B{B}_T{T}"] = dict(recurrent_us=round(r1["ms_per_step"] * 1e3, 1),
+                                     chunked_us=round(r2["ms_per_step"] * 1e3, 1))
+            print(f"# crossover B={B} T={T}: recurrent {r1['ms_per_step'] * 1e3:.1f} us, "
+                  f"chunked {r2['ms_per_step'] * 1e3:.1f} us", flush=True)
+    return out
+
+
 def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str, M: int = 1):
     """48 layers of the DeltaNet projections for M operand rows in one launch (M = 1: B=1
     decode, the GEMV kernel; M = 40: a B=8, T=5 verify block, the MFMA kernel): "in_proj" =
@@ -347,7 +381,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="comma list: decode1,decode1layer,decode32,verify,prefill,in_proj,"
-                         "out_proj,in_proj40,out_proj40,copy")
+                         "out_proj,in_proj40,out_proj40,copy; crossover runs only when named")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the gated-delta path "
@@ -422,6 +456,8 @@ def main() -> int:
             sec[f"{which}_48_layers_m40"] = r
             print(f"# {which} x48 M=40 (4-bit, MFMA): {r['us_per_step']:.1f} us/step, {r['GBps']:.0f} GB/s, "
                   f"{r['TFLOPs']:.1f} TFLOP/s", flush=True)
+    if "crossover" in only:
+        sec["crossover_recurrent_vs_chunked"] = bench_crossover(torch, gdn, dev, timer, args.steps, 3)
     if want("copy"):
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)

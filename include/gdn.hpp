@@ -43,6 +43,12 @@ inline void check_hip(hipError_t e, const char* what) {
 
 inline bool available() { return gdn_available() != 0; }
 
+// Blocks that are not recorded and carry at least this many tokens run the chunked form
+// (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet near T = 20 on MI355X
+// (one layer, conv front end, B = 1 and 4). The reference chooses by length the same way
+// (python/qwen35.py:338, 606-626).
+constexpr int kChunkedMinT = 20;
+
 // delta::run (delta.hpp:66-68) on device buffers: q, k (B,L,H,128), v (B,L,H,128), alpha,
 // beta (B,L,H), all fp32, head-expanded as the reference passes them; S (B,H,128,128) or
 // nullptr for zeros. Writes o (B,L,H,128) fp32, s_out and, when states != nullptr, the
@@ -93,8 +99,12 @@ class DeltaCache {
   // Recorded blocks go to two buffers of max_record_steps states each, (T, B, Hv) order,
   // used in turn: commit(n) adopts step n-1 of the block by pointer (no copy), and the
   // next block is recorded into the other buffer, which no longer holds the live state.
-  DeltaCache(const LayerParams& p, int batch, int max_record_steps)
-      : p_(p), B_(batch), max_T_(max_record_steps) {
+  // Blocks of kChunkedMinT .. max_prefill_tokens tokens (the reference prefills in windows of
+  // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here;
+  // max_prefill_tokens = 0 keeps every block on the recurrent kernel.
+  DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0)
+      : p_(p), B_(batch), max_T_(max_record_steps),
+        max_prefill_T_(max_prefill_tokens >= kChunkedMinT ? max_prefill_tokens : 0) {
     const size_t D = GDN_HEAD_DIM;
     state_bytes_ = (size_t)B_ * p_.num_v_heads * D * D * sizeof(float);
     conv_bytes_ = (size_t)B_ * (GDN_CONV_TAPS - 1) * p_.conv_dim() * 2;
@@ -103,6 +113,16 @@ class DeltaCache {
     check_hip(hipMalloc(&conv_spare_, conv_bytes_), "hipMalloc conv");
     for (float*& r : rec_)
       if (max_T_ > 0) check_hip(hipMalloc(&r, state_bytes_ * max_T_), "hipMalloc states");
+    if (max_prefill_T_ > 0) {
+      gdn_layer_args w{};
+      w.batch = B_;
+      w.seq_len = max_prefill_T_;
+      w.num_k_heads = p_.num_k_heads;
+      w.num_v_heads = p_.num_v_heads;
+      w.frontend = GDN_FRONTEND_CONV;
+      check(gdn_prefill_workspace_size(&w, &ws_bytes_));
+      check_hip(hipMalloc(&ws_, ws_bytes_), "hipMalloc prefill workspace");
+    }
     check_hip(hipMemset(own_state_, 0, state_bytes_), "hipMemset");
     check_hip(hipMemset(conv_, 0, conv_bytes_), "hipMemset");
     state_ = own_state_;
@@ -115,6 +135,7 @@ class DeltaCache {
     (void)hipFree(conv_spare_);
     for (float* r : rec_)
       if (r) (void)hipFree(r);
+    if (ws_) (void)hipFree(ws_);
   }
 
   int offset = 0;
@@ -130,7 +151,8 @@ class DeltaCache {
   // GatedDeltaNet::operator() from the in_proj outputs to o (model.cpp:585-638):
   // x (B,T,C) bf16 = in_proj_qkv(x), a, b (B,T,Hv) bf16 = in_proj_a/b(x); o (B,T,Hv,128)
   // bf16. In record mode the state is not advanced and every per-step state is kept for
-  // commit(); x must then stay valid until commit().
+  // commit(); x must then stay valid until commit(). A block that is not recorded and has
+  // kChunkedMinT .. max_prefill_tokens tokens (x and o 16-byte aligned) runs the chunked form.
   void step(const void* x, const void* a, const void* b, int T, void* o, hipStream_t stream) {
     gdn_layer_args g{};
     g.n_layers = 1;
@@ -163,7 +185,14 @@ class DeltaCache {
     } else {
       g.conv_state_out = conv_spare_;
       g.state_out = state_;
-      check(gdn_run(&g));
+      const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(o)) % 16 == 0;
+      if (T >= kChunkedMinT && T <= max_prefill_T_ && aligned) {
+        g.workspace = ws_;
+        g.workspace_bytes = ws_bytes_;
+        check(gdn_prefill_chunked(&g));
+      } else {
+        check(gdn_run(&g));
+      }
       std::swap(conv_, conv_spare_);
       offset += T;
     }
@@ -202,7 +231,9 @@ class DeltaCache {
   LayerParams p_;
   int B_;
   int max_T_;
-  size_t state_bytes_ = 0, conv_bytes_ = 0;
+  int max_prefill_T_;
+  size_t state_bytes_ = 0, conv_bytes_ = 0, ws_bytes_ = 0;
+  void* ws_ = nullptr;
   bool holds_state(const float* rec) const {
     const uintptr_t s = reinterpret_cast<uintptr_t>(state_), r = reinterpret_cast<uintptr_t>(rec);
     return rec && s >= r && s < r + state_bytes_ * (size_t)max_T_;

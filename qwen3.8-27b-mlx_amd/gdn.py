@@ -31,6 +31,15 @@ STATES_BHT, STATES_TBH = 0, 1
 HEAD_DIM = 128
 CONV_TAPS = 4
 
+# Calls that do not record and carry at least this many tokens run the chunked form
+# (gdn_prefill_chunked); shorter ones the recurrent kernel (gdn_run), serial in T. Measured on
+# MI355X with one layer and the conv front end (bench.py --only crossover): at B = 1 the
+# recurrent kernel takes 25 us at T = 16 and 46 us at T = 32, the chunked form 31 us at both;
+# at B = 4, 37 / 69 against 46 us -- they meet near T = 20 either way. Module-level so that
+# tests can force either form, as the reference's CHUNK_THRESHOLD (python/qwen35.py:338,
+# 606-626), which makes the same choice by length.
+CHUNKED_MIN_T = 20
+
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
 QLINEAR_MAX_ROWS = 512
@@ -274,13 +283,25 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
         stream=_stream(stream))
 
 
+def _use_chunked(T: int, record: bool, x, q, tensors) -> bool:
+    """The length-based choice of the form (CHUNKED_MIN_T), for calls the chunked form takes:
+    not recording, bf16 q, k, v when given, 16-byte aligned inputs."""
+    import torch
+    if record or T < CHUNKED_MIN_T:
+        return False
+    if x is None and q.dtype != torch.bfloat16:
+        return False
+    return all(t is None or t.data_ptr() % 16 == 0 for t in tensors)
+
+
 def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
           conv_weight=None, conv_state=None, collect: bool = False, in_place: bool = True,
           o_dtype=None, Hk: int = 16, stream=None):
     """The per-layer call of GatedDeltaNet::operator() (cpp/src/model.cpp:585-641) at the
     recurrence: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
     (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
-    v (B,T,Hv,128). Returns dict(o, state, states, conv_state)."""
+    v (B,T,Hv,128). Returns dict(o, state, states, conv_state). A call that does not record
+    and has at least CHUNKED_MIN_T tokens runs the chunked form (python/qwen35.py:606-626)."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
@@ -299,11 +320,14 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     conv_out = None
     if x is not None and not record:
         conv_out = torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
+    chunked = _use_chunked(T, record, x, q, (x, conv_state, q, k, v))
+    ws = (torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None), dtype=torch.uint8,
+                      device=dev) if chunked else None)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
                       A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out,
-                      states=states, o=o, stream=stream)
-    call_run(args)
+                      states=states, o=o, workspace=ws, stream=stream)
+    (call_prefill if chunked else call_run)(args)
     return dict(o=o, state=state_out, states=states, conv_state=conv_out)
 
 
@@ -370,7 +394,8 @@ class DeltaCache:
         self.pending = None
 
     def step(self, x, conv_weight, a, b, A_log, dt_bias, o_dtype=None, stream=None):
-        """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache."""
+        """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache; a block of at
+        least CHUNKED_MIN_T tokens that is not recorded runs the chunked form."""
         import torch
         B, T = x.shape[0], x.shape[1]
         o = torch.empty((B, T, self.Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16,
@@ -386,11 +411,14 @@ class DeltaCache:
             self.base_offset = self.offset
             self.pending = (x, states, T)
         else:
+            chunked = _use_chunked(T, False, x, None, (x,))
+            ws = (torch.empty(prefill_workspace_size(B, T, self.Hk, self.Hv), dtype=torch.uint8,
+                              device=x.device) if chunked else None)
             args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,
                               conv_state_in=self.conv, conv_state_out=self._conv_spare, a=a,
                               b=b, A_log=A_log, dt_bias=dt_bias, state_in=self.state,
-                              state_out=self.state, o=o, stream=stream)
-            call_run(args)
+                              state_out=self.state, o=o, workspace=ws, stream=stream)
+            (call_prefill if chunked else call_run)(args)
             self.conv, self._conv_spare = self._conv_spare, self.conv
             self.offset += T
         return o

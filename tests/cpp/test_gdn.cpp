@@ -194,6 +194,53 @@ void test_cache() {
   check(threw, "commit out of range throws (model.cpp:443)");
 }
 
+// A block of kChunkedMinT .. max_prefill_tokens tokens runs the chunked form
+// (python/qwen35.py:606-626 chooses by length the same way): against a cache without a
+// prefill workspace, which runs the same block on the recurrent kernel, within the chunked
+// form's tolerance (1e-2); the conv window is exact in both forms.
+void test_cache_chunked() {
+  printf("\nDeltaCache: long block on the chunked form\n");
+  const int B = 2, Hk = 16, Hv = 48, C = 2 * Hk * 128 + Hv * 128, T = 40;
+  std::vector<uint16_t> w(4 * C), x((size_t)B * T * C), a((size_t)B * T * Hv), b((size_t)B * T * Hv);
+  gdno_round_bf16(normal(21, w.size(), 0.1f).data(), w.data(), (int64_t)w.size());
+  gdno_round_bf16(normal(22, x.size()).data(), x.data(), (int64_t)x.size());
+  gdno_round_bf16(normal(23, a.size()).data(), a.data(), (int64_t)a.size());
+  gdno_round_bf16(normal(24, b.size()).data(), b.data(), (int64_t)b.size());
+  std::vector<float> A_log(Hv), dt = normal(26, Hv, 0.1f);
+  gdno_fill_uniform(25, -1.0f, 1.0f, A_log.data(), Hv);
+  uint16_t *dw = to_dev(w), *dx = to_dev(x), *da = to_dev(a), *db = to_dev(b);
+  float *dA = to_dev(A_log), *ddt = to_dev(dt);
+  gdn::LayerParams p;
+  p.conv_weight = dw;
+  p.A_log = dA;
+  p.dt_bias = ddt;
+  uint16_t *o1, *o2;
+  gdn::check_hip(hipMalloc(&o1, (size_t)B * T * Hv * 128 * 2), "hipMalloc");
+  gdn::check_hip(hipMalloc(&o2, (size_t)B * T * Hv * 128 * 2), "hipMalloc");
+  gdn::DeltaCache chunked(p, B, 0, 1024), recurrent(p, B, 0);
+  chunked.step(dx, da, db, T, o1, nullptr);
+  recurrent.step(dx, da, db, T, o2, nullptr);
+  gdn::check_hip(hipDeviceSynchronize(), "sync");
+  const auto s1 = to_host(chunked.state(), chunked.state_bytes() / 4);
+  const auto s2 = to_host(recurrent.state(), recurrent.state_bytes() / 4);
+  const auto c1 = to_host((const uint16_t*)chunked.conv(), chunked.conv_bytes() / 2);
+  const auto c2 = to_host((const uint16_t*)recurrent.conv(), recurrent.conv_bytes() / 2);
+  const auto h1 = to_host(o1, (size_t)B * T * Hv * 128), h2 = to_host(o2, (size_t)B * T * Hv * 128);
+  std::vector<float> f1(h1.size()), f2(h2.size());
+  for (size_t i = 0; i < h1.size(); ++i) {
+    uint32_t u1 = (uint32_t)h1[i] << 16, u2 = (uint32_t)h2[i] << 16;
+    memcpy(&f1[i], &u1, 4);
+    memcpy(&f2[i], &u2, 4);
+  }
+  const float es = rel_err(s1, s2), eo = rel_err(f1, f2);
+  char buf[200];
+  snprintf(buf, sizeof(buf), "T=%d block: chunked vs recurrent state %.2e, o %.2e (<= 1e-2), conv window exact",
+           T, es, eo);
+  check(es <= 1e-2f && eo <= 1e-2f && c1 == c2 && chunked.offset == T, buf);
+  for (void* ptr : {(void*)dw, (void*)dx, (void*)da, (void*)db, (void*)dA, (void*)ddt, (void*)o1, (void*)o2})
+    (void)hipFree(ptr);
+}
+
 }  // namespace
 
 // gdn::linears (the layer's four in_proj matrices on one x) and gdn::norm_out_proj vs the
@@ -332,6 +379,7 @@ int main() {
   try {
     test_delta();
     test_cache();
+    test_cache_chunked();
     test_qlinear();
   } catch (const std::exception& e) {
     printf("  [FAIL] exception: %s\n", e.what());

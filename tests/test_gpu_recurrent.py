@@ -422,6 +422,59 @@ def test_deltacache_spec_equals_plain(O, gdn, dev):
         assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
 
 
+def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
+    """A block of at least CHUNKED_MIN_T tokens that is not recorded runs the chunked form
+    (python/qwen35.py:606-626 makes the same choice by length): a 100-token prefill through
+    DeltaCache.step and then one decode step, against the oracle's token-by-token recurrence
+    at the chunked form's tolerance (1e-2, the prefill tests'); the same calls with the
+    threshold raised run the recurrent kernel, at the recurrent tolerance (1e-4)."""
+    import torch
+    mod = gdn.gdn
+    calls = []
+    orig = mod.call_prefill
+    monkeypatch.setattr(mod, "call_prefill", lambda args: (calls.append(args.seq_len), orig(args))[1])
+    B, T = 2, 100
+    inp = O.make_inputs(config=4, layer=7, B=B, L=T + 1, conv=True)
+    ref = O.reference_layer(inp)
+    pre = O.reference_layer(O.LayerInputs(None, None, None, np.ascontiguousarray(inp.x[:, :T]), inp.conv_w,
+                                          inp.conv_state, np.ascontiguousarray(inp.a[:, :T]),
+                                          np.ascontiguousarray(inp.b[:, :T]), inp.A_log, inp.dt_bias, inp.state))
+    for threshold, tol in ((mod.CHUNKED_MIN_T, 1e-2), (10 ** 9, 1e-4)):
+        monkeypatch.setattr(mod, "CHUNKED_MIN_T", threshold)
+        calls.clear()
+        log_case(f"length dispatch: T={T} block then 1 token, threshold {threshold}")
+        c = gdn.DeltaCache(B, device=dev)
+        c.state.copy_(to_dev(inp.state, dev))
+        c.conv.copy_(to_dev(inp.conv_state, dev))
+        w, Al, dt = to_dev(inp.conv_w, dev), to_dev(inp.A_log, dev), to_dev(inp.dt_bias, dev)
+        x, a, b = to_dev(inp.x, dev), to_dev(inp.a, dev), to_dev(inp.b, dev)
+        o1 = c.step(x[:, :T].contiguous(), w, a[:, :T].contiguous(), b[:, :T].contiguous(), Al, dt,
+                    o_dtype=torch.float32)
+        torch.cuda.synchronize()
+        e_o, e_s = O.rel_err(to_np(o1), pre["o"]), O.rel_err(to_np(c.state), pre["state"])
+        o2 = c.step(x[:, T:].contiguous(), w, a[:, T:].contiguous(), b[:, T:].contiguous(), Al, dt,
+                    o_dtype=torch.float32)
+        torch.cuda.synchronize()
+        e_o2, e_s2 = O.rel_err(to_np(o2), ref["o"][:, T:]), O.rel_err(to_np(c.state), ref["state"])
+        print(f"  prefill o {e_o:.2e} state {e_s:.2e}; next token o {e_o2:.2e} state {e_s2:.2e}; "
+              f"chunked calls {calls}", flush=True)
+        assert calls == ([T] if threshold <= T else [])
+        assert max(e_o, e_s, e_o2, e_s2) <= tol
+        assert np.array_equal(to_np(c.conv), ref["xp"][:, -3:])
+    # layer() with q, k, v given (bf16) takes the same choice
+    monkeypatch.setattr(mod, "CHUNKED_MIN_T", 20)
+    calls.clear()
+    qi = O.make_inputs(config=4, layer=8, B=1, L=64)
+    qref = O.reference_layer(qi)
+    out = gdn.layer(q=to_dev(qi.q, dev), k=to_dev(qi.k, dev), v=to_dev(qi.v, dev), a=to_dev(qi.a, dev),
+                    b=to_dev(qi.b, dev), A_log=to_dev(qi.A_log, dev), dt_bias=to_dev(qi.dt_bias, dev),
+                    state=to_dev(qi.state, dev), o_dtype=torch.float32)
+    torch.cuda.synchronize()
+    eo, es = O.rel_err(to_np(out["o"]), qref["o"]), O.rel_err(to_np(out["state"]), qref["state"])
+    print(f"  layer() qkv T=64: o {eo:.2e} state {es:.2e}, chunked calls {calls}", flush=True)
+    assert calls == [64] and max(eo, es) <= 1e-2
+
+
 def test_gpu_rejects_bad_arguments_without_launching(gdn, dev):
     import torch
     log_case("argument errors on the GPU path")
