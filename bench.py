@@ -260,13 +260,13 @@ def bench_crossover(torch, gdn, dev, timer, steps: int, warmup: int, Ts=(16, 32,
     return out
 
 
-def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str, M: int = 1):
-    """48 layers of the DeltaNet projections for M operand rows in one launch (M = 1: B=1
-    decode, the GEMV kernel; M = 40: a B=8, T=5 verify block, the MFMA kernel): "in_proj" =
-    in_proj_qkv, in_proj_z, in_proj_a, in_proj_b on x (5120); "out_proj" = GatedRMSNorm of
-    o (6144, fp32) with z, then out_proj (5120 rows). Synthetic 4-bit weights (random
-    words, scales and biases in the checkpoint's ranges)."""
-    NL = 48
+def bench_qlinear(torch, gdn, dev, timer, steps: int, warmup: int, which: str, M: int = 1, NL: int = 48):
+    """NL layers (48: a model's DeltaNet layers) of the projections for M operand rows in one
+    launch (M = 1: B=1 decode, the GEMV kernel; M = 40: a B=8, T=5 verify block, and M = 1024
+    with NL = 1: one layer's prefill window, the MFMA kernel): "in_proj" = in_proj_qkv,
+    in_proj_z, in_proj_a, in_proj_b on x (5120); "out_proj" = GatedRMSNorm of o (6144, fp32)
+    with z, then out_proj (5120 rows). Synthetic 4-bit weights (random words, scales and
+    biases in the checkpoint's ranges)."""
     g = torch.Generator(device=dev)
     g.manual_seed(700 if which == "in_proj" else 701)
 
@@ -381,7 +381,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
                     help="comma list: decode1,decode1layer,decode32,verify,prefill,in_proj,"
-                         "out_proj,in_proj40,out_proj40,copy; crossover runs only when named")
+                         "out_proj,in_proj40,out_proj40,in_proj1024,out_proj1024,copy; crossover runs "
+                         "only when named")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the gated-delta path "
@@ -451,6 +452,12 @@ def main() -> int:
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)
             sec[f"{which}_48_layers_b1"] = r
             print(f"# {which} x48 B=1 (4-bit): {r['us_per_step']:.1f} us/step, {r['GBps']:.0f} GB/s", flush=True)
+        if want(which + "1024"):
+            r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 8), warmup=3, which=which, M=1024,
+                              NL=1)
+            sec[f"{which}_1_layer_m1024"] = r
+            print(f"# {which} x1 M=1024 (4-bit, MFMA): {r['us_per_step']:.1f} us/step, {r['TFLOPs']:.1f} TFLOP/s, "
+                  f"{r['GBps']:.0f} GB/s", flush=True)
         if want(which + "40"):
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 8), warmup=3, which=which, M=40)
             sec[f"{which}_48_layers_m40"] = r

@@ -182,12 +182,14 @@ int gdn_commit(const gdn_commit_args* args);
  * (model.cpp:350-354, 626-627), bf16(rmsnorm(norm_x) * norm_gamma * silu(norm_z)) over
  * each 128-value head, so norm + out_proj (model.cpp:641) is one call.
  * Up to GDN_QLINEAR_GEMV_ROWS operand rows (decode) the call needs no workspace; more
- * rows (verify blocks, batched decode: up to GDN_QLINEAR_MAX_ROWS, the range the reference
- * keeps quantized_matmul for, model.hpp:137) run on MFMA and take a workspace of
+ * rows (verify blocks, batched decode, and prefill windows: the reference keeps
+ * quantized_matmul below 512 rows and dequantizes and multiplies above, model.hpp:137,
+ * model.cpp:358-362, in windows of 1024 tokens, session.hpp:136) run on MFMA with the same
+ * exact arithmetic at every row count, up to GDN_QLINEAR_MAX_ROWS, and take a workspace of
  * gdn_qlinear_workspace_size() bytes for the operand in MFMA fragment order. */
 #define GDN_QLINEAR_MAX_SEGS 4
 #define GDN_QLINEAR_GEMV_ROWS 4
-#define GDN_QLINEAR_MAX_ROWS 512
+#define GDN_QLINEAR_MAX_ROWS 4096
 
 typedef struct gdn_qlinear_seg {
   const void* w;      /* (N, K/8) uint32, 16-byte aligned */
@@ -229,7 +231,7 @@ int gdn_qlinear_workspace_size(const gdn_qlinear_args* args, size_t* bytes);
  * must be NULL and `workspace_bytes` 0: the MFMA path's operand goes to a scratch array
  * the library holds on each device (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES, kept until the
  * process ends), so calls whose gdn_qlinear_workspace_size() exceeds that are GDN_EINVAL
- * (one layer at any m and k fits). Every call on a device shares that device's scratch:
+ * (one layer of up to 512 rows at any k fits; 1024 rows fit for k up to 4096). Every call on a device shares that device's scratch:
  * calls that overlap in time on one device (different streams or threads) race. */
 #define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 int gdn_qlinear_noalloc(const gdn_qlinear_args* args);

@@ -68,6 +68,8 @@ struct QParams {
   // are zeros
   uint16_t* xfrag;
   int mtiles;
+  int mgroups;  // MFMA path: groups of MT m-tiles (the grid is layers x tiles x mgroups)
+  int remap;    // MFMA path: XCD-aware workgroup order (see qgemm_kernel)
 };
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -369,8 +371,15 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
     uint32_t sb[kRows * (kMaxG + 1)];
     f4 red[3][MT * NT][64];
   } sm;
-  const int layer = blockIdx.x / p.tiles, tile = blockIdx.x % p.tiles;
-  const int mt0 = blockIdx.y * MT;
+  // Workgroup = (layer, weight tile, m group), m groups fastest. Workgroups are dispatched to
+  // the 8 XCDs round robin; with several m groups the ids are renumbered so that each XCD
+  // runs a contiguous range -- all m groups of a weight tile on one XCD, one after another,
+  // so its weight rows come from HBM once and from that XCD's L2 after.
+  int bid = blockIdx.x;
+  if (p.remap) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
+  const int mg = bid % p.mgroups, lt = bid / p.mgroups;
+  const int layer = lt / p.tiles, tile = lt % p.tiles;
+  const int mt0 = mg * MT;
   const int lane = threadIdx.x & 63, g4 = lane >> 4, nn = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K, G = K / 64, nch = K / 32, sbs = G + 1;
@@ -623,7 +632,10 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   int NT = 4;
   while (NT > 1 && (size_t)a.n_layers * ((R + 16 * NT - 1) / (16 * NT)) * gy < 512) NT /= 2;
   p.tiles = (R + 16 * NT - 1) / (16 * NT);
-  const dim3 grid((unsigned)((size_t)a.n_layers * p.tiles), (unsigned)gy);
+  p.mgroups = gy;
+  const size_t nwg = (size_t)a.n_layers * p.tiles * gy;
+  p.remap = gy > 1 && nwg % 8 == 0;
+  const dim3 grid((unsigned)nwg);
   switch (MT) {
     case 1: return launch_gemm_mt<1>(NT, p, grid, stream);
     case 2: return launch_gemm_mt<2>(NT, p, grid, stream);

@@ -42,7 +42,7 @@ CHUNKED_MIN_T = 20
 
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
-QLINEAR_MAX_ROWS = 512
+QLINEAR_MAX_ROWS = 4096
 QLINEAR_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",

@@ -255,7 +255,7 @@ def _ql(gdn, **kw):
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(m=0), "bad shape"),
-    (dict(m=513), "bad shape"),
+    (dict(m=4097), "bad shape"),
     (dict(n_layers=0), "bad shape"),
     (dict(k=5000), "unsupported"),
     (dict(m=5), "needs a workspace"),
@@ -298,8 +298,10 @@ def test_qlinear_workspace_size(gdn):
     assert gdn.qlinear_workspace_size(40, 6144, n_layers=2) == 2 * 3 * 192 * 1024
     assert gdn.qlinear_workspace_size(65, 5120) == 8 * 160 * 1024  # 5 tiles -> 2 x 4
     assert gdn.qlinear_workspace_size(512, 1024) == 32 * 32 * 1024
+    assert gdn.qlinear_workspace_size(1024, 5120) == 64 * 160 * 1024
+    assert gdn.qlinear_workspace_size(4096, 8192) == 256 * 256 * 1024
     with pytest.raises(gdn.GdnError):
-        gdn.qlinear_workspace_size(513, 5120)
+        gdn.qlinear_workspace_size(4097, 5120)
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -307,7 +309,8 @@ def test_qlinear_workspace_size(gdn):
     (dict(m=4, workspace_bytes=16), "takes no workspace"),
     (dict(n_layers=2, m=512, k=8192), "more than the 8388608"),
     (dict(n_layers=48, m=40, k=5120), "more than the 8388608"),
-    (dict(m=513), "bad shape"),
+    (dict(m=1024, k=8192), "more than the 8388608"),
+    (dict(m=4097), "bad shape"),
     (dict(x=None), "exactly one"),
 ])
 def test_qlinear_noalloc_rejects_bad_arguments(gdn, kw, msg):

@@ -236,3 +236,62 @@ def test_qlinear_mfma_512_rows(O, gdn, dev):
     (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev))
     torch.cuda.synchronize()
     check(to_np(y), O.qlinear_blocked(x[0], w[0], s[0], b[0]), bound(O, x[0], s[0], b[0]), "y")
+
+
+# ---- prefill windows: more than 512 rows (the reference dequantizes and multiplies there,
+# model.cpp:358-362, in windows of 1024 tokens, session.hpp:136; this path keeps the exact
+# per-group arithmetic at every row count) ----
+
+def test_qlinear_in_proj_prefill_window_1024_rows(O, gdn, dev):
+    """A 1024-token window through the layer's four in_proj matrices (K = 5120; N reduced to
+    1024 / 512 / 48 / 48 to keep the fp64 check short): 16 m groups of 64 rows, XCD-ordered."""
+    import torch
+    log_case("qlinear (MFMA path) in_proj 4 segments, M=1024, K=5120")
+    M, K = 1024, 5120
+    ns = [1024, 512, 48, 48]
+    mats, host, x = [], [], None
+    for i, n in enumerate(ns):
+        xi, w, s, b = quant_inputs(O, 1, M, n, K, seed=800 + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w[0], s[0], b[0]))
+        host.append((w[0], s[0], b[0]))
+    ys = gdn.qlinear(mats, to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        check(to_np(y), O.qlinear_blocked(x[0], w, s, b), bound(O, x[0], s, b), f"segment {i}")
+
+
+def test_qlinear_out_proj_prefill_window_1024_rows(O, gdn, dev):
+    """out_proj(GatedRMSNorm(o, z)) over a 1024-token window: K = 6144, N = 5120 (full size),
+    the norm applied while the operand goes to the workspace; same tolerance as the M <= 512
+    norm tests."""
+    import torch
+    log_case("qlinear (MFMA path) out_proj with GatedRMSNorm, M=1024, K=6144, N=5120")
+    M, K, N = 1024, 6144, 5120
+    rng = np.random.default_rng(901)
+    o = (rng.standard_normal((M, K)) * 0.3).astype(np.float32)
+    z = O.to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    gamma = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    _, w, s, b = quant_inputs(O, 1, M, N, K, seed=902)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])],
+                       norm=(to_dev(o, dev), to_dev(z, dev), to_dev(gamma, dev), 1e-6))
+    torch.cuda.synchronize()
+    xn = O.gated_rmsnorm(o.reshape(M * 48, 128), z.reshape(M * 48, 128), gamma, 1e-6).reshape(M, K)
+    ref = O.qlinear_blocked(xn, w[0], s[0], b[0])
+    W = (np.abs(np.repeat(bf16_to_f32(s[0]), 64, axis=1)) * 15 + np.abs(np.repeat(bf16_to_f32(b[0]), 64, axis=1)))
+    flip = 3 * 2.0 ** -8 * (np.abs(bf16_to_f32(xn)).max(axis=1, keepdims=True) * W.max(axis=1)[None, :])
+    check(to_np(y), ref, bound(O, xn, s[0], b[0]) + flip, "y")
+
+
+def test_qlinear_4096_rows_two_layers(O, gdn, dev):
+    """The most rows (4096) on two stacked layers, K = 1024, N = 96: every m group of both
+    layers, against the oracle."""
+    import torch
+    log_case("qlinear (MFMA path) M=4096, 2 layers, K=1024, N=96")
+    L, M, N, K = 2, 4096, 96, 1024
+    x, w, s, b = quant_inputs(O, L, M, N, K, seed=903)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w, s, b)], to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    got = to_np(y)
+    for l in range(L):
+        check(got[l], O.qlinear_blocked(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"layer {l}")
