@@ -351,10 +351,13 @@ __device__ __forceinline__ RowPtrs row_ptrs(const QParams& p, int layer, int row
 }
 
 // MFMA path, step 2. Workgroup = 16 NT weight rows (the output columns) x 16 MT operand
-// rows; wave w takes the groups [w G / 4, (w + 1) G / 4) of the G = K / 64 groups (a
-// multiple of 4 for every supported K). Lane (g4, nn) = (l / 16, l % 16) reads the nibble
-// words 8 g + 2 g4 + s of its row 16 nt + nn (one 8-byte load per row and group) and gets
-// C rows m = 4 g4 + i of column nn.
+// rows; wave w takes the groups g = 4 i + w, i < G / 4, of the G = K / 64 groups (a multiple
+// of 4 for every supported K), so the four groups of a weight row's 128-byte line are asked
+// for by the four waves together and the line is fetched once (when each wave took a
+// contiguous quarter of K, a line's four groups were read at four different times and
+// lines were fetched again after eviction). Lane (g4, nn) = (l / 16, l % 16) reads the
+// nibble words 8 g + 2 g4 + s of its row 16 nt + nn (one 8-byte load per row and group) and
+// gets C rows m = 4 g4 + i of column nn.
 // Memory: the weight stream comes from HBM once, so what bounds the kernel is how many of
 // its bytes each wave keeps in flight: every load is issued kRing groups ahead (the ring
 // below), and the workgroup's scale and bias pairs are staged in LDS once at the start
@@ -383,7 +386,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, nn = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K, G = K / 64, nch = K / 32, sbs = G + 1;
-  const int g0 = wave * G / 4, g1 = (wave + 1) * G / 4;
+  const int ng = G / 4;  // this wave's groups: 4 i + wave, i < ng
 
   // this lane's weight row for each n-tile
   g_u32x2* wr[NT];
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   };
   Slot R[kRing];
 #pragma unroll
-  for (int j = 0; j < kRing; ++j) load(g0 + j, R[j]);  // (g1 - g0 >= kRing)
+  for (int j = 0; j < kRing; ++j) load(4 * j + wave, R[j]);  // (ng >= kRing)
 
   // the scale and bias pairs of the workgroup's rows, all groups: thread t takes row
   // t / (256 / kRows), four groups at a time (8-byte loads: G and the block starts are
@@ -451,8 +454,9 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // group g from slot sl, then sl reloaded with group g + kRing
-  auto step = [&](int g, Slot& sl) {
+  // the wave's i-th group from slot sl, then sl reloaded with its (i + kRing)-th
+  auto step = [&](int i, Slot& sl) {
+    const int g = 4 * i + wave;
     f4 xs[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -473,11 +477,11 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
         for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
       }
     }
-    load(min(g + kRing, g1 - 1), sl);
+    load(4 * min(i + kRing, ng - 1) + wave, sl);
   };
-  for (int gb = g0; gb < g1; gb += kRing) {
+  for (int ib = 0; ib < ng; ib += kRing) {
 #pragma unroll
-    for (int j = 0; j < kRing; ++j) step(gb + j, R[j]);
+    for (int j = 0; j < kRing; ++j) step(ib + j, R[j]);
   }
 
   // the four waves' partial sums (fixed order: wave 0 + 1 + 2 + 3), rounded to bf16 once
