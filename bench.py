@@ -223,7 +223,27 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
                 intra_frac_mfma=intra / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 all_products_frac_mfma=(intra + inter) / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 intra_flop=intra, inter_flop=inter,
-                hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9)
+                hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9,
+                per_kernel=prefill_kernel_fracs() if T == 4096 else None)
+
+
+def prefill_kernel_fracs():
+    """MFMA fraction of each prefill kernel alone, from the committed rocprofv3 kernel trace
+    (durations) and counter run (executed MFMA FLOPs, busy cycles): normative FLOPs and
+    executed FLOPs over the kernel's own duration, against the dense bf16 peak."""
+    path = os.path.join(ROOT, "profiles", "prefill_kernels.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        ks = json.load(fh)["kernels"]
+    peak = MFMA_BF16_PEAK_TFLOPS * 1e12
+    out = {}
+    for name, k in ks.items():
+        s = k["avg_us"] * 1e-6
+        out[name] = dict(avg_us=k["avg_us"], frac_mfma_normative=round(k["normative_flop"] / s / peak, 4),
+                         frac_mfma_executed=round(k["executed_mfma_flop"] / s / peak, 4),
+                         mfma_busy_counter=k["mfma_busy"])
+    return out
 
 
 def bench_crossover(torch, gdn, dev, timer, steps: int, warmup: int, Ts=(16, 32, 64, 128, 256, 512, 1024),
