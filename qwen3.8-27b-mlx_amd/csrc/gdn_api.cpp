@@ -313,10 +313,10 @@ int gdn_run(const gdn_layer_args* a) {
       GDN_HEAD_DIM / gdn::recurrent_tile_rows((long long)a->n_layers * a->batch * a->num_v_heads);
   const int64_t nblocks = (int64_t)a->n_layers * a->batch * a->num_v_heads * tiles;
   p.nblocks = static_cast<int>(nblocks);
-  // XCD-aware order (the 6 workgroups of a k-head on one XCD, whose L2 serves their shared
-  // q/k/x reads) only for large grids: measured faster from B = 8 at 48 layers (36,864
-  // workgroups: 407 vs 418 us; B = 16: 821 vs 865 us), even at B = 4, and slower for smaller
-  // grids, where dispatch order is better (B = 1: 50.4 vs 52.6 us; B = 2: 98.8 vs 102.7 us).
+  // XCD order: the contiguous split (each XCD one eighth of the grid) for large grids,
+  // measured faster from B = 8 at 48 layers (36,864 workgroups: 407 vs 418 us; B = 16: 821
+  // vs 865 us) and slower for smaller ones (B = 1 over 8 state sets: 56.2 vs 53.2 us), which
+  // interleave k-head groups over the XCDs instead (B = 1: 53.6 -> 52.9 us).
   p.remap = (nblocks % 8) == 0 && nblocks > 16384;
   p.q = a->q;
   p.k = a->k;
