@@ -355,8 +355,8 @@ __device__ __forceinline__ RowPtrs row_ptrs(const QParams& p, int layer, int row
 // of 4 for every supported K), so the four groups of a weight row's 128-byte line are asked
 // for by the four waves together and the line is fetched once (when each wave took a
 // contiguous quarter of K, a line's four groups were read at four different times and
-// lines were fetched again after eviction). Lane (g4, nn) = (l / 16, l % 16) reads the
-// nibble words 8 g + 2 g4 + s of its row 16 nt + nn (one 8-byte load per row and group) and
+// lines were fetched again after eviction). Lane (g4, nn) = (l / 16, l % 16) takes the
+// nibble words 8 g + 2 g4 + s of its row 16 nt + nn (loaded by another lane, see below) and
 // gets C rows m = 4 g4 + i of column nn.
 // Memory: the weight stream comes from HBM once, so what bounds the kernel is how many of
 // its bytes each wave keeps in flight: every load is issued kRing groups ahead (the ring
@@ -388,7 +388,13 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   const int K = p.K, G = K / 64, nch = K / 32, sbs = G + 1;
   const int ng = G / 4;  // this wave's groups: 4 i + wave, i < ng
 
-  // this lane's weight row for each n-tile
+  // Weight loads are laid out for the memory path, not for the MFMA: lane 4 r + c reads the
+  // 8-byte chunk c (words 2 c, 2 c + 1) of row r's group, so the 32 bytes of a row's group
+  // come from one lane quad in one L1 access (with lane 16 c + r reading them, the four
+  // lanes of every quad hit four rows: four times the L1 accesses, and the address path
+  // saturates). The B fragment wants chunk g4 of row nn in lane 16 g4 + nn, so each loaded
+  // word pair crosses lanes with ds_bpermute before its nibbles are expanded.
+  const int bsrc = (4 * nn + g4) * 4;  // byte address of the lane that loaded (nn, g4)
   g_u32x2* wr[NT];
   uint16_t* yr[NT];
   int ystride[NT];
@@ -398,9 +404,11 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
     const int grow = (tile * NT + nt) * 16 + nn;
     valid[nt] = grow < p.R;
     const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
-    wr[nt] = (g_u32x2*)(rp.w) + g4;  // + 4 g: words 8 g + 2 g4, +1
     yr[nt] = rp.y;
     ystride[nt] = rp.ystride;
+    const int lrow = (tile * NT + nt) * 16 + (lane >> 2);
+    const RowPtrs rl = row_ptrs(p, layer, lrow < p.R ? lrow : p.R - 1);
+    wr[nt] = (g_u32x2*)(rl.w) + (lane & 3);  // + 4 g: words 8 g + 2 c, +1
   }
   const bf8* xa = reinterpret_cast<const bf8*>(p.xfrag + ((size_t)layer * p.mtiles + mt0) * nch * 512) + lane;
   const bf8 ones = __builtin_bit_cast(bf8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -468,7 +476,9 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
       const uint32_t sbv = sm.sb[(16 * nt + nn) * sbs + g];
       const float sc = __builtin_bit_cast(float, sbv << 16);
       const float off = __builtin_bit_cast(float, sbv & 0xFFFF0000u) - 128.0f * sc;
-      const bf8 b0 = nibbles_bf16(sl.w[nt][0], nk), b1 = nibbles_bf16(sl.w[nt][1], nk);
+      const uint32_t w0 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)sl.w[nt][0]);
+      const uint32_t w1 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)sl.w[nt][1]);
+      const bf8 b0 = nibbles_bf16(w0, nk), b1 = nibbles_bf16(w1, nk);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         f4 acc = mfma(sl.a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
