@@ -375,9 +375,11 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
     f4 red[3][MT * NT][64];
   } sm;
   // Workgroup = (layer, weight tile, m group), m groups fastest. Workgroups are dispatched to
-  // the 8 XCDs round robin; with several m groups the ids are renumbered so that each XCD
-  // runs a contiguous range -- all m groups of a weight tile on one XCD, one after another,
-  // so its weight rows come from HBM once and from that XCD's L2 after.
+  // the 8 XCDs round robin; the ids are renumbered (p.remap) so that each XCD runs a
+  // contiguous range: with several m groups, all m groups of a weight tile on one XCD, one
+  // after another, so its weight rows come from HBM once and from that XCD's L2 after; with
+  // 8 layers or more, whole layers per XCD, so a layer's operand is read from HBM into one
+  // L2 instead of all eight.
   int bid = blockIdx.x;
   if (p.remap) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
   const int mg = bid % p.mgroups, lt = bid / p.mgroups;
@@ -648,7 +650,7 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   p.tiles = (R + 16 * NT - 1) / (16 * NT);
   p.mgroups = gy;
   const size_t nwg = (size_t)a.n_layers * p.tiles * gy;
-  p.remap = gy > 1 && nwg % 8 == 0;
+  p.remap = (gy > 1 || a.n_layers >= 8) && nwg % 8 == 0;
   const dim3 grid((unsigned)nwg);
   switch (MT) {
     case 1: return launch_gemm_mt<1>(NT, p, grid, stream);

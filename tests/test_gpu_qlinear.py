@@ -226,6 +226,27 @@ def test_qlinear_mfma_in_proj_two_layers_64_row_tiles(O, gdn, dev, M):
             check(got[l], O.qlinear_blocked(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
 
 
+@pytest.mark.parametrize("M,nseg", [(40, [300, 100]), (9, [700])])
+def test_qlinear_mfma_eight_layers_whole_layers_per_xcd(O, gdn, dev, M, nseg):
+    """8 layers in one launch: the workgroup ids are renumbered so each XCD runs whole layers
+    (a layer's operand then reaches one L2); every layer and segment must still be right."""
+    import torch
+    log_case(f"qlinear (MFMA path) 8 layers, segments {nseg}, M={M}, K=1024")
+    L, K = 8, 1024
+    mats, host, x = [], [], None
+    for i, n in enumerate(nseg):
+        xi, w, s, b = quant_inputs(O, L, M, n, K, seed=1200 + 10 * M + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w, s, b))
+        host.append((w, s, b))
+    ys = gdn.qlinear(mats, to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        got = to_np(y)
+        for l in range(L):
+            check(got[l], O.qlinear(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
+
+
 def test_qlinear_mfma_512_rows(O, gdn, dev):
     """The most rows the quantized path takes (512 = 32 m-tiles in 8 groups of 4), N = 4096:
     64 tiles of 64 rows x 8 = 512 workgroups, so the 64-row form with 4 m-tiles runs."""
