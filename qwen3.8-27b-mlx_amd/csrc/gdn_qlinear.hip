@@ -238,33 +238,57 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
 }
 
 // MFMA path, step 1: the operand (normalised when NORM) into the workspace's fragment
-// order. Thread = (layer, row, 32-value piece c): the piece is 4 fragment lanes of 8
-// values (blocks 2 (c / 2) + s, lanes 16 (2 (c % 2) + j / 2) + row % 16, s = j % 2). The
-// thread count is a multiple of 4 and pieces run fastest, so a DPP quad is one head.
+// order. Thread = (layer, row, 32-value piece c, quarter j): 8 consecutive values, one
+// fragment lane (block 2 (c / 2) + j % 2, lane 16 (2 (c % 2) + j / 2) + row % 16), so four
+// consecutive threads read a piece's contiguous bytes and a 16-lane DPP row holds one
+// 128-value head (nch is a multiple of 4). For the norm, each thread sums its 8 squares and
+// the row adds the 16 partial sums.
 template <bool NORM>
 __global__ __launch_bounds__(kThreads) void qprep_kernel(QParams p, int layers) {
   const int nch = p.K / 32, rows = 16 * p.mtiles;
-  const size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x;
-  if (t >= (size_t)layers * rows * nch) return;  // whole quads (nch is a multiple of 4)
+  const size_t tt = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (tt >= (size_t)layers * rows * nch * 4) return;  // whole 16-lane rows
+  const int j = (int)(tt & 3);
+  const size_t t = tt >> 2;
   const int c = (int)(t % nch);
   const size_t rg = t / nch;
   const int mrow = (int)(rg % rows), layer = (int)(rg / rows);
-  float v[32];
-  if (mrow < p.M) {
-    operand_piece<NORM>(p, layer, mrow, c, v);
-  } else {
+  const bool live = mrow < p.M;
+  const size_t base = ((size_t)layer * p.M + (live ? mrow : 0)) * p.K + 32 * c + 8 * j;
+  float v[8];
+  if (NORM) {
+    // GatedRMSNorm (model.cpp:350-354): h = o * rsqrt(mean(o^2) + eps) * gamma (fp32), times
+    // silu(fp32(z)), rounded to bf16 (the activation dtype out_proj takes)
+    const f4 o0 = *reinterpret_cast<const f4*>(p.xf + base);
+    const f4 o1 = *reinterpret_cast<const f4*>(p.xf + base + 4);
+    const u16x8 zz = *reinterpret_cast<const u16x8*>(p.z + base);
+    const float* gm = p.gamma + (size_t)layer * 128 + 32 * (c & 3) + 8 * j;
+    const f4 g0 = *reinterpret_cast<const f4*>(gm);
+    const f4 g1 = *reinterpret_cast<const f4*>(gm + 4);
+    float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = 0.0f;
+    for (int e = 0; e < 4; ++e) ss += o0[e] * o0[e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += o1[e] * o1[e];
+    ss = row16_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / 128.0f + p.eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float zf = bf2f(zz[e]);
+      const float h = (e < 4 ? o0[e] : o1[e - 4]) * rs * (e < 4 ? g0[e] : g1[e - 4]);
+      v[e] = live ? rbf(h * (zf * d_sigmoidf(zf))) : 0.0f;
+    }
+  } else {
+    const u16x8 xx = *reinterpret_cast<const u16x8*>(p.x + base);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = live ? bf2f(xx[e]) : 0.0f;
   }
   uint16_t* blk = p.xfrag + ((size_t)layer * p.mtiles + mrow / 16) * nch * 512;
+  u32x4 q;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    u32x4 q;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) q[e] = pack_bf2(v[8 * j + e], v[8 * j + e + 4]);
-    const int f = 2 * (c / 2) + (j & 1), ln = 16 * (2 * (c & 1) + j / 2) + (mrow & 15);
-    *reinterpret_cast<u32x4*>(blk + ((size_t)f * 64 + ln) * 8) = q;
-  }
+  for (int e = 0; e < 4; ++e) q[e] = pack_bf2(v[e], v[e + 4]);
+  const int f = 2 * (c / 2) + (j & 1), ln = 16 * (2 * (c & 1) + j / 2) + (mrow & 15);
+  *reinterpret_cast<u32x4*>(blk + ((size_t)f * 64 + ln) * 8) = q;
 }
 
 __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
@@ -637,7 +661,7 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   const int MT = qgemm_mt(a.m);
   p.mtiles = qgemm_mtiles(a.m);
   p.xfrag = static_cast<uint16_t*>(a.workspace);
-  const size_t prep_threads = (size_t)a.n_layers * 16 * p.mtiles * (a.k / 32);
+  const size_t prep_threads = (size_t)a.n_layers * 16 * p.mtiles * (a.k / 32) * 4;
   const dim3 gp((unsigned)((prep_threads + kThreads - 1) / kThreads));
   if (norm) hipLaunchKernelGGL(qprep_kernel<true>, gp, dim3(kThreads), 0, stream, p, a.n_layers);
   else hipLaunchKernelGGL(qprep_kernel<false>, gp, dim3(kThreads), 0, stream, p, a.n_layers);
