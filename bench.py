@@ -525,7 +525,9 @@ def main() -> int:
                      "traffic": load_traffic("decode_b1_48_layers_conv"),
                      "kernel_us_avg": round(launch_us, 2),
                      "kernel_us_event_bracketed_avg": round(head["launch_ms_avg"] * 1e3, 2),
+                     "kernel_us_event_bracketed_p10": round(head["launch_ms_p10"] * 1e3, 2),
                      "kernel_us_event_bracketed_p50": round(head["launch_ms_p50"] * 1e3, 2),
+                     "kernel_us_event_bracketed_p90": round(head["launch_ms_p90"] * 1e3, 2),
                      "bytes_per_launch": head["bytes_per_step"]},
         "cpu_baseline": cpu,
         "secondary": sec,
