@@ -164,7 +164,7 @@ def test_qlinear_mfma_two_layers_two_segments(O, gdn, dev):
             check(got[l], O.qlinear(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
 
 
-@pytest.mark.parametrize("M", [5, 40])
+@pytest.mark.parametrize("M", [5, 17, 40, 64])
 def test_qlinear_mfma_gated_rmsnorm_prologue(O, gdn, dev, M):
     """out_proj(GatedRMSNorm(o, z)) for M rows on the MFMA path (the norm applied while the
     operand goes to the workspace), same tolerance as the GEMV path's test."""
@@ -180,7 +180,7 @@ def test_qlinear_mfma_gated_rmsnorm_prologue(O, gdn, dev, M):
                        norm=(to_dev(o, dev), to_dev(z, dev), to_dev(gamma, dev), 1e-6))
     torch.cuda.synchronize()
     xn = O.gated_rmsnorm(o.reshape(M * 48, 128), z.reshape(M * 48, 128), gamma, 1e-6).reshape(M, K)
-    ref = O.qlinear(xn, w[0], s[0], b[0])
+    ref = O.qlinear_blocked(xn, w[0], s[0], b[0])
     W = (np.abs(np.repeat(bf16_to_f32(s[0]), 64, axis=1)) * 15 + np.abs(np.repeat(bf16_to_f32(b[0]), 64, axis=1)))
     flip = 3 * 2.0 ** -8 * (np.abs(bf16_to_f32(xn)).max(axis=1, keepdims=True) * W.max(axis=1)[None, :])
     check(to_np(y), ref, bound(O, xn, s[0], b[0]) + flip, "y")
