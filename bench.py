@@ -334,6 +334,40 @@ def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
     return dict(GBps=2 * n * 4 / (r["ms_per_step"] * 1e-3) / 1e9, bytes=2 * n * 4)
 
 
+def stream_ceilings(torch, dev, timer, steps: int):
+    """Plain memory streams with the decode and verify state traffic's shapes (libgdn_probe.so,
+    no arithmetic): the decode step's 4,608 tiles of 32 KB read and written back in place,
+    and verify's 768 tiles read once and written 5 times, each rotated over 8 buffer sets
+    as the kernels' lines are. The kernels' rates are read against these."""
+    import ctypes
+    path = os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "libgdn_probe.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    L.gdn_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    L.gdn_probe_read_write_t.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p]
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    tile = 8192  # floats (32 KB)
+    out = {}
+    nd = 48 * HV * 2  # decode: 48 layers x 48 heads x two 64-row tiles
+    bufs = [torch.randn(nd * tile, device=dev) for _ in range(8)]
+    r = timer.time_calls(lambda it: L.gdn_probe_rmw(bufs[it % 8].data_ptr(), nd, st()), steps, 10)
+    nbytes = 2 * nd * tile * 4
+    out["decode_shape_rmw_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                                          GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=nbytes)
+    del bufs
+    nv, T = 8 * HV * 2, 5  # verify: B=8 x 48 heads x two tiles, 5 per-step states
+    src = [torch.randn(nv * tile, device=dev) for _ in range(8)]
+    dst = [torch.empty(nv * T * tile, device=dev) for _ in range(8)]
+    r = timer.time_calls(lambda it: L.gdn_probe_read_write_t(src[it % 8].data_ptr(), dst[it % 8].data_ptr(), nv, T, st()),
+                         steps, 10)
+    nbytes = (1 + T) * nv * tile * 4
+    out["verify_shape_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                                      GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=nbytes)
+    return out
+
+
 def launch_floors(torch, dev, timer, steps: int):
     """What a one-layer launch cannot beat, timed the same way: a one-element kernel (the
     launch itself) and a device copy of one layer's 3.1 MB state (3.1 MB read + 3.1 MB
@@ -490,6 +524,16 @@ def main() -> int:
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)
         print(f"# device copy ceiling: {cc['GBps']:.0f} GB/s", flush=True)
+        sc = stream_ceilings(torch, dev, timer, steps=max(20, args.steps // 2))
+        if sc is not None:
+            sec["stream_ceilings"] = sc
+            if head is not None:
+                sc["decode_vs_rmw_stream"] = round(head["GBps"] / sc["decode_shape_rmw_stream"]["GBps"], 4)
+            if "verify_b8_t5" in sec:
+                sc["verify_vs_stream"] = round(sec["verify_b8_t5"]["GBps"] / sc["verify_shape_stream"]["GBps"], 4)
+            print(f"# same-shape streams: decode RMW {sc['decode_shape_rmw_stream']['us']:.1f} us "
+                  f"({sc['decode_shape_rmw_stream']['GBps']:.0f} GB/s), verify "
+                  f"{sc['verify_shape_stream']['us']:.1f} us ({sc['verify_shape_stream']['GBps']:.0f} GB/s)", flush=True)
 
     if head is None:
         print(json.dumps({"secondary": sec}))

@@ -1,0 +1,64 @@
+// Memory streams with the shapes of the decode and verify state traffic, for bench.py's
+// ceiling lines (libgdn_probe.so; not part of libgdn's ABI). They move the same bytes in the
+// same pattern as the kernels with none of the arithmetic, so the kernels' rate can be read
+// against what this GPU streams for that pattern rather than only against the 8 TB/s peak.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Decode shape: each workgroup of 256 threads reads its 32 KB tile and writes it back in
+// place (non-temporal both ways, as the decode state). Written as a loop over a run-time
+// tile size: the compiler then stores each float4 as soon as its load has landed, which
+// streams faster here (48.2 us for the decode step's 302 MB of state) than the same kernel
+// with the size a constant, where it holds the stores back behind later loads (50.1 us).
+__global__ __launch_bounds__(256) void rmw_tile_kernel(f4* buf, int64_t per, float a) {
+  f4* base = buf + (int64_t)blockIdx.x * per;
+  const int64_t per_thread = per / 256;
+  f4 v[8];
+  for (int64_t i0 = 0; i0 < per_thread; i0 += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(base + (i0 + j) * 256 + threadIdx.x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f4 r = v[j] * a;
+      __builtin_nontemporal_store(r, base + (i0 + j) * 256 + threadIdx.x);
+    }
+  }
+}
+
+// Verify shape: each workgroup reads its 32 KB tile and writes it T times (the per-step
+// states), non-temporal.
+__global__ __launch_bounds__(256) void read_write_t_kernel(const f4* src, f4* dst, int T, float a) {
+  const f4* s = src + (int64_t)blockIdx.x * 2048;
+  f4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(s + j * 256 + threadIdx.x);
+  for (int t = 0; t < T; ++t) {
+    f4* d = dst + ((int64_t)blockIdx.x * T + t) * 2048;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = v[j] * a;
+      __builtin_nontemporal_store(v[j], d + j * 256 + threadIdx.x);
+    }
+  }
+}
+
+}  // namespace
+
+// buf: tiles x 32 KB (16-byte aligned); returns a hipError_t.
+extern "C" int gdn_probe_rmw(void* buf, int tiles, void* stream) {
+  if (!buf || tiles < 1) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f);
+  return (int)hipGetLastError();
+}
+
+// src: tiles x 32 KB; dst: tiles x T x 32 KB.
+extern "C" int gdn_probe_read_write_t(const void* src, void* dst, int tiles, int T, void* stream) {
+  if (!src || !dst || tiles < 1 || T < 1) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(read_write_t_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (const f4*)src, (f4*)dst, T,
+                     1.0001f);
+  return (int)hipGetLastError();
+}
