@@ -65,10 +65,6 @@ __device__ __forceinline__ float wave64_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float load_qkv(const void* base, size_t i, int bf16) {
-  return bf16 ? bf2f(static_cast<const uint16_t*>(base)[i]) : static_cast<const float*>(base)[i];
-}
-
 // Causal depthwise conv at one channel from its 4 xp rows and 4 taps
 // (model.cpp:385-395): taps in order j = 0..3, every product and partial sum rounded
 // to bf16.
@@ -132,20 +128,26 @@ __device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
 template <int SLOTS>
 __device__ __forceinline__ int row_of(int wave, int i, int grp) { return wave * 4 * SLOTS + i * 4 + grp; }
 
+// The tile's rows of one (layer, batch, v-head) state at `base`.
+template <int SLOTS>
+__device__ __forceinline__ void load_rows(const float* base, const Tile& t, int wave, int grp, int j16,
+                                          f4v (&s)[SLOTS][2]) {
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) {
+    const int row = t.r0 + row_of<SLOTS>(wave, i, grp);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      s[i][hf] = __builtin_nontemporal_load(
+          reinterpret_cast<const f4v*>(base + (size_t)row * kD + hf * 64 + j16 * 4));
+    }
+  }
+}
+
 template <int SLOTS>
 __device__ __forceinline__ void load_state(const RecurrentParams& p, const Tile& t, int wave,
                                            int grp, int j16, f4v (&s)[SLOTS][2]) {
   if (p.state_in) {
-    const float* base = p.state_in + t.head * kD * kD;
-#pragma unroll
-    for (int i = 0; i < SLOTS; ++i) {
-      const int row = t.r0 + row_of<SLOTS>(wave, i, grp);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        s[i][hf] = __builtin_nontemporal_load(
-            reinterpret_cast<const f4v*>(base + (size_t)row * kD + hf * 64 + j16 * 4));
-      }
-    }
+    load_rows<SLOTS>(p.state_in + t.head * kD * kD, t, wave, grp, j16, s);
   } else {
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
@@ -438,7 +440,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
 
 // ---------------------------------------------------------------- any T (verify, prefill-size L)
 
-template <int SLOTS, int FE, bool COLLECT>
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
+// Every load of a pass is issued unconditionally (addresses clamped to valid rows, values
+// past the pass unused) and the first pass, which also loads the state, is a separate
+// instantiation of the pass: a load under a data-dependent branch would make the compiler
+// count the loads after it conservatively at the join, so the front end would wait for the
+// whole state tile (or each conv row for the previous one) before its arithmetic.
+template <int SLOTS, int FE, bool COLLECT, bool HAS_STATE>
 __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
   constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   __shared__ float sm_q[kTC][kD];
@@ -452,71 +464,91 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4, j16 = lane & 15;
   const int T = p.T;
-  constexpr int kWin = kTC + kTaps - 1;  // xp rows feeding one chunk
+  constexpr int kWin = kTC + kTaps - 1;  // xp rows feeding one pass
+  constexpr int kPer = 2 * kD + kTileRows;  // q, k, v values of one step (FE = 0)
+  constexpr int kRaw = (kTC * kPer + kThreads - 1) / kThreads;
 
   const uint16_t* x_b = nullptr;
   const uint16_t* cin_b = nullptr;
-  const uint16_t* w_l = nullptr;
-  int c0 = 0;
-  float wv[2][kTaps] = {};
+  int c0 = 0, c1 = 0;
+  uint32_t wr[2][kTaps] = {};
   if (FE == 1) {
     x_b = p.x + t.lb * (size_t)T * p.C;
     cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
-    w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
-    c0 = fe_channel<SLOTS>(p, t, wave, lane);
+    const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
+    // waves 0..2 own channels (q, k: two per lane; the tile's v rows: one, read twice);
+    // wave 3 mirrors wave 2 so that every wave issues the same loads
+    c0 = fe_channel<SLOTS>(p, t, wave < 3 ? wave : 2, lane);
+    c1 = wave < 2 ? c0 + 64 : c0;
+#pragma unroll
+    for (int j = 0; j < kTaps; ++j) {
+      wr[0][j] = w_l[(size_t)j * p.C + c0];
+      wr[1][j] = w_l[(size_t)j * p.C + c1];
+    }
   }
   const int nm = wave < 2 ? 2 : 1;  // conv channels per lane (waves 0..2)
+  const int gt = tid - (kThreads - kTC);  // the last 8 threads: one step's gates each
 
   f4v s[SLOTS][2];
-  for (int t0 = 0; t0 < T; t0 += kTC) {
+  auto pass = [&](int t0, auto first) {
+    constexpr bool kFirst = decltype(first)::value;
     const int tc = min(kTC, T - t0);
-    if (t0 > 0) __syncthreads();  // the previous pass is done reading LDS
+    if (!kFirst) __syncthreads();  // the previous pass is done reading LDS
 
-    // front-end loads of the chunk (raw bits, all in flight together)
+    // 1. loads: the pass's conv window or q/k/v, its gates, and (first pass) the state
     uint32_t xr[2][kWin] = {};
-    uint32_t wr[2][kTaps] = {};
-    if (FE == 1 && wave < 3) {
+    uint32_t raw[kRaw] = {};
+    if (FE == 1) {
+      const int last = T + kConvRows - 1;  // last row of xp = [conv_in ; x]
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        if (m < nm) {
+      for (int r = 0; r < kWin; ++r) {
+        const int rr = min(t0 + r, last);
+        xr[0][r] = *xp_addr(x_b, cin_b, p.C, c0, rr);
+        xr[1][r] = *xp_addr(x_b, cin_b, p.C, c1, rr);
+      }
+    } else {
 #pragma unroll
-          for (int r = 0; r < kWin; ++r) {
-            if (r < tc + kTaps - 1) xr[m][r] = *xp_addr(x_b, cin_b, p.C, c0 + 64 * m, t0 + r);
-          }
-          if (t0 == 0) {
-#pragma unroll
-            for (int j = 0; j < kTaps; ++j) wr[m][j] = w_l[(size_t)j * p.C + c0 + 64 * m];
-          }
-        }
+      for (int i = 0; i < kRaw; ++i) {
+        const int e = min(tid + i * kThreads, tc * kPer - 1);
+        const int tt = e / kPer, c = e % kPer;
+        const size_t row = t.lb * T + (t0 + tt);
+        const void* base = c < kD ? p.q : c < 2 * kD ? p.k : p.v;
+        const size_t idx = c < 2 * kD ? (row * p.Hk + t.g) * kD + (c & (kD - 1))
+                                      : (row * p.Hv + t.h) * kD + t.r0 + (c - 2 * kD);
+        raw[i] = qkv_raw(base, idx, p.qkv_bf16);
       }
     }
-    GateRaw gr;
-    const int gt = tid - (kThreads - kTC);  // the last 8 threads: one step each
-    if (gt >= 0 && gt < tc) gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gt)) * p.Hv + t.h);
+    const int gsel = min(max(gt, 0), tc - 1);
+    const GateRaw gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gsel)) * p.Hv + t.h);
+    if constexpr (kFirst) {
+      if constexpr (HAS_STATE) {
+        load_rows<SLOTS>(p.state_in + t.head * kD * kD, t, wave, grp, j16, s);
+      } else {
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
 
-    if (t0 == 0) load_state<SLOTS>(p, t, wave, grp, j16, s);
-
+    // 2. front end into LDS while the state is in flight
     if (FE == 0) {
-      const int per = 2 * kD + kTileRows;
-      for (int e = tid; e < tc * per; e += kThreads) {
-        const int tt = e / per;
-        const int c = e % per;
-        const size_t row = t.lb * T + (t0 + tt);
-        if (c < kD) {
-          sm_q[tt][c] = load_qkv(p.q, (row * p.Hk + t.g) * kD + c, p.qkv_bf16);
-        } else if (c < 2 * kD) {
-          sm_k[tt][c - kD] = load_qkv(p.k, (row * p.Hk + t.g) * kD + c - kD, p.qkv_bf16);
-        } else {
-          sm_v[tt][c - 2 * kD] = load_qkv(p.v, (row * p.Hv + t.h) * kD + t.r0 + c - 2 * kD, p.qkv_bf16);
+#pragma unroll
+      for (int i = 0; i < kRaw; ++i) {
+        const int e = tid + i * kThreads;
+        if (e < tc * kPer) {
+          const int tt = e / kPer, c = e % kPer;
+          const float val = qkv_value(raw[i], p.qkv_bf16);
+          if (c < kD) sm_q[tt][c] = val;
+          else if (c < 2 * kD) sm_k[tt][c - kD] = val;
+          else sm_v[tt][c - 2 * kD] = val;
         }
       }
     } else if (wave < 3) {
-      if (t0 == 0) {
+      float wv[2][kTaps];
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
+      for (int m = 0; m < 2; ++m) {
 #pragma unroll
-          for (int j = 0; j < kTaps; ++j) wv[m][j] = bf2f((uint16_t)wr[m][j]);
-        }
+        for (int j = 0; j < kTaps; ++j) wv[m][j] = bf2f((uint16_t)wr[m][j]);
       }
 #pragma unroll
       for (int tt = 0; tt < kTC; ++tt) {
@@ -546,11 +578,14 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     if (gt >= 0 && gt < tc) gate_math(p, gr, sm_a[gt], sm_b[gt]);
     __syncthreads();
 
+    // 3. the pass's steps on the rows in registers
     for (int tt = 0; tt < tc; ++tt) {
       apply_step<SLOTS, COLLECT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave, grp,
                                  j16, s);
     }
-  }
+  };
+  pass(0, BoolTag<true>{});
+  for (int t0 = kTC; t0 < T; t0 += kTC) pass(t0, BoolTag<false>{});
 
   if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
   if (FE == 1 && p.conv_out) write_conv_out<SLOTS>(p, t, x_b, cin_b);
@@ -578,10 +613,16 @@ __global__ void copy_u16_kernel(uint16_t* __restrict__ dst, const uint16_t* __re
 #endif
 constexpr long long kSmallTileMaxHeads = GDN_SMALL_TILE_MAX_HEADS;
 
+template <int SLOTS, int FE, bool HAS_STATE>
+void launch_steps_s(const RecurrentParams& p, bool collect, dim3 grid, dim3 block, hipStream_t stream) {
+  if (collect) hipLaunchKernelGGL((steps_kernel<SLOTS, FE, true, HAS_STATE>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((steps_kernel<SLOTS, FE, false, HAS_STATE>), grid, block, 0, stream, p);
+}
+
 template <int SLOTS, int FE>
 void launch_steps(const RecurrentParams& p, bool collect, dim3 grid, dim3 block, hipStream_t stream) {
-  if (collect) hipLaunchKernelGGL((steps_kernel<SLOTS, FE, true>), grid, block, 0, stream, p);
-  else hipLaunchKernelGGL((steps_kernel<SLOTS, FE, false>), grid, block, 0, stream, p);
+  if (p.state_in) launch_steps_s<SLOTS, FE, true>(p, collect, grid, block, stream);
+  else launch_steps_s<SLOTS, FE, false>(p, collect, grid, block, stream);
 }
 
 template <int SLOTS>
