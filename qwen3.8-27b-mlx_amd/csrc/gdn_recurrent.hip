@@ -209,6 +209,11 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
   const f4v k1 = *reinterpret_cast<const f4v*>(kk + 64 + j16 * 4);
   const f4v q0 = *reinterpret_cast<const f4v*>(qq + j16 * 4);
   const f4v q1 = *reinterpret_cast<const f4v*>(qq + 64 + j16 * 4);
+  // with COLLECT, this step's state; each slot's rows go out as soon as they are updated
+  float* const dst = !COLLECT ? nullptr
+                     : p.states_tbh
+                         ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
+                         : p.states + (t.head * p.T + step) * kD * kD;
   float ov[SLOTS];
 #pragma unroll
   for (int i = 0; i < SLOTS; ++i) {
@@ -230,6 +235,11 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
     GDN_UPD(a0.x, k0.x); GDN_UPD(a0.y, k0.y); GDN_UPD(a0.z, k0.z); GDN_UPD(a0.w, k0.w);
     GDN_UPD(a1.x, k1.x); GDN_UPD(a1.y, k1.y); GDN_UPD(a1.z, k1.z); GDN_UPD(a1.w, k1.w);
 #undef GDN_UPD
+    if (COLLECT) {
+      const int row = t.r0 + row_of<SLOTS>(wave, i, grp);
+      __builtin_nontemporal_store(a0, reinterpret_cast<f4v*>(dst + (size_t)row * kD + j16 * 4));
+      __builtin_nontemporal_store(a1, reinterpret_cast<f4v*>(dst + (size_t)row * kD + 64 + j16 * 4));
+    }
     float po = q0.x * a0.x;
     po = __builtin_fmaf(q0.y, a0.y, po);
     po = __builtin_fmaf(q0.z, a0.z, po);
@@ -240,12 +250,7 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
     po = __builtin_fmaf(q1.w, a1.w, po);
     ov[i] = row16_sum(po);
   }
-  if (COLLECT) {
-    float* dst = p.states_tbh
-                     ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
-                     : p.states + (t.head * p.T + step) * kD * kD;
-    store_rows<SLOTS>(dst, t, wave, grp, j16, s);
-  }
+
   // lane j (< SLOTS) of each group writes the output of slot j
   if (j16 < SLOTS) {
     float val = ov[0];
