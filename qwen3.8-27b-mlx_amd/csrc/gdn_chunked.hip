@@ -868,10 +868,16 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
   const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
   const size_t srow = ((size_t)b * p.Hv + h) * kD * kD + (size_t)(jt * kDt + fr) * kD + 4 * lg;
+  // one branch around all the state loads (a branch per load would make the compiler wait
+  // for each before the next and for all of them before the operand loads below)
   f4 S[kD / 16];
+  if (p.state_in) {
 #pragma unroll
-  for (int a = 0; a < kD / 16; ++a)
-    S[a] = p.state_in ? *reinterpret_cast<const f4*>(p.state_in + srow + 16 * a) : f4{0.f, 0.f, 0.f, 0.f};
+    for (int a = 0; a < kD / 16; ++a) S[a] = *reinterpret_cast<const f4*>(p.state_in + srow + 16 * a);
+  } else {
+#pragma unroll
+    for (int a = 0; a < kD / 16; ++a) S[a] = f4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const int last = p.nC - 1;
   StateOps A, B;
