@@ -13,7 +13,9 @@
 //
 // q, k, the tile's v rows and the gates of up to 8 steps are staged in LDS by the
 // workgroup (computed there from x in the conv front end: causal depthwise conv,
-// SiLU, l2norm, q scale, gate math), then every wave applies the steps to its rows:
+// SiLU, l2norm, q scale, gate math) -- except in decode with q, k, v given, where each
+// lane loads the 16 elements of q and k and the v values it uses itself -- then every
+// wave applies the steps to its rows:
 //   kS = k . s            (per-lane partial dot, then a 16-lane DPP butterfly)
 //   s  = a (s - b kS k) + b v_r k
 //   o_r = q . s           (partial dot + DPP butterfly)
@@ -200,15 +202,13 @@ __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const T
   }
 }
 
+// One step on the tile's rows in registers, from this lane's elements of k and q
+// ([4 j16, 4 j16 + 4) and [64 + 4 j16, 64 + 4 j16 + 4)) and its slots' v values.
 template <int SLOTS, bool COLLECT>
-__device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
-                                           float al, float be, const float* kk, const float* qq,
-                                           const float* vv, int wave, int grp, int j16,
-                                           f4v (&s)[SLOTS][2]) {
-  const f4v k0 = *reinterpret_cast<const f4v*>(kk + j16 * 4);
-  const f4v k1 = *reinterpret_cast<const f4v*>(kk + 64 + j16 * 4);
-  const f4v q0 = *reinterpret_cast<const f4v*>(qq + j16 * 4);
-  const f4v q1 = *reinterpret_cast<const f4v*>(qq + 64 + j16 * 4);
+__device__ __forceinline__ void apply_step_r(const RecurrentParams& p, const Tile& t, int step,
+                                             float al, float be, f4v k0, f4v k1, f4v q0, f4v q1,
+                                             const float (&vrs)[SLOTS], int wave, int grp, int j16,
+                                             f4v (&s)[SLOTS][2]) {
   // with COLLECT, this step's state; each slot's rows go out as soon as they are updated
   float* const dst = !COLLECT ? nullptr
                      : p.states_tbh
@@ -217,7 +217,7 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
   float ov[SLOTS];
 #pragma unroll
   for (int i = 0; i < SLOTS; ++i) {
-    const float vr = vv[row_of<SLOTS>(wave, i, grp)];
+    const float vr = vrs[i];
     f4v& a0 = s[i][0];
     f4v& a1 = s[i][1];
     float pk = k0.x * a0.x;
@@ -264,6 +264,22 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
       static_cast<float*>(p.o)[oi] = val;
     }
   }
+}
+
+// The same with k, q and the tile's v rows staged in LDS.
+template <int SLOTS, bool COLLECT>
+__device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
+                                           float al, float be, const float* kk, const float* qq,
+                                           const float* vv, int wave, int grp, int j16,
+                                           f4v (&s)[SLOTS][2]) {
+  const f4v k0 = *reinterpret_cast<const f4v*>(kk + j16 * 4);
+  const f4v k1 = *reinterpret_cast<const f4v*>(kk + 64 + j16 * 4);
+  const f4v q0 = *reinterpret_cast<const f4v*>(qq + j16 * 4);
+  const f4v q1 = *reinterpret_cast<const f4v*>(qq + 64 + j16 * 4);
+  float vrs[SLOTS];
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) vrs[i] = vv[row_of<SLOTS>(wave, i, grp)];
+  apply_step_r<SLOTS, COLLECT>(p, t, step, al, be, k0, k1, q0, q1, vrs, wave, grp, j16, s);
 }
 
 // Address of row r of the padded conv input xp = [conv_in ; x] at channel c. A row of a
@@ -332,7 +348,78 @@ __device__ __forceinline__ int fe_channel(const RecurrentParams& p, const Tile& 
 
 // ---------------------------------------------------------------- decode, T = 1
 
-template <int SLOTS, int FE>
+// q, k, v given (the reference's delta::run inputs): every lane loads its own elements of
+// q and k and its slots' v values, and every wave does the gate math, so there is no LDS
+// staging and no barrier; with the state present there is no branch around any load, so
+// nothing but the step itself waits for the state.
+template <int SLOTS, bool HAS_STATE>
+__global__ __launch_bounds__(kThreads) void decode_qkv_kernel(RecurrentParams p) {
+  typedef int i2v __attribute__((ext_vector_type(2)));
+  const Tile t = decode_block<SLOTS>(p);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = lane >> 4, j16 = lane & 15;
+  const size_t row0 = t.lb;  // (layer, b) at step 0
+
+  // 1. loads: q and k raw (bf16 pairs or fp32), v of the slots' rows, gates, the state
+  i4v qr[2], kr[2];
+  const size_t qkb = (row0 * p.Hk + t.g) * kD + 4 * j16;
+  if (p.qkv_bf16) {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const i2v a = *reinterpret_cast<const i2v*>(static_cast<const uint16_t*>(p.q) + qkb + 64 * h2);
+      const i2v b = *reinterpret_cast<const i2v*>(static_cast<const uint16_t*>(p.k) + qkb + 64 * h2);
+      qr[h2] = i4v{a.x, a.y, 0, 0};
+      kr[h2] = i4v{b.x, b.y, 0, 0};
+    }
+  } else {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      qr[h2] = *reinterpret_cast<const i4v*>(static_cast<const float*>(p.q) + qkb + 64 * h2);
+      kr[h2] = *reinterpret_cast<const i4v*>(static_cast<const float*>(p.k) + qkb + 64 * h2);
+    }
+  }
+  uint32_t vraw[SLOTS];
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i)
+    vraw[i] = qkv_raw(p.v, (row0 * p.Hv + t.h) * kD + t.r0 + row_of<SLOTS>(wave, i, grp), p.qkv_bf16);
+  const GateRaw gr = gate_load(p, t.layer, t.h, row0 * p.Hv + t.h);
+  f4v s[SLOTS][2];
+  if constexpr (HAS_STATE) {
+    load_rows<SLOTS>(p.state_in + t.head * kD * kD, t, wave, grp, j16, s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic below the loads
+
+  // 2. gates and values while the state is in flight, then the step
+  float al, be;
+  gate_math(p, gr, al, be);
+  f4v qf[2], kf[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    if (p.qkv_bf16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qf[h2][e] = bf2f((uint16_t)((uint32_t)qr[h2][e >> 1] >> (16 * (e & 1))));
+        kf[h2][e] = bf2f((uint16_t)((uint32_t)kr[h2][e >> 1] >> (16 * (e & 1))));
+      }
+    } else {
+      qf[h2] = __builtin_bit_cast(f4v, qr[h2]);
+      kf[h2] = __builtin_bit_cast(f4v, kr[h2]);
+    }
+  }
+  float vrs[SLOTS];
+#pragma unroll
+  for (int i = 0; i < SLOTS; ++i) vrs[i] = qkv_value(vraw[i], p.qkv_bf16);
+  apply_step_r<SLOTS, false>(p, t, 0, al, be, kf[0], kf[1], qf[0], qf[1], vrs, wave, grp, j16, s);
+  if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+}
+
+// The conv front end (x and the conv state given): q, k, v computed in the workgroup and
+// staged in LDS.
+template <int SLOTS>
 __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   __shared__ float sm_q[kD];
@@ -347,14 +434,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   const size_t row0 = t.lb;  // (layer, b) at step 0
 
   // 1. the front end's global loads, all in flight together
-  uint32_t xr[2][kTaps] = {}, wr[2][kTaps] = {};
-  uint32_t fe_raw = 0, v_raw = 0;
-  const uint16_t* x_b = nullptr;
-  const uint16_t* cin_b = nullptr;
+  uint32_t xr[2][kTaps], wr[2][kTaps];
+  const uint16_t* x_b = p.x + t.lb * (size_t)p.C;
+  const uint16_t* cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
   int c0 = 0;
-  if (FE == 1) {
-    x_b = p.x + t.lb * (size_t)p.C;
-    cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
+  {
     const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
     // Every wave issues the same loads (no branch, so nothing waits on them early);
     // waves 2 and 3 read their one channel twice, wave 3's values go unused.
@@ -367,10 +451,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
       xr[1][j] = *xp_addr(x_b, cin_b, p.C, c1, j);
       wr[1][j] = w_l[(size_t)j * p.C + c1];
     }
-  } else {
-    // thread i stages q[i] (i < 128) or k[i - 128]; threads < 64 also the tile's v rows
-    fe_raw = qkv_raw(tid < kD ? p.q : p.k, (row0 * p.Hk + t.g) * kD + (tid & (kD - 1)), p.qkv_bf16);
-    if (tid < kTileRows) v_raw = qkv_raw(p.v, (row0 * p.Hv + t.h) * kD + t.r0 + tid, p.qkv_bf16);
   }
   // 2. the tile's state; then the gate inputs, which only wave 3 waits for
   f4v s[SLOTS][2];
@@ -380,34 +460,27 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   __builtin_amdgcn_sched_barrier(0);  // keep the front-end arithmetic below the loads
 
   // 3. front-end arithmetic while the state is in flight
-  if (FE == 1) {
-    if (wave < 3) {
-      float u[2];
+  if (wave < 3) {
+    float u[2];
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        float xv[kTaps], wv[kTaps];
+    for (int m = 0; m < 2; ++m) {
+      float xv[kTaps], wv[kTaps];
 #pragma unroll
-        for (int j = 0; j < kTaps; ++j) {
-          xv[j] = xp_value(xr[m][j], cin_b, j);
-          wv[j] = bf2f((uint16_t)wr[m][j]);
-        }
-        u[m] = silu_bf(conv4(xv, wv));
+      for (int j = 0; j < kTaps; ++j) {
+        xv[j] = xp_value(xr[m][j], cin_b, j);
+        wv[j] = bf2f((uint16_t)wr[m][j]);
       }
-      if (wave < 2) {
-        float y0, y1;
-        l2norm_pair(u[0], u[1], wave == 0, y0, y1);
-        float* dst = wave == 0 ? sm_q : sm_k;
-        dst[lane] = y0;
-        dst[lane + 64] = y1;
-      } else if (lane < kTileRows) {
-        sm_v[lane] = u[0];
-      }
+      u[m] = silu_bf(conv4(xv, wv));
     }
-  } else {
-    const float val = qkv_value(fe_raw, p.qkv_bf16);
-    if (tid < kD) sm_q[tid] = val;
-    else sm_k[tid - kD] = val;
-    if (tid < kTileRows) sm_v[tid] = qkv_value(v_raw, p.qkv_bf16);
+    if (wave < 2) {
+      float y0, y1;
+      l2norm_pair(u[0], u[1], wave == 0, y0, y1);
+      float* dst = wave == 0 ? sm_q : sm_k;
+      dst[lane] = y0;
+      dst[lane + 64] = y1;
+    } else if (lane < kTileRows) {
+      sm_v[lane] = u[0];
+    }
   }
   if (wave == 3) {
     float al, be;
@@ -426,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   // 5. conv state hand-off from the rows already in registers: new rows 0..2 are xp
   // rows 1..3. This tile's v channels; the q (tile 0) or k (tile 1) channels of the
   // k-head when h is its k-head's first v-head -- every channel has one writer.
-  if (FE == 1 && p.conv_out) {
+  if (p.conv_out) {
     uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
     const bool qk_writer = (t.h % p.rep) == 0 && wave == t.tile;
     const int nm = wave == 2 ? (lane < kTileRows ? 1 : 0) : (wave < 2 && qk_writer ? 2 : 0);
@@ -634,8 +707,9 @@ template <int SLOTS>
 void launch_slots(const RecurrentParams& p, int frontend, bool collect, hipStream_t stream) {
   const dim3 grid(p.nblocks), block(kThreads);
   if (p.T == 1 && !collect) {
-    if (frontend == 0) hipLaunchKernelGGL((decode_kernel<SLOTS, 0>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((decode_kernel<SLOTS, 1>), grid, block, 0, stream, p);
+    if (frontend == 1) hipLaunchKernelGGL((decode_kernel<SLOTS>), grid, block, 0, stream, p);
+    else if (p.state_in) hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, false>), grid, block, 0, stream, p);
   } else if (frontend == 0) {
     launch_steps<SLOTS, 0>(p, collect, grid, block, stream);
   } else {
