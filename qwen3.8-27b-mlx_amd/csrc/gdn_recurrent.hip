@@ -351,8 +351,9 @@ __device__ __forceinline__ int fe_channel(const RecurrentParams& p, const Tile& 
 // q, k, v given (the reference's delta::run inputs): every lane loads its own elements of
 // q and k and its slots' v values, and every wave does the gate math, so there is no LDS
 // staging and no barrier; with the state present there is no branch around any load, so
-// nothing but the step itself waits for the state.
-template <int SLOTS, bool HAS_STATE>
+// nothing but the step itself waits for the state. VEC: q and k aligned to 4 elements, read
+// 4 elements per load (else one element per load).
+template <int SLOTS, bool HAS_STATE, bool VEC>
 __global__ __launch_bounds__(kThreads) void decode_qkv_kernel(RecurrentParams p) {
   typedef int i2v __attribute__((ext_vector_type(2)));
   const Tile t = decode_block<SLOTS>(p);
@@ -364,7 +365,22 @@ __global__ __launch_bounds__(kThreads) void decode_qkv_kernel(RecurrentParams p)
   // 1. loads: q and k raw (bf16 pairs or fp32), v of the slots' rows, gates, the state
   i4v qr[2], kr[2];
   const size_t qkb = (row0 * p.Hk + t.g) * kD + 4 * j16;
-  if (p.qkv_bf16) {
+  if constexpr (!VEC) {
+    // element by element, packed as the vector loads would leave them
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      uint32_t qe[4], ke[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qe[e] = qkv_raw(p.q, qkb + 64 * h2 + e, p.qkv_bf16);
+        ke[e] = qkv_raw(p.k, qkb + 64 * h2 + e, p.qkv_bf16);
+      }
+      qr[h2] = p.qkv_bf16 ? i4v{(int)(qe[0] | qe[1] << 16), (int)(qe[2] | qe[3] << 16), 0, 0}
+                          : i4v{(int)qe[0], (int)qe[1], (int)qe[2], (int)qe[3]};
+      kr[h2] = p.qkv_bf16 ? i4v{(int)(ke[0] | ke[1] << 16), (int)(ke[2] | ke[3] << 16), 0, 0}
+                          : i4v{(int)ke[0], (int)ke[1], (int)ke[2], (int)ke[3]};
+    }
+  } else if (p.qkv_bf16) {
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       const i2v a = *reinterpret_cast<const i2v*>(static_cast<const uint16_t*>(p.q) + qkb + 64 * h2);
@@ -707,9 +723,13 @@ template <int SLOTS>
 void launch_slots(const RecurrentParams& p, int frontend, bool collect, hipStream_t stream) {
   const dim3 grid(p.nblocks), block(kThreads);
   if (p.T == 1 && !collect) {
+    const uintptr_t vec = p.qkv_bf16 ? 8 : 16;  // 4 elements
+    const bool aligned = (reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k)) % vec == 0;
     if (frontend == 1) hipLaunchKernelGGL((decode_kernel<SLOTS>), grid, block, 0, stream, p);
-    else if (p.state_in) hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, false>), grid, block, 0, stream, p);
+    else if (p.state_in && aligned) hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, true, true>), grid, block, 0, stream, p);
+    else if (p.state_in) hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, true, false>), grid, block, 0, stream, p);
+    else if (aligned) hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, false, false>), grid, block, 0, stream, p);
   } else if (frontend == 0) {
     launch_steps<SLOTS, 0>(p, collect, grid, block, stream);
   } else {

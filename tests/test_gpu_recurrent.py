@@ -14,12 +14,13 @@ Tolerances (written here, from the task statement):
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import numpy as np
 import pytest
 
-from _util import log_case, to_dev, to_np
+from _util import bf16_to_f32, log_case, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -112,6 +113,42 @@ def test_decode_single_layer_qkv(O, gdn, dev, o_dtype):
     check_state(O, out["state"][0], ref["state"], "state")
     check_o(O, out["o"][0], ref["o"], o_dtype, "o")
     assert np.array_equal(out["state_in_after"][0], inp.state)  # out of place: input untouched
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_decode_qkv_element_aligned_views(O, gdn, dev, dtype):
+    """q, k, v one element past an aligned address (aligned to their element size only, which
+    the ABI allows): decode reads q and k element by element then, and must give the same
+    bits as from aligned buffers, and the oracle's result within tolerance."""
+    import torch
+    log_case(f"decode 1 layer B=2 qkv {dtype}, views at an odd element offset")
+    base = O.make_inputs(config=0, layer=5, B=2, L=1)
+    ref = O.reference_layer(base)
+    inp = base if dtype == "bf16" else dataclasses.replace(
+        base, q=bf16_to_f32(base.q), k=bf16_to_f32(base.k), v=bf16_to_f32(base.v))
+    aligned = run_layers(gdn, dev, [inp], o_dtype="f32")
+
+    def odd_view(a):
+        flat = to_dev(np.ascontiguousarray(a[None]).reshape(-1), dev)
+        buf = torch.zeros(flat.numel() + 1, dtype=flat.dtype, device=dev)
+        buf[1:] = flat
+        return buf[1:].view((1,) + a.shape)
+
+    q, k, v = odd_view(inp.q), odd_view(inp.k), odd_view(inp.v)
+    assert q.data_ptr() % (16 if dtype == "f32" else 8) != 0
+    B, Hv = inp.q.shape[0], inp.A_log.size
+    st = to_dev(inp.state[None], dev)
+    state_out = torch.full_like(st, float("nan"))
+    o = torch.empty((1, B, 1, Hv, D), dtype=torch.float32, device=dev)
+    args = gdn.layer_args(B=B, T=1, n_layers=1, q=q, k=k, v=v, a=to_dev(inp.a[None], dev),
+                          b=to_dev(inp.b[None], dev), A_log=to_dev(inp.A_log[None], dev),
+                          dt_bias=to_dev(inp.dt_bias[None], dev), state_in=st, state_out=state_out, o=o)
+    gdn.call_run(args)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(state_out)[0], aligned["state"][0])
+    assert np.array_equal(to_np(o)[0], aligned["o"][0])
+    check_state(O, to_np(state_out)[0], ref["state"], "state")
+    check_o(O, to_np(o)[0], ref["o"], "f32", "o")
 
 
 def test_decode_48_layers_conv(O, gdn, dev):
