@@ -400,7 +400,10 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
 
 // q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output.
 // ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
-// dead after the first group).
+// dead after the first group). Everything it writes for the scan (Q, K^T, M, U, W: 224 MB at
+// T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
+// scan that reads it back. (The front end's outputs, which this kernel reads, stay
+// cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
 template <bool ONE_GROUP>
 __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) IntraSmem s;
@@ -454,7 +457,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) {
-      *reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag) = frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg);
+      __builtin_nontemporal_store(frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg),
+                                  reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
     }
     const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
@@ -473,7 +477,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int a = 2 * wave + a2;
-        *reinterpret_cast<bf8*>(wkt + (a * 2 + ks) * kFrag) = frag_ilv(s.kt, 16 * a + fr, 32 * ks, lg);
+        __builtin_nontemporal_store(frag_ilv(s.kt, 16 * a + fr, 32 * ks, lg),
+                                    reinterpret_cast<bf8*>(wkt + (a * 2 + ks) * kFrag));
       }
   }
 
@@ -536,8 +541,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         const int off = ilv_off(i, j0, 2);
         const int blk = off / kFrag, within = off % kFrag;
         if (ct >= 2 || wave < 2) {
-          *reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within) = hi;
-          *reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within) = lo;
+          __builtin_nontemporal_store(hi, reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within));
+          __builtin_nontemporal_store(lo, reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within));
         }
       }
     }
@@ -600,7 +605,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           acc = mfma(al[0], vb[d][0], acc);
           acc = mfma(ah[1], vb[d][1], acc);
           acc = mfma(al[1], vb[d][1], acc);
-          *reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256) = acc;
+          __builtin_nontemporal_store(acc, reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256));
         }
         // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]
         __bf16* ww = p.ws_w + hc * kChunkElems;
@@ -610,7 +615,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           f4 acc = {0.f, 0.f, 0.f, 0.f};
           acc = mfma(k0, te[0], acc);
           acc = mfma(k1, te[1], acc);
-          *reinterpret_cast<bf4*>(ww + ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32)) = to_bf4(acc);
+          __builtin_nontemporal_store(to_bf4(acc),
+                                      reinterpret_cast<bf4*>(ww + ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32)));
         }
       }
     }
