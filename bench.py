@@ -218,31 +218,45 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
     intra, inter = prefill_flops(T)
     sec = r["ms_per_step"] * 1e-3
     traffic = load_traffic("prefill_t4096_b1_conv") if T == 4096 else None
+    # each kernel between its own event pair (gdn_prefill_chunked_timed; outside the timed
+    # region above: every such call waits for its events)
+    per = [gdn.call_prefill_timed(args) for _ in range(max(steps, 10))]
+    event_us = [sorted(p[i] for p in per)[len(per) // 2] * 1e3 for i in range(3)]
     return dict(tokens_per_s=T / sec, us_per_call=r["ms_per_step"] * 1e3,
                 intra_TFLOPs=intra / sec / 1e12,
                 intra_frac_mfma=intra / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 all_products_frac_mfma=(intra + inter) / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 intra_flop=intra, inter_flop=inter,
                 hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9,
-                per_kernel=prefill_kernel_fracs() if T == 4096 else None)
+                per_kernel=prefill_kernel_fracs(event_us) if T == 4096 else None)
 
 
-def prefill_kernel_fracs():
-    """MFMA fraction of each prefill kernel alone, from the committed rocprofv3 kernel trace
-    (durations) and counter run (executed MFMA FLOPs, busy cycles): normative FLOPs and
-    executed FLOPs over the kernel's own duration, against the dense bf16 peak."""
+def prefill_kernel_fracs(event_us=None):
+    """MFMA fraction of each prefill kernel alone: its normative and executed MFMA FLOPs
+    (from the committed counter run) over its own duration, against the dense bf16 peak --
+    the duration measured in this run between the kernel's own event pair (event_us: front
+    end, intra, scan, from gdn_prefill_chunked_timed) and, beside it, the committed
+    rocprofv3 kernel-trace average with the busy-cycle counter."""
     path = os.path.join(ROOT, "profiles", "prefill_kernels.json")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
         ks = json.load(fh)["kernels"]
     peak = MFMA_BF16_PEAK_TFLOPS * 1e12
+    order = ("prefill_frontend_kernel", "prefill_intra_kernel", "prefill_scan_kernel")
     out = {}
-    for name, k in ks.items():
+    for i, name in enumerate(order):
+        k = ks[name]
         s = k["avg_us"] * 1e-6
-        out[name] = dict(avg_us=k["avg_us"], frac_mfma_normative=round(k["normative_flop"] / s / peak, 4),
-                         frac_mfma_executed=round(k["executed_mfma_flop"] / s / peak, 4),
-                         mfma_busy_counter=k["mfma_busy"])
+        d = dict(avg_us=k["avg_us"], frac_mfma_normative=round(k["normative_flop"] / s / peak, 4),
+                 frac_mfma_executed=round(k["executed_mfma_flop"] / s / peak, 4),
+                 mfma_busy_counter=k["mfma_busy"])
+        if event_us is not None:
+            se = event_us[i] * 1e-6
+            d.update(event_us=round(event_us[i], 2),
+                     frac_mfma_normative_event=round(k["normative_flop"] / se / peak, 4),
+                     frac_mfma_executed_event=round(k["executed_mfma_flop"] / se / peak, 4))
+        out[name] = d
     return out
 
 
@@ -502,6 +516,13 @@ def main() -> int:
         hbm = "" if r["hbm_GBps"] is None else f", HBM {r['hbm_GBps']:.0f} GB/s (counted bytes)"
         print(f"# prefill T=4096: {r['us_per_call']:.1f} us, {r['tokens_per_s'] / 1e6:.2f} M tok/s, "
               f"intra MFMA frac {r['intra_frac_mfma']:.4f}{hbm}", flush=True)
+        pk = r["per_kernel"]
+        if pk and "event_us" in pk["prefill_intra_kernel"]:
+            ki, ks = pk["prefill_intra_kernel"], pk["prefill_scan_kernel"]
+            print(f"# prefill kernels (events): front end {pk['prefill_frontend_kernel']['event_us']:.1f} us, "
+                  f"intra {ki['event_us']:.1f} us (MFMA {ki['frac_mfma_normative_event']:.4f} normative, "
+                  f"{ki['frac_mfma_executed_event']:.4f} executed), scan {ks['event_us']:.1f} us "
+                  f"({ks['frac_mfma_executed_event']:.4f} executed)", flush=True)
     for which in ("in_proj", "out_proj"):
         if want(which):
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 3
+#define GDN_ABI_VERSION 4
 #define GDN_HEAD_DIM 128 /* Dk = Dv */
 #define GDN_CONV_TAPS 4  /* conv kernel size; the conv state holds GDN_CONV_TAPS-1 rows */
 
@@ -139,6 +139,14 @@ int gdn_run(const gdn_layer_args* args);
  * the state hand-off between chunks stays fp32. The workspace contents are scratch: they
  * need no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);
+
+/* gdn_prefill_chunked with a HIP event recorded before its first kernel and after each of
+ * its three (the front end, the intra-chunk products, the chunk scan); it waits for the
+ * last event and writes the kernels' durations in milliseconds to kernel_ms[0..2] (zeros
+ * when nothing is launched). For measurement: unlike every other entry point it creates
+ * events and waits for the stream. No counterpart in the reference (its callers are
+ * benchmarks that report each kernel's share of the MFMA peak). */
+int gdn_prefill_chunked_timed(const gdn_layer_args* args, float* kernel_ms);
 
 /* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
  * counts and front end (the conv front end also stages its bf16 q, k in the workspace);

@@ -17,7 +17,8 @@
 namespace gdn {
 int recurrent_tile_rows(long long heads);
 size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv);
-hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream);
+hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
+                                  hipEvent_t* events);
 }  // namespace gdn
 
 namespace {
@@ -349,7 +350,10 @@ int gdn_prefill_workspace_size(const gdn_layer_args* a, size_t* bytes) {
   return ok();
 }
 
-int gdn_prefill_chunked(const gdn_layer_args* a) {
+namespace {
+
+// The argument checks of gdn_prefill_chunked (no HIP call).
+int prefill_validate(const gdn_layer_args* a) {
   int rc = validate_layer(a, "gdn_prefill_chunked", false);
   if (rc != GDN_OK) return rc;
   if (a->batch == 0) return ok();
@@ -401,13 +405,53 @@ int gdn_prefill_chunked(const gdn_layer_args* a) {
       if (overlap(ws, range_of(buf.p, buf.bytes)))
         return fail(GDN_EINVAL, "gdn_prefill_chunked: the workspace must not overlap %s", buf.name);
   }
-  rc = check_device();
+  return ok();
+}
+
+// The launches of gdn_prefill_chunked for validated arguments; with `events` (four, when
+// the call launches the three kernels), an event is recorded before the first kernel and
+// after each.
+int prefill_launch(const gdn_layer_args* a, hipEvent_t* events) {
+  if (a->batch == 0) return ok();
+  int rc = check_device();
   if (rc != GDN_OK) return rc;
   hipStream_t stream = static_cast<hipStream_t>(a->stream);
   if (a->seq_len == 0) return run_empty(a, stream);
-  hipError_t e = gdn::launch_chunked_prefill(*a, a->workspace, stream);
+  hipError_t e = gdn::launch_chunked_prefill(*a, a->workspace, stream, events);
   if (e != hipSuccess) return hip_fail(e, "gdn_prefill_chunked launch");
   return ok();
+}
+
+}  // namespace
+
+int gdn_prefill_chunked(const gdn_layer_args* a) {
+  const int rc = prefill_validate(a);
+  return rc != GDN_OK ? rc : prefill_launch(a, nullptr);
+}
+
+int gdn_prefill_chunked_timed(const gdn_layer_args* a, float* kernel_ms) {
+  if (!kernel_ms) return fail(GDN_EINVAL, "gdn_prefill_chunked_timed: kernel_ms is NULL");
+  for (int i = 0; i < 3; ++i) kernel_ms[i] = 0.0f;
+  int rc = prefill_validate(a);
+  if (rc != GDN_OK) return rc;
+  if (a->batch == 0 || a->seq_len == 0) return prefill_launch(a, nullptr);
+  rc = check_device();
+  if (rc != GDN_OK) return rc;
+  hipEvent_t ev[4] = {};
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e = hipEventCreate(&ev[i]);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      return hip_fail(e, "gdn_prefill_chunked_timed: hipEventCreate");
+    }
+  }
+  rc = prefill_launch(a, ev);
+  hipError_t e = hipSuccess;
+  if (rc == GDN_OK) e = hipEventSynchronize(ev[3]);
+  for (int i = 0; rc == GDN_OK && e == hipSuccess && i < 3; ++i) e = hipEventElapsedTime(&kernel_ms[i], ev[i], ev[i + 1]);
+  for (int i = 0; i < 4; ++i) (void)hipEventDestroy(ev[i]);
+  if (rc == GDN_OK && e != hipSuccess) return hip_fail(e, "gdn_prefill_chunked_timed: events");
+  return rc;
 }
 
 int gdn_commit(const gdn_commit_args* a) {

@@ -1106,7 +1106,8 @@ size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv) {
   return workspace_layout(B, T, Hk, Hv, conv).total;
 }
 
-hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream) {
+hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
+                                  hipEvent_t* events) {
   PrefillParams p{};
   p.B = a.batch;
   p.T = a.seq_len;
@@ -1152,6 +1153,11 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   const dim3 block(kThreads);
   const dim3 g1((unsigned)((size_t)p.B * p.Hk * p.nC));
   const dim3 g2((unsigned)((size_t)p.B * p.Hv * kScanGroups));
+  // events[0..3] (when given) are recorded before the first kernel and after each
+  auto mark = [&](int i) {
+    if (events) (void)hipEventRecord(events[i], stream);
+  };
+  mark(0);
   if (conv) {
     const size_t nh = ((size_t)2 * p.Hk + p.Hv + kFeHeads - 1) / kFeHeads;
     const dim3 g0((unsigned)((size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
@@ -1160,16 +1166,19 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
     const dim3 gv((unsigned)((size_t)p.B * p.Hv * p.nC));
     hipLaunchKernelGGL(prefill_vfrag_kernel, gv, block, 0, stream, p);
   }
+  mark(1);
   if (p.rep <= kGroup) {
     hipLaunchKernelGGL((prefill_intra_kernel<true>), g1, block, 0, stream, p);
   } else {
     hipLaunchKernelGGL((prefill_intra_kernel<false>), g1, block, 0, stream, p);
   }
+  mark(2);
   if (p.o_bf16) {
     hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
   } else {
     hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
   }
+  mark(3);
   return hipGetLastError();
 }
 

@@ -45,7 +45,7 @@ QLINEAR_GEMV_ROWS = 4
 QLINEAR_MAX_ROWS = 4096
 QLINEAR_NOALLOC_SCRATCH_BYTES = 8 << 20
 
-EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
+EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_chunked_timed", "gdn_prefill_workspace_size", "gdn_commit",
            "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_qlinear_noalloc", "gdn_available",
            "gdn_abi_version", "gdn_last_error")
 
@@ -121,6 +121,8 @@ def lib() -> ctypes.CDLL:
         L.gdn_run.restype = _int
         L.gdn_prefill_chunked.argtypes = [ctypes.POINTER(LayerArgs)]
         L.gdn_prefill_chunked.restype = _int
+        L.gdn_prefill_chunked_timed.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(ctypes.c_float)]
+        L.gdn_prefill_chunked_timed.restype = _int
         L.gdn_prefill_workspace_size.argtypes = [ctypes.POINTER(LayerArgs), ctypes.POINTER(ctypes.c_size_t)]
         L.gdn_prefill_workspace_size.restype = _int
         L.gdn_commit.argtypes = [ctypes.POINTER(CommitArgs)]
@@ -161,6 +163,14 @@ def call_run(args: LayerArgs) -> None:
 
 def call_prefill(args: LayerArgs) -> None:
     _check(lib().gdn_prefill_chunked(ctypes.byref(args)))
+
+
+def call_prefill_timed(args: LayerArgs) -> tuple:
+    """gdn_prefill_chunked_timed: runs the chunked prefill, waits for it and returns the
+    durations (ms) of its front-end, intra-chunk and scan kernels."""
+    ms = (ctypes.c_float * 3)()
+    _check(lib().gdn_prefill_chunked_timed(ctypes.byref(args), ms))
+    return tuple(ms)
 
 
 def call_commit(args: CommitArgs) -> None:

@@ -21,7 +21,7 @@ def declared_functions():
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(
-        ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_workspace_size", "gdn_commit",
+        ["gdn_run", "gdn_prefill_chunked", "gdn_prefill_chunked_timed", "gdn_prefill_workspace_size", "gdn_commit",
          "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_qlinear_noalloc", "gdn_available",
          "gdn_abi_version", "gdn_last_error"])
 
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(gdn):
                          text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s+(gdn_\w+)", out))
     assert set(declared_functions()) <= exported
-    assert L.gdn_abi_version() == 3
+    assert L.gdn_abi_version() == 4
     assert set(gdn.EXPORTS) == set(declared_functions())
 
 
@@ -172,6 +172,13 @@ def test_null_args_and_prefill_states(gdn):
     L = gdn.lib()
     assert L.gdn_run(None) == gdn.GDN_EINVAL and "NULL" in gdn.last_error()
     assert L.gdn_prefill_chunked(None) == gdn.GDN_EINVAL
+    ms = (ctypes.c_float * 3)(1.0, 1.0, 1.0)
+    assert L.gdn_prefill_chunked_timed(None, ms) == gdn.GDN_EINVAL and list(ms) == [0.0, 0.0, 0.0]
+    assert L.gdn_prefill_chunked_timed(ctypes.byref(_args(gdn, seq_len=100)), None) == gdn.GDN_EINVAL
+    assert "kernel_ms" in gdn.last_error()
+    # the timed form checks its arguments as the plain one does, before any HIP call
+    rc = L.gdn_prefill_chunked_timed(ctypes.byref(_args(gdn, seq_len=100)), ms)
+    assert rc == gdn.GDN_EINVAL and "workspace" in gdn.last_error(), gdn.last_error()
     assert L.gdn_commit(None) == gdn.GDN_EINVAL
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, states=0x9000000 * 4)))
     assert rc == gdn.GDN_EINVAL and "per-step states" in gdn.last_error()

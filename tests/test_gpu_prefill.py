@@ -224,3 +224,29 @@ def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
     bad = int((v_got != v_want).sum())
     print(f"  {finite.size} finite inputs, mismatches {bad}", flush=True)
     assert bad == 0
+
+
+def test_prefill_timed_equals_untimed(O, gdn, dev):
+    """gdn_prefill_chunked_timed runs the same kernels as gdn_prefill_chunked (identical
+    outputs) and reports three positive kernel durations."""
+    import torch
+    log_case("prefill timed vs untimed, T=300 conv")
+    T = 300
+    inp = O.make_inputs(config=4, layer=7, B=1, L=T, conv=True, conv_state=False, zero_state=True)
+    d = lambda a: to_dev(a, dev)  # noqa: E731
+    outs = []
+    for timed in (False, True):
+        o = torch.empty((1, T, 48, D), dtype=torch.bfloat16, device=dev)
+        st = torch.empty((1, 48, D, D), device=dev)
+        ws = torch.empty(gdn.prefill_workspace_size(1, T), dtype=torch.uint8, device=dev)
+        args = gdn.layer_args(B=1, T=T, x=d(inp.x), conv_weight=d(inp.conv_w), a=d(inp.a), b=d(inp.b),
+                              A_log=d(inp.A_log), dt_bias=d(inp.dt_bias), state_out=st, o=o, workspace=ws)
+        if timed:
+            ms = gdn.call_prefill_timed(args)
+            print(f"  kernel ms {ms}", flush=True)
+            assert len(ms) == 3 and all(m > 0 for m in ms), ms
+        else:
+            gdn.call_prefill(args)
+        torch.cuda.synchronize()
+        outs.append((o.clone(), st.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
