@@ -353,17 +353,19 @@ def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
     return dict(GBps=2 * n * 4 / (r["ms_per_step"] * 1e-3) / 1e9, bytes=2 * n * 4)
 
 
-def stream_ceilings(torch, dev, timer, steps: int):
+def stream_ceilings(torch, dev, timer, steps: int, b32: bool = False):
     """Plain memory streams with the decode and verify state traffic's shapes (libgdn_probe.so,
     no arithmetic): the decode step's 4,608 tiles of 32 KB read and written back in place,
     and verify's 768 tiles read once and written 5 times, each rotated over 8 buffer sets
-    as the kernels' lines are. The kernels' rates are read against these."""
+    as the kernels' lines are; with b32, the B=32 step's 147,456 tiles over 2 sets. The
+    kernels' rates are read against these."""
     import ctypes
     path = os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "libgdn_probe.so")
     if not os.path.exists(path):
         return None
     L = ctypes.CDLL(path)
     L.gdn_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    L.gdn_probe_rmw_split.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     L.gdn_probe_read_write_t.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_void_p]
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
@@ -376,6 +378,18 @@ def stream_ceilings(torch, dev, timer, steps: int):
     out["decode_shape_rmw_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
                                           GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=nbytes)
     del bufs
+    if b32:
+        # the B=32 step's state traffic: 147,456 tiles (4.8 GB) over 2 sets, as its bench line,
+        # in dispatch order and split into a contiguous eighth per XCD (the kernel's order)
+        nb = 32 * nd
+        bufs = [torch.empty(nb * tile, device=dev).uniform_() for _ in range(2)]
+        nbytes = 2 * nb * tile * 4
+        for key, fn in (("decode_b32_shape_rmw_stream", L.gdn_probe_rmw),
+                        ("decode_b32_shape_rmw_stream_split", L.gdn_probe_rmw_split)):
+            r = timer.time_calls(lambda it: fn(bufs[it % 2].data_ptr(), nb, st()), max(10, steps // 2), 3)
+            out[key] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                            GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=nbytes)
+        del bufs
     nv, T = 8 * HV * 2, 5  # verify: B=8 x 48 heads x two tiles, 5 per-step states
     src = [torch.randn(nv * tile, device=dev) for _ in range(8)]
     dst = [torch.empty(nv * T * tile, device=dev) for _ in range(8)]
@@ -550,16 +564,23 @@ def main() -> int:
         cc = bench_copy_ceiling(torch, dev, timer)
         sec["copy_ceiling_GBps"] = round(cc["GBps"], 1)
         print(f"# device copy ceiling: {cc['GBps']:.0f} GB/s", flush=True)
-        sc = stream_ceilings(torch, dev, timer, steps=max(20, args.steps // 2))
+        sc = stream_ceilings(torch, dev, timer, steps=max(20, args.steps // 2), b32="decode_b32_48_layers" in sec)
         if sc is not None:
             sec["stream_ceilings"] = sc
             if head is not None:
                 sc["decode_vs_rmw_stream"] = round(head["GBps"] / sc["decode_shape_rmw_stream"]["GBps"], 4)
             if "verify_b8_t5" in sec:
                 sc["verify_vs_stream"] = round(sec["verify_b8_t5"]["GBps"] / sc["verify_shape_stream"]["GBps"], 4)
+            if "decode_b32_shape_rmw_stream" in sc:
+                best = max(sc["decode_b32_shape_rmw_stream"]["GBps"], sc["decode_b32_shape_rmw_stream_split"]["GBps"])
+                sc["decode_b32_vs_rmw_stream"] = round(sec["decode_b32_48_layers"]["GBps"] / best, 4)
             print(f"# same-shape streams: decode RMW {sc['decode_shape_rmw_stream']['us']:.1f} us "
                   f"({sc['decode_shape_rmw_stream']['GBps']:.0f} GB/s), verify "
                   f"{sc['verify_shape_stream']['us']:.1f} us ({sc['verify_shape_stream']['GBps']:.0f} GB/s)", flush=True)
+            if "decode_b32_shape_rmw_stream" in sc:
+                b, b2 = sc["decode_b32_shape_rmw_stream"], sc["decode_b32_shape_rmw_stream_split"]
+                print(f"# same-shape streams: B=32 decode RMW {b['us'] / 1e3:.3f} ms ({b['GBps']:.0f} GB/s) in "
+                      f"dispatch order, {b2['us'] / 1e3:.3f} ms ({b2['GBps']:.0f} GB/s) split per XCD", flush=True)
 
     if head is None:
         print(json.dumps({"secondary": sec}))
