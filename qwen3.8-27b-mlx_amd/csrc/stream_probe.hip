@@ -14,10 +14,18 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // tile size: the compiler then stores each float4 as soon as its load has landed, which
 // streams faster here (48.2 us for the decode step's 302 MB of state) than the same kernel
 // with the size a constant, where it holds the stores back behind later loads (50.1 us).
-__global__ __launch_bounds__(256) void rmw_tile_kernel(f4* buf, int64_t per, float a, int split) {
-  // split: each XCD (workgroups are dispatched to the 8 XCDs round robin) takes one
-  // contiguous eighth of the tiles, the order the decode kernel uses for large grids
-  const int tile = split ? (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3)) : (int)blockIdx.x;
+__global__ __launch_bounds__(256) void rmw_tile_kernel(f4* buf, int64_t per, float a, int split, int group) {
+  // Workgroups are dispatched to the 8 XCDs round robin. split: each XCD takes one
+  // contiguous eighth of the tiles (the decode kernel's order for large grids); group > 0:
+  // groups of `group` consecutive tiles go to the XCDs in turn, dispatch id
+  // 8 group s + 8 j + x being tile j of group 8 s + x (its order for smaller grids)
+  int tile = (int)blockIdx.x;
+  if (split) {
+    tile = (int)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3));
+  } else if (group > 0) {
+    const int s = tile / (8 * group), r = tile % (8 * group);
+    tile = group * (8 * s + (r & 7)) + (r >> 3);
+  }
   f4* base = buf + (int64_t)tile * per;
   const int64_t per_thread = per / 256;
   f4 v[8];
@@ -54,14 +62,22 @@ __global__ __launch_bounds__(256) void read_write_t_kernel(const f4* src, f4* ds
 // buf: tiles x 32 KB (16-byte aligned); returns a hipError_t.
 extern "C" int gdn_probe_rmw(void* buf, int tiles, void* stream) {
   if (!buf || tiles < 1) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f, 0);
+  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f, 0, 0);
+  return (int)hipGetLastError();
+}
+
+// The same in groups of `group` consecutive tiles per XCD turn (tiles % (8 group) == 0).
+extern "C" int gdn_probe_rmw_groups(void* buf, int tiles, int group, void* stream) {
+  if (!buf || group < 1 || tiles < 8 * group || tiles % (8 * group)) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f, 0,
+                     group);
   return (int)hipGetLastError();
 }
 
 // The same with each XCD streaming one contiguous eighth of the tiles (tiles % 8 == 0).
 extern "C" int gdn_probe_rmw_split(void* buf, int tiles, void* stream) {
   if (!buf || tiles < 8 || tiles % 8) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f, 1);
+  hipLaunchKernelGGL(rmw_tile_kernel, dim3(tiles), dim3(256), 0, (hipStream_t)stream, (f4*)buf, (int64_t)2048, 1.0001f, 1, 0);
   return (int)hipGetLastError();
 }
 
