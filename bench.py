@@ -408,16 +408,33 @@ def stream_ceilings(torch, dev, timer, steps: int, b32: bool = False):
 
 def launch_floors(torch, dev, timer, steps: int):
     """What a one-layer launch cannot beat, timed the same way: a one-element kernel (the
-    launch itself) and a device copy of one layer's 3.1 MB state (3.1 MB read + 3.1 MB
-    written), each back to back over rotating buffers."""
+    launch itself), a device copy of one layer's 3.1 MB state (3.1 MB read + 3.1 MB
+    written), and the same state read and written back in place by the decode kernel's
+    one-layer grid (384 workgroups of 16-row tiles in its XCD order, libgdn_probe.so),
+    each back to back over rotating buffers."""
     one = torch.zeros(1, device=dev)
     r = timer.time_calls(lambda it: one.add_(1), steps, 20)
     n = HV * D * D
     src = [torch.randn(n, device=dev) for _ in range(48)]
     dst = [torch.empty(n, device=dev) for _ in range(48)]
     c = timer.time_calls(lambda it: dst[it % 48].copy_(src[it % 48]), steps, 20)
-    return dict(empty_kernel_us=round(r["ms_per_step"] * 1e3, 2),
-                copy_one_layer_state_us=round(c["ms_per_step"] * 1e3, 2))
+    out = dict(empty_kernel_us=round(r["ms_per_step"] * 1e3, 2),
+               copy_one_layer_state_us=round(c["ms_per_step"] * 1e3, 2))
+    del src, dst
+    path = os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "libgdn_probe.so")
+    if os.path.exists(path):
+        import ctypes
+        L = ctypes.CDLL(path)
+        L.gdn_probe_rmw_small.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        tiles, group = HV * (D // 16), (HV // HK) * (D // 16)  # 384 tiles of 8 KB, 24 per k-head
+        bufs = [torch.randn(n, device=dev) for _ in range(96)]
+        st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+        if L.gdn_probe_rmw_small(bufs[0].data_ptr(), tiles, group, st()) != 0:
+            raise RuntimeError("gdn_probe_rmw_small failed")
+        m = timer.time_calls(lambda it: L.gdn_probe_rmw_small(bufs[it % 96].data_ptr(), tiles, group, st()),
+                             steps, 20)
+        out["rmw_one_layer_state_us"] = round(m["ms_per_step"] * 1e3, 2)
+    return out
 
 
 def cpu_baseline(target_seconds: float = 12.0):

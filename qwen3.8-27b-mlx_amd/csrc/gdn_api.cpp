@@ -318,20 +318,37 @@ int gdn_run(const gdn_layer_args* a) {
   // measured faster from B = 8 at 48 layers (36,864 workgroups: 407 vs 418 us; B = 16: 821
   // vs 865 us) and slower for smaller ones (B = 1 over 8 state sets: 56.2 vs 53.2 us), which
   // interleave k-head groups over the XCDs instead (B = 1: 53.6 -> 52.9 us).
-  p.remap = (nblocks % 8) == 0 && nblocks > 16384;
-  p.q = a->q;
-  p.k = a->k;
-  p.v = a->v;
-  p.x = static_cast<const uint16_t*>(a->x);
-  p.conv_w = static_cast<const uint16_t*>(a->conv_weight);
-  p.conv_in = static_cast<const uint16_t*>(a->conv_state_in);
-  p.conv_out = static_cast<uint16_t*>(a->conv_state_out);
-  p.a = static_cast<const uint16_t*>(a->a);
-  p.b = static_cast<const uint16_t*>(a->b);
-  p.A_log = a->A_log;
-  p.dt_bias = a->dt_bias;
-  p.alpha = a->alpha;
-  p.beta = a->beta;
+  const bool split = (nblocks % 8) == 0 && nblocks > 16384;
+  const int64_t grp8 = 8 * (int64_t)p.rep * tiles;  // workgroups of 8 k-heads
+  p.order = split ? 1 : (nblocks % grp8 == 0 ? 2 : 0);
+  // The block map's quotients n / d (n < nblocks) as multiply-highs by ceil(2^32 / d): exact
+  // when n d <= 2^32 (the error n (d ceil(2^32 / d) - 2^32) / d 2^32 stays below 1 / d).
+  auto recip = [](int64_t d) -> uint32_t { return d == 1 ? 0u : (uint32_t)(((1ull << 32) + d - 1) / d); };
+  const int64_t dmax = std::max(std::max(grp8, (int64_t)p.Hv), std::max((int64_t)p.B, (int64_t)p.rep));
+  p.fastdiv = nblocks * dmax <= (1ll << 32);
+  p.rc_grp8 = recip(grp8);
+  p.rc_hv = recip(p.Hv);
+  p.rc_b = recip(p.B);
+  p.rc_rep = recip(p.rep);
+  if (a->frontend == GDN_FRONTEND_CONV) {
+    p.x = static_cast<const uint16_t*>(a->x);
+    p.conv_w = static_cast<const uint16_t*>(a->conv_weight);
+    p.conv_in = static_cast<const uint16_t*>(a->conv_state_in);
+    p.conv_out = static_cast<uint16_t*>(a->conv_state_out);
+  } else {
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+  }
+  if (p.gate_raw) {
+    p.a = static_cast<const uint16_t*>(a->a);
+    p.b = static_cast<const uint16_t*>(a->b);
+    p.A_log = a->A_log;
+    p.dt_bias = a->dt_bias;
+  } else {
+    p.alpha = a->alpha;
+    p.beta = a->beta;
+  }
   p.state_in = a->state_in;
   p.state_out = a->state_out;
   p.states = a->states;

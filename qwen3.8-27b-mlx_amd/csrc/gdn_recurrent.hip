@@ -100,31 +100,45 @@ struct Tile {
   size_t lb, head;
 };
 
-template <int SLOTS>
-__device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
+// n / d, d one of the block map's divisors: with FAST as one scalar multiply-high by
+// rc = ceil(2^32 / d) (0 for d = 1), exact since the host checked n d <= 2^32 for the grid;
+// else the integer division (a sequence in the vector unit).
+template <bool FAST>
+__device__ __forceinline__ int map_div(int n, int d, uint32_t rc) {
+  if constexpr (FAST) return rc ? (int)__umulhi((uint32_t)n, rc) : n;
+  return n / d;
+}
+
+template <int SLOTS, bool FAST>
+__device__ __forceinline__ Tile decode_block_as(const RecurrentParams& p) {
   int bid = blockIdx.x;
   const int gs = p.rep * Geom<SLOTS>::kTilesPerHead;  // workgroups of one k-head
-  if (p.remap) {
-    const int per = p.nblocks >> 3;
+  if (p.order == 1) {
+    const int per = (int)gridDim.x >> 3;
     bid = (bid & 7) * per + (bid >> 3);
-  } else if (p.nblocks % (8 * gs) == 0) {
+  } else if (p.order == 2) {
     // dispatch id d = 8 gs s + 8 j + x runs on XCD x as workgroup j of k-head group
     // 8 s + x: each k-head on one XCD, consecutive k-heads on consecutive XCDs
-    const int s = bid / (8 * gs), r = bid % (8 * gs), j = r >> 3, x = r & 7;
+    const int s = map_div<FAST>(bid, 8 * gs, p.rc_grp8), r = bid - s * 8 * gs, j = r >> 3, x = r & 7;
     bid = gs * (8 * s + x) + j;
   }
   Tile t;
   t.tile = bid % Geom<SLOTS>::kTilesPerHead;
-  int rest = bid / Geom<SLOTS>::kTilesPerHead;
-  t.h = rest % p.Hv;
-  rest /= p.Hv;
-  t.bb = rest % p.B;
-  t.layer = rest / p.B;
-  t.g = t.h / p.rep;
+  const int rest = bid / Geom<SLOTS>::kTilesPerHead;
+  const int lb = map_div<FAST>(rest, p.Hv, p.rc_hv);
+  t.h = rest - lb * p.Hv;
+  t.layer = map_div<FAST>(lb, p.B, p.rc_b);
+  t.bb = lb - t.layer * p.B;
+  t.g = map_div<FAST>(t.h, p.rep, p.rc_rep);
   t.r0 = t.tile * Geom<SLOTS>::kTileRows;
   t.lb = (size_t)t.layer * p.B + t.bb;
   t.head = t.lb * p.Hv + t.h;
   return t;
+}
+
+template <int SLOTS>
+__device__ __forceinline__ Tile decode_block(const RecurrentParams& p) {
+  return p.fastdiv ? decode_block_as<SLOTS, true>(p) : decode_block_as<SLOTS, false>(p);
 }
 
 template <int SLOTS>
@@ -184,7 +198,7 @@ __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const T
   constexpr int kTileRows = Geom<SLOTS>::kTileRows;
   uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
   const int vbase = 2 * p.Hk * kD + t.h * kD + t.r0;
-  const bool qk_writer = (t.h % p.rep) == 0 && t.tile < 2;
+  const bool qk_writer = t.h == t.g * p.rep && t.tile < 2;
   const int qkbase = (t.tile == 0 ? 0 : p.Hk * kD) + t.g * kD;
   const int nch = kTileRows + (qk_writer ? kD : 0);
   for (int e = threadIdx.x; e < nch * kConvRows; e += kThreads) {
@@ -205,15 +219,15 @@ __device__ __forceinline__ void write_conv_out(const RecurrentParams& p, const T
 // One step on the tile's rows in registers, from this lane's elements of k and q
 // ([4 j16, 4 j16 + 4) and [64 + 4 j16, 64 + 4 j16 + 4)) and its slots' v values.
 template <int SLOTS, bool COLLECT>
-__device__ __forceinline__ void apply_step_r(const RecurrentParams& p, const Tile& t, int step,
+__device__ __forceinline__ void apply_step_r(const RecurrentParams& p, const Tile& t, int T, int step,
                                              float al, float be, f4v k0, f4v k1, f4v q0, f4v q1,
                                              const float (&vrs)[SLOTS], int wave, int grp, int j16,
                                              f4v (&s)[SLOTS][2]) {
   // with COLLECT, this step's state; each slot's rows go out as soon as they are updated
   float* const dst = !COLLECT ? nullptr
                      : p.states_tbh
-                         ? p.states + ((((size_t)t.layer * p.T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
-                         : p.states + (t.head * p.T + step) * kD * kD;
+                         ? p.states + ((((size_t)t.layer * T + step) * p.B + t.bb) * p.Hv + t.h) * kD * kD
+                         : p.states + (t.head * T + step) * kD * kD;
   float ov[SLOTS];
 #pragma unroll
   for (int i = 0; i < SLOTS; ++i) {
@@ -257,7 +271,7 @@ __device__ __forceinline__ void apply_step_r(const RecurrentParams& p, const Til
 #pragma unroll
     for (int i = 1; i < SLOTS; ++i) val = (j16 == i) ? ov[i] : val;
     const int row = t.r0 + row_of<SLOTS>(wave, j16, grp);
-    const size_t oi = ((t.lb * p.T + step) * p.Hv + t.h) * kD + row;
+    const size_t oi = ((t.lb * T + step) * p.Hv + t.h) * kD + row;
     if (p.o_bf16) {
       static_cast<uint16_t*>(p.o)[oi] = f2bf(val);
     } else {
@@ -268,7 +282,7 @@ __device__ __forceinline__ void apply_step_r(const RecurrentParams& p, const Til
 
 // The same with k, q and the tile's v rows staged in LDS.
 template <int SLOTS, bool COLLECT>
-__device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int step,
+__device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile& t, int T, int step,
                                            float al, float be, const float* kk, const float* qq,
                                            const float* vv, int wave, int grp, int j16,
                                            f4v (&s)[SLOTS][2]) {
@@ -279,7 +293,7 @@ __device__ __forceinline__ void apply_step(const RecurrentParams& p, const Tile&
   float vrs[SLOTS];
 #pragma unroll
   for (int i = 0; i < SLOTS; ++i) vrs[i] = vv[row_of<SLOTS>(wave, i, grp)];
-  apply_step_r<SLOTS, COLLECT>(p, t, step, al, be, k0, k1, q0, q1, vrs, wave, grp, j16, s);
+  apply_step_r<SLOTS, COLLECT>(p, t, T, step, al, be, k0, k1, q0, q1, vrs, wave, grp, j16, s);
 }
 
 // Address of row r of the padded conv input xp = [conv_in ; x] at channel c. A row of a
@@ -429,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void decode_qkv_kernel(RecurrentParams p)
   float vrs[SLOTS];
 #pragma unroll
   for (int i = 0; i < SLOTS; ++i) vrs[i] = qkv_value(vraw[i], p.qkv_bf16);
-  apply_step_r<SLOTS, false>(p, t, 0, al, be, kf[0], kf[1], qf[0], qf[1], vrs, wave, grp, j16, s);
+  apply_step_r<SLOTS, false>(p, t, 1, 0, al, be, kf[0], kf[1], qf[0], qf[1], vrs, wave, grp, j16, s);
   if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
 }
 
@@ -509,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   __syncthreads();
 
   // 4. the step, then the state goes back
-  apply_step<SLOTS, false>(p, t, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
+  apply_step<SLOTS, false>(p, t, 1, 0, sm_ab[0], sm_ab[1], sm_k, sm_q, sm_v, wave, grp, j16, s);
   if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
 
   // 5. conv state hand-off from the rows already in registers: new rows 0..2 are xp
@@ -517,7 +531,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(RecurrentParams p) {
   // k-head when h is its k-head's first v-head -- every channel has one writer.
   if (p.conv_out) {
     uint16_t* cout_b = p.conv_out + t.lb * (size_t)kConvRows * p.C;
-    const bool qk_writer = (t.h % p.rep) == 0 && wave == t.tile;
+    const bool qk_writer = t.h == t.g * p.rep && wave == t.tile;
     const int nm = wave == 2 ? (lane < kTileRows ? 1 : 0) : (wave < 2 && qk_writer ? 2 : 0);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -674,7 +688,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
 
     // 3. the pass's steps on the rows in registers
     for (int tt = 0; tt < tc; ++tt) {
-      apply_step<SLOTS, COLLECT>(p, t, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave, grp,
+      apply_step<SLOTS, COLLECT>(p, t, T, t0 + tt, sm_a[tt], sm_b[tt], sm_k[tt], sm_q[tt], sm_v[tt], wave, grp,
                                  j16, s);
     }
   };
