@@ -44,10 +44,11 @@ inline void check_hip(hipError_t e, const char* what) {
 inline bool available() { return gdn_available() != 0; }
 
 // Blocks that are not recorded and carry at least this many tokens run the chunked form
-// (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet near T = 20 on MI355X
-// (one layer, conv front end, B = 1 and 4). The reference chooses by length the same way
+// (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet between T = 24 and 32
+// on MI355X (one layer, conv front end, B = 1, 2, 4, 8), and from 28 on the chunked form is
+// never more than 3 us slower. The reference chooses by length the same way
 // (python/qwen35.py:338, 606-626).
-constexpr int kChunkedMinT = 20;
+constexpr int kChunkedMinT = 28;
 
 // delta::run (delta.hpp:66-68) on device buffers: q, k (B,L,H,128), v (B,L,H,128), alpha,
 // beta (B,L,H), all fp32, head-expanded as the reference passes them; S (B,H,128,128) or

@@ -33,12 +33,13 @@ CONV_TAPS = 4
 
 # Calls that do not record and carry at least this many tokens run the chunked form
 # (gdn_prefill_chunked); shorter ones the recurrent kernel (gdn_run), serial in T. Measured on
-# MI355X with one layer and the conv front end (bench.py --only crossover): at B = 1 the
-# recurrent kernel takes 25 us at T = 16 and 46 us at T = 32, the chunked form 31 us at both;
-# at B = 4, 37 / 69 against 46 us -- they meet near T = 20 either way. Module-level so that
-# tests can force either form, as the reference's CHUNK_THRESHOLD (python/qwen35.py:338,
-# 606-626), which makes the same choice by length.
-CHUNKED_MIN_T = 20
+# MI355X with one layer and the conv front end (bench.py --only crossover): the chunked form
+# takes 31 / 37 / 45 / 61 us at B = 1 / 2 / 4 / 8 for any T up to 40; the recurrent kernel
+# 28.5 / 35.3 / 47.1 / 64.3 us at T = 28 and 24.7 / 30.3 / 40.5 / 55.5 us at T = 24 -- they
+# meet between T = 24 and 32, and from 28 on the chunked form is never more than 3 us slower.
+# Module-level so that tests can force either form, as the reference's CHUNK_THRESHOLD
+# (python/qwen35.py:338, 606-626), which makes the same choice by length.
+CHUNKED_MIN_T = 28
 
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
