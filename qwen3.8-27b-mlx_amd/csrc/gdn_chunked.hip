@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       for (int e = 0; e < 4; ++e) pr[e] = rbf(u[e] * u[e]) + rbf(u[4 + e] * u[4 + e]);
       const float ssum = rbf(row16_sum((pr[0] + pr[1]) + (pr[2] + pr[3])));
       const float den = rbf(ssum + eps_b);
-      const float rs = rbf(1.0f / sqrtf(den));
+      const float rs = rsqrt_bf(den);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         y0[e] = rbf(y0[e] * rs);

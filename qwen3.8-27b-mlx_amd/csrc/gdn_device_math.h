@@ -142,6 +142,18 @@ __device__ __forceinline__ void silu_bf_batch(float (&y)[N]) {
   for (int e = 0; e < N; ++e) y[e] = rbf(y[e] * sg[e]);
 }
 
+// rbf(1 / sqrtf(d)) -- the l2norm's bf16 reciprocal square root of a bf16 value d
+// (ops.cpp:27-30). The hardware v_rsq_f32 is within 1 ulp of 1 / sqrt(d) for normal d, so
+// when its result lies more than 4 ulp from a bf16 rounding midpoint (bits 0x8000 of its
+// low half) both round to the same bf16; otherwise (and for d below the normal range, which
+// v_rsq_f32 flushes, or NaN) the correctly rounded path runs. On the device the fast value
+// alone already rounds as the exact one for every positive normal bf16 d.
+__device__ __forceinline__ float rsqrt_bf(float d) {
+  const float f = __builtin_amdgcn_rsqf(d);
+  if (d >= 1.17549435e-38f && __builtin_amdgcn_sad_u16(f_bits(f), 0x8000u, 0u) > 4u) return rbf(f);
+  return rbf(1.0f / sqrtf(d));
+}
+
 // Sum over the 16 lanes of a DPP row; every lane receives the same total.
 // quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror. When lane m of
 // the row holds the partial sum of group m, this is the butterfly p[m] += p[m ^ s],

@@ -94,7 +94,7 @@ __device__ __forceinline__ void l2norm_pair(float u0, float u1, bool scale, floa
   const float pr = rbf(u0 * u0) + rbf(u1 * u1);
   const float ssum = rbf(wave64_sum(pr));
   const float den = rbf(ssum + eps_b);
-  const float rs = rbf(1.0f / sqrtf(den));
+  const float rs = rsqrt_bf(den);
   y0 = rbf(u0 * rs);
   y1 = rbf(u1 * rs);
   if (scale) {
