@@ -43,12 +43,13 @@ inline void check_hip(hipError_t e, const char* what) {
 
 inline bool available() { return gdn_available() != 0; }
 
-// Blocks that are not recorded and carry at least this many tokens run the chunked form
-// (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet between T = 24 and 32
-// on MI355X (one layer, conv front end, B = 1, 2, 4, 8), and from 28 on the chunked form is
-// never more than 3 us slower. The reference chooses by length the same way
+// Blocks of B sequences that are not recorded and carry at least chunked_min_t(B) tokens run
+// the chunked form (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet near
+// T = 36, 34, 30 and 28 for B = 1, 2, 4 and 8 on MI355X (one layer, conv front end), i.e.
+// 38 - 2 B, and kChunkedMinT from B = 5 on. The reference chooses by length the same way
 // (python/qwen35.py:338, 606-626).
 constexpr int kChunkedMinT = 28;
+constexpr int chunked_min_t(int B) { return 38 - 2 * B > kChunkedMinT ? 38 - 2 * B : kChunkedMinT; }
 
 // delta::run (delta.hpp:66-68) on device buffers: q, k (B,L,H,128), v (B,L,H,128), alpha,
 // beta (B,L,H), all fp32, head-expanded as the reference passes them; S (B,H,128,128) or
@@ -100,12 +101,12 @@ class DeltaCache {
   // Recorded blocks go to two buffers of max_record_steps states each, (T, B, Hv) order,
   // used in turn: commit(n) adopts step n-1 of the block by pointer (no copy), and the
   // next block is recorded into the other buffer, which no longer holds the live state.
-  // Blocks of kChunkedMinT .. max_prefill_tokens tokens (the reference prefills in windows of
+  // Blocks of chunked_min_t(batch) .. max_prefill_tokens tokens (the reference prefills in windows of
   // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here;
   // max_prefill_tokens = 0 keeps every block on the recurrent kernel.
   DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0)
       : p_(p), B_(batch), max_T_(max_record_steps),
-        max_prefill_T_(max_prefill_tokens >= kChunkedMinT ? max_prefill_tokens : 0) {
+        max_prefill_T_(max_prefill_tokens >= chunked_min_t(batch) ? max_prefill_tokens : 0) {
     const size_t D = GDN_HEAD_DIM;
     state_bytes_ = (size_t)B_ * p_.num_v_heads * D * D * sizeof(float);
     conv_bytes_ = (size_t)B_ * (GDN_CONV_TAPS - 1) * p_.conv_dim() * 2;
@@ -153,7 +154,7 @@ class DeltaCache {
   // x (B,T,C) bf16 = in_proj_qkv(x), a, b (B,T,Hv) bf16 = in_proj_a/b(x); o (B,T,Hv,128)
   // bf16. In record mode the state is not advanced and every per-step state is kept for
   // commit(); x must then stay valid until commit(). A block that is not recorded and has
-  // kChunkedMinT .. max_prefill_tokens tokens (x and o 16-byte aligned) runs the chunked form.
+  // chunked_min_t(B) .. max_prefill_tokens tokens (x and o 16-byte aligned) runs the chunked form.
   void step(const void* x, const void* a, const void* b, int T, void* o, hipStream_t stream) {
     gdn_layer_args g{};
     g.n_layers = 1;
@@ -187,7 +188,7 @@ class DeltaCache {
       g.conv_state_out = conv_spare_;
       g.state_out = state_;
       const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(o)) % 16 == 0;
-      if (T >= kChunkedMinT && T <= max_prefill_T_ && aligned) {
+      if (T >= chunked_min_t(B_) && T <= max_prefill_T_ && aligned) {
         g.workspace = ws_;
         g.workspace_bytes = ws_bytes_;
         check(gdn_prefill_chunked(&g));

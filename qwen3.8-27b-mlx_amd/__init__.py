@@ -1,7 +1,7 @@
 """MI355X-native (gfx950) gated-delta recurrence: HIP kernels behind the C ABI of
 include/gdn.h, with a Python mirror of the reference's per-layer interface."""
 from .gdn import (  # noqa: F401
-    CHUNKED_MIN_T, CONV_TAPS, DTYPE_BF16, DTYPE_F32, EXPORTS, FRONTEND_CONV, FRONTEND_QKV, GATES_PRECOMPUTED,
+    CHUNKED_MIN_T, chunked_min_t, CONV_TAPS, DTYPE_BF16, DTYPE_F32, EXPORTS, FRONTEND_CONV, FRONTEND_QKV, GATES_PRECOMPUTED,
     GATES_RAW, GDN_EDEVICE, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_OK, HEAD_DIM, LIB_PATH,
     STATES_BHT, STATES_TBH, CommitArgs, DeltaCache, GdnError, LayerArgs, Result, available,
     call_commit, call_prefill, call_prefill_timed, call_qlinear, call_qlinear_noalloc, call_run, commit, last_error, layer, layer_args,

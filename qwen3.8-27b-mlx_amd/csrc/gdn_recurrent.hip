@@ -587,24 +587,31 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
 
   const uint16_t* x_b = nullptr;
   const uint16_t* cin_b = nullptr;
-  int c0 = 0, c1 = 0;
-  uint32_t wr[2][kTaps] = {};
+  // conv front end: wave w takes steps 2 w and 2 w + 1 of every pass, all of their q, k and
+  // v channels -- lane l: q and k channels (l, l + 64) of the k-head and the tile's v row l
+  // (lanes past the tile's rows repeat its last one; their values go unused)
+  constexpr int kFeCh = 5, kFeRows = 2 + kTaps - 1;
+  int ch[kFeCh] = {};
+  float wv[kFeCh][kTaps] = {};
   if (FE == 1) {
     x_b = p.x + t.lb * (size_t)T * p.C;
     cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
     const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
-    // waves 0..2 own channels (q, k: two per lane; the tile's v rows: one, read twice);
-    // wave 3 mirrors wave 2 so that every wave issues the same loads
-    c0 = fe_channel<SLOTS>(p, t, wave < 3 ? wave : 2, lane);
-    c1 = wave < 2 ? c0 + 64 : c0;
+    ch[0] = fe_channel<SLOTS>(p, t, 0, lane);
+    ch[1] = ch[0] + 64;
+    ch[2] = fe_channel<SLOTS>(p, t, 1, lane);
+    ch[3] = ch[2] + 64;
+    ch[4] = fe_channel<SLOTS>(p, t, 2, lane);
 #pragma unroll
-    for (int j = 0; j < kTaps; ++j) {
-      wr[0][j] = w_l[(size_t)j * p.C + c0];
-      wr[1][j] = w_l[(size_t)j * p.C + c1];
+    for (int c = 0; c < kFeCh; ++c) {
+#pragma unroll
+      for (int j = 0; j < kTaps; ++j) wv[c][j] = bf2f(w_l[(size_t)j * p.C + ch[c]]);
     }
   }
-  const int nm = wave < 2 ? 2 : 1;  // conv channels per lane (waves 0..2)
-  const int gt = tid - (kThreads - kTC);  // the last 8 threads: one step's gates each
+  // gates: lanes 0 and 1 of wave w for steps 2 w and 2 w + 1 (FE = 1); else the last 8
+  // threads, one step each
+  const int gt = FE == 1 ? (lane < 2 ? 2 * wave + lane : -1) : tid - (kThreads - kTC);
+  const int gload = FE == 1 ? 2 * wave + (lane & 1) : gt;  // the step whose gates a thread loads
 
   f4v s[SLOTS][2];
   auto pass = [&](int t0, auto first) {
@@ -613,15 +620,15 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
     if (!kFirst) __syncthreads();  // the previous pass is done reading LDS
 
     // 1. loads: the pass's conv window or q/k/v, its gates, and (first pass) the state
-    uint32_t xr[2][kWin] = {};
+    uint32_t xr[kFeCh][kFeRows] = {};
     uint32_t raw[kRaw] = {};
     if (FE == 1) {
       const int last = T + kConvRows - 1;  // last row of xp = [conv_in ; x]
 #pragma unroll
-      for (int r = 0; r < kWin; ++r) {
-        const int rr = min(t0 + r, last);
-        xr[0][r] = *xp_addr(x_b, cin_b, p.C, c0, rr);
-        xr[1][r] = *xp_addr(x_b, cin_b, p.C, c1, rr);
+      for (int r = 0; r < kFeRows; ++r) {
+        const int rr = min(t0 + 2 * wave + r, last);
+#pragma unroll
+        for (int c = 0; c < kFeCh; ++c) xr[c][r] = *xp_addr(x_b, cin_b, p.C, ch[c], rr);
       }
     } else {
 #pragma unroll
@@ -635,7 +642,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
         raw[i] = qkv_raw(base, idx, p.qkv_bf16);
       }
     }
-    const int gsel = min(max(gt, 0), tc - 1);
+    const int gsel = min(max(gload, 0), tc - 1);
     const GateRaw gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gsel)) * p.Hv + t.h);
     if constexpr (kFirst) {
       if constexpr (HAS_STATE) {
@@ -660,36 +667,29 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
           else sm_v[tt][c - 2 * kD] = val;
         }
       }
-    } else if (wave < 3) {
-      float wv[2][kTaps];
+    } else {
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-#pragma unroll
-        for (int j = 0; j < kTaps; ++j) wv[m][j] = bf2f((uint16_t)wr[m][j]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < kTC; ++tt) {
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int tt = 2 * wave + k2;
         if (tt < tc) {
-          float u[2] = {0.f, 0.f};
+          float u[kFeCh + 1];
 #pragma unroll
-          for (int m = 0; m < 2; ++m) {
-            if (m < nm) {
-              float xv[kTaps];
+          for (int c = 0; c < kFeCh; ++c) {
+            float xv[kTaps];
 #pragma unroll
-              for (int j = 0; j < kTaps; ++j) xv[j] = xp_value(xr[m][tt + j], cin_b, t0 + tt + j);
-              u[m] = conv4(xv, wv[m]);
-            }
+            for (int j = 0; j < kTaps; ++j) xv[j] = xp_value(xr[c][k2 + j], cin_b, t0 + tt + j);
+            u[c] = conv4(xv, wv[c]);
           }
-          silu_bf_batch(u);  // SiLU(0) = 0 for the unused channel
-          if (wave < 2) {
-            float y0, y1;
-            l2norm_pair(u[0], u[1], wave == 0, y0, y1);
-            float* dst = wave == 0 ? sm_q[tt] : sm_k[tt];
-            dst[lane] = y0;
-            dst[lane + 64] = y1;
-          } else if (lane < kTileRows) {
-            sm_v[tt][lane] = u[0];
-          }
+          u[kFeCh] = 0.0f;
+          silu_bf_batch(u);
+          float y0, y1;
+          l2norm_pair(u[0], u[1], true, y0, y1);
+          sm_q[tt][lane] = y0;
+          sm_q[tt][lane + 64] = y1;
+          l2norm_pair(u[2], u[3], false, y0, y1);
+          sm_k[tt][lane] = y0;
+          sm_k[tt][lane + 64] = y1;
+          if (lane < kTileRows) sm_v[tt][lane] = u[4];
         }
       }
     }

@@ -31,15 +31,21 @@ STATES_BHT, STATES_TBH = 0, 1
 HEAD_DIM = 128
 CONV_TAPS = 4
 
-# Calls that do not record and carry at least this many tokens run the chunked form
+# Calls that do not record and carry at least chunked_min_t(B) tokens run the chunked form
 # (gdn_prefill_chunked); shorter ones the recurrent kernel (gdn_run), serial in T. Measured on
 # MI355X with one layer and the conv front end (bench.py --only crossover): the chunked form
-# takes 31 / 37 / 45 / 61 us at B = 1 / 2 / 4 / 8 for any T up to 40; the recurrent kernel
-# 28.5 / 35.3 / 47.1 / 64.3 us at T = 28 and 24.7 / 30.3 / 40.5 / 55.5 us at T = 24 -- they
-# meet between T = 24 and 32, and from 28 on the chunked form is never more than 3 us slower.
-# Module-level so that tests can force either form, as the reference's CHUNK_THRESHOLD
-# (python/qwen35.py:338, 606-626), which makes the same choice by length.
+# takes 31 / 38 / 45 / 61 us at B = 1 / 2 / 4 / 8 for any T up to 32 (66 us at B = 8 from
+# T = 36); the recurrent kernel 26.8 / 35.3 / 47.6 / 66.8 us at T = 32 and 31.3 / 41.1 / 54.6
+# / 76.5 us at T = 36. The forms meet near T = 36, 34, 30 and 28 for B = 1, 2, 4 and 8: 38 - 2 B,
+# and CHUNKED_MIN_T from B = 5 on. Module-level so that tests can force either form, as the
+# reference's CHUNK_THRESHOLD (python/qwen35.py:338, 606-626), which makes the same choice by
+# length.
 CHUNKED_MIN_T = 28
+
+
+def chunked_min_t(B: int) -> int:
+    """Fewest tokens of a non-recording call of B sequences that run on the chunked form."""
+    return max(CHUNKED_MIN_T, 38 - 2 * B)
 
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
@@ -294,11 +300,11 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
         stream=_stream(stream))
 
 
-def _use_chunked(T: int, record: bool, x, q, tensors) -> bool:
-    """The length-based choice of the form (CHUNKED_MIN_T), for calls the chunked form takes:
+def _use_chunked(B: int, T: int, record: bool, x, q, tensors) -> bool:
+    """The length-based choice of the form (chunked_min_t), for calls the chunked form takes:
     not recording, bf16 q, k, v when given, 16-byte aligned inputs."""
     import torch
-    if record or T < CHUNKED_MIN_T:
+    if record or T < chunked_min_t(B):
         return False
     if x is None and q.dtype != torch.bfloat16:
         return False
@@ -312,7 +318,7 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     recurrence: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
     (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
     v (B,T,Hv,128). Returns dict(o, state, states, conv_state). A call that does not record
-    and has at least CHUNKED_MIN_T tokens runs the chunked form (python/qwen35.py:606-626)."""
+    and has at least chunked_min_t(B) tokens runs the chunked form (python/qwen35.py:606-626)."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
@@ -331,7 +337,7 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     conv_out = None
     if x is not None and not record:
         conv_out = torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
-    chunked = _use_chunked(T, record, x, q, (x, conv_state, q, k, v))
+    chunked = _use_chunked(B, T, record, x, q, (x, conv_state, q, k, v))
     ws = (torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None), dtype=torch.uint8,
                       device=dev) if chunked else None)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
@@ -406,7 +412,7 @@ class DeltaCache:
 
     def step(self, x, conv_weight, a, b, A_log, dt_bias, o_dtype=None, stream=None):
         """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache; a block of at
-        least CHUNKED_MIN_T tokens that is not recorded runs the chunked form."""
+        least chunked_min_t(B) tokens that is not recorded runs the chunked form."""
         import torch
         B, T = x.shape[0], x.shape[1]
         o = torch.empty((B, T, self.Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16,
@@ -422,7 +428,7 @@ class DeltaCache:
             self.base_offset = self.offset
             self.pending = (x, states, T)
         else:
-            chunked = _use_chunked(T, False, x, None, (x,))
+            chunked = _use_chunked(B, T, False, x, None, (x,))
             ws = (torch.empty(prefill_workspace_size(B, T, self.Hk, self.Hv), dtype=torch.uint8,
                               device=x.device) if chunked else None)
             args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,

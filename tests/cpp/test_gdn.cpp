@@ -194,7 +194,7 @@ void test_cache() {
   check(threw, "commit out of range throws (model.cpp:443)");
 }
 
-// A block of kChunkedMinT .. max_prefill_tokens tokens runs the chunked form
+// A block of chunked_min_t(B) .. max_prefill_tokens tokens runs the chunked form
 // (python/qwen35.py:606-626 chooses by length the same way): against a cache without a
 // prefill workspace, which runs the same block on the recurrent kernel, within the chunked
 // form's tolerance (1e-2); the conv window is exact in both forms.

@@ -460,7 +460,7 @@ def test_deltacache_spec_equals_plain(O, gdn, dev):
 
 
 def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
-    """A block of at least CHUNKED_MIN_T tokens that is not recorded runs the chunked form
+    """A block of at least chunked_min_t(B) tokens that is not recorded runs the chunked form
     (python/qwen35.py:606-626 makes the same choice by length): a 100-token prefill through
     DeltaCache.step and then one decode step, against the oracle's token-by-token recurrence
     at the chunked form's tolerance (1e-2, the prefill tests'); the same calls with the
@@ -495,7 +495,7 @@ def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
         e_o2, e_s2 = O.rel_err(to_np(o2), ref["o"][:, T:]), O.rel_err(to_np(c.state), ref["state"])
         print(f"  prefill o {e_o:.2e} state {e_s:.2e}; next token o {e_o2:.2e} state {e_s2:.2e}; "
               f"chunked calls {calls}", flush=True)
-        assert calls == ([T] if threshold <= T else [])
+        assert calls == ([T] if mod.chunked_min_t(B) <= T else [])
         assert max(e_o, e_s, e_o2, e_s2) <= tol
         assert np.array_equal(to_np(c.conv), ref["xp"][:, -3:])
     # layer() with q, k, v given (bf16) takes the same choice
