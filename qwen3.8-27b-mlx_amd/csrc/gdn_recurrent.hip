@@ -709,6 +709,118 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
   if (FE == 1 && p.conv_out) write_conv_out<SLOTS>(p, t, x_b, cin_b);
 }
 
+// Any T > 8 without per-step states, conv front end, 16-row tiles: 8 waves. Waves 0..3 hold the tile's
+// state rows and run the steps of pass p from one LDS buffer while waves 4..7 compute the
+// conv front end of pass p + 1 into the other (wave 4 + w: steps 2 w and 2 w + 1 of the pass,
+// their q, k and v channels and their gates, as in steps_kernel); one barrier per pass, the
+// same count in every wave. On a SIMD the front-end wave's independent work fills the issue
+// slots that the steps' dependent chains leave idle.
+template <int SLOTS, bool HAS_STATE>
+__global__ __launch_bounds__(2 * kThreads) void steps_overlap_kernel(RecurrentParams p) {
+  constexpr int kTileRows = Geom<SLOTS>::kTileRows;
+  __shared__ float sm_q[2][kTC][kD];
+  __shared__ float sm_k[2][kTC][kD];
+  __shared__ float sm_v[2][kTC][kTileRows];
+  __shared__ float sm_a[2][kTC];
+  __shared__ float sm_b[2][kTC];
+
+  const Tile t = decode_block<SLOTS>(p);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool fe_wave = wave >= 4;
+  const int fw = wave & 3;
+  const int grp = lane >> 4, j16 = lane & 15;
+  const int T = p.T;
+  const uint16_t* x_b = p.x + t.lb * (size_t)T * p.C;
+  const uint16_t* cin_b = p.conv_in ? p.conv_in + t.lb * (size_t)kConvRows * p.C : nullptr;
+  constexpr int kFeCh = 5, kFeRows = 2 + kTaps - 1;
+  int ch[kFeCh] = {};
+  float wv[kFeCh][kTaps] = {};
+
+  // the front end of the pass at t0 into buffer buf (front-end waves)
+  auto fe_pass = [&](int t0, int buf) {
+    const int tc = min(kTC, T - t0);
+    uint32_t xr[kFeCh][kFeRows];
+    const int last = T + kConvRows - 1;  // last row of xp = [conv_in ; x]
+#pragma unroll
+    for (int r = 0; r < kFeRows; ++r) {
+      const int rr = min(t0 + 2 * fw + r, last);
+#pragma unroll
+      for (int c = 0; c < kFeCh; ++c) xr[c][r] = *xp_addr(x_b, cin_b, p.C, ch[c], rr);
+    }
+    const int gsel = min(2 * fw + (lane & 1), tc - 1);
+    const GateRaw gr = gate_load(p, t.layer, t.h, (t.lb * T + (t0 + gsel)) * p.Hv + t.h);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int tt = 2 * fw + k2;
+      if (tt < tc) {
+        float u[kFeCh + 1];
+#pragma unroll
+        for (int c = 0; c < kFeCh; ++c) {
+          float xv[kTaps];
+#pragma unroll
+          for (int j = 0; j < kTaps; ++j) xv[j] = xp_value(xr[c][k2 + j], cin_b, t0 + tt + j);
+          u[c] = conv4(xv, wv[c]);
+        }
+        u[kFeCh] = 0.0f;
+        silu_bf_batch(u);
+        float y0, y1;
+        l2norm_pair(u[0], u[1], true, y0, y1);
+        sm_q[buf][tt][lane] = y0;
+        sm_q[buf][tt][lane + 64] = y1;
+        l2norm_pair(u[2], u[3], false, y0, y1);
+        sm_k[buf][tt][lane] = y0;
+        sm_k[buf][tt][lane + 64] = y1;
+        if (lane < kTileRows) sm_v[buf][tt][lane] = u[4];
+      }
+    }
+    const int gt = 2 * fw + lane;
+    if (lane < 2 && gt < tc) gate_math(p, gr, sm_a[buf][gt], sm_b[buf][gt]);
+  };
+
+  f4v s[SLOTS][2];
+  if (fe_wave) {
+    const uint16_t* w_l = p.conv_w + (size_t)t.layer * kTaps * p.C;
+    ch[0] = fe_channel<SLOTS>(p, t, 0, lane);
+    ch[1] = ch[0] + 64;
+    ch[2] = fe_channel<SLOTS>(p, t, 1, lane);
+    ch[3] = ch[2] + 64;
+    ch[4] = fe_channel<SLOTS>(p, t, 2, lane);
+#pragma unroll
+    for (int c = 0; c < kFeCh; ++c) {
+#pragma unroll
+      for (int j = 0; j < kTaps; ++j) wv[c][j] = bf2f(w_l[(size_t)j * p.C + ch[c]]);
+    }
+    fe_pass(0, 0);
+  } else if constexpr (HAS_STATE) {
+    load_rows<SLOTS>(p.state_in + t.head * kD * kD, t, wave, grp, j16, s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) s[i][0] = s[i][1] = f4v{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();  // pass 0's front end is in buffer 0
+
+  int buf = 0;
+  for (int t0 = 0; t0 < T; t0 += kTC) {
+    if (fe_wave) {
+      if (t0 + kTC < T) fe_pass(t0 + kTC, buf ^ 1);
+    } else {
+      const int tc = min(kTC, T - t0);
+      for (int tt = 0; tt < tc; ++tt) {
+        apply_step<SLOTS, false>(p, t, T, t0 + tt, sm_a[buf][tt], sm_b[buf][tt], sm_k[buf][tt], sm_q[buf][tt],
+                                 sm_v[buf][tt], wave, grp, j16, s);
+      }
+    }
+    __syncthreads();  // buffer buf is read, buffer buf ^ 1 is written
+    buf ^= 1;
+  }
+
+  if (!fe_wave) {
+    if (p.state_out) store_rows<SLOTS>(p.state_out + t.head * kD * kD, t, wave, grp, j16, s);
+    if (p.conv_out) write_conv_out<SLOTS>(p, t, x_b, cin_b);
+  }
+}
+
 __global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -756,6 +868,14 @@ void launch_slots(const RecurrentParams& p, int frontend, bool collect, hipStrea
     else hipLaunchKernelGGL((decode_qkv_kernel<SLOTS, false, false>), grid, block, 0, stream, p);
   } else if (frontend == 0) {
     launch_steps<SLOTS, 0>(p, collect, grid, block, stream);
+  } else if (SLOTS == kSmallSlots && !collect && p.T > kTC) {
+    // several passes on small grids: the front end of each pass overlaps the previous steps
+    // (on 64-row tiles the 8-wave workgroups' registers leave one per CU: slower there)
+    if constexpr (SLOTS == kSmallSlots) {
+      const dim3 block2(2 * kThreads);
+      if (p.state_in) hipLaunchKernelGGL((steps_overlap_kernel<SLOTS, true>), grid, block2, 0, stream, p);
+      else hipLaunchKernelGGL((steps_overlap_kernel<SLOTS, false>), grid, block2, 0, stream, p);
+    }
   } else {
     launch_steps<SLOTS, 1>(p, collect, grid, block, stream);
   }

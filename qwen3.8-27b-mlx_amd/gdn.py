@@ -34,18 +34,19 @@ CONV_TAPS = 4
 # Calls that do not record and carry at least chunked_min_t(B) tokens run the chunked form
 # (gdn_prefill_chunked); shorter ones the recurrent kernel (gdn_run), serial in T. Measured on
 # MI355X with one layer and the conv front end (bench.py --only crossover): the chunked form
-# takes 31 / 38 / 45 / 61 us at B = 1 / 2 / 4 / 8 for any T up to 32 (66 us at B = 8 from
-# T = 36); the recurrent kernel 26.8 / 35.3 / 47.6 / 66.8 us at T = 32 and 31.3 / 41.1 / 54.6
-# / 76.5 us at T = 36. The forms meet near T = 36, 34, 30 and 28 for B = 1, 2, 4 and 8: 38 - 2 B,
-# and CHUNKED_MIN_T from B = 5 on. Module-level so that tests can force either form, as the
-# reference's CHUNK_THRESHOLD (python/qwen35.py:338, 606-626), which makes the same choice by
-# length.
+# takes 31 / 38 / 45 / 61 us at B = 1 / 2 / 4 / 8 (66 us at B = 8 from T = 36); the recurrent
+# kernel 28.1 / 31.2 / 32.7 us at B = 1 and T = 40 / 44 / 48, 34.8 / 39.7 us at B = 2 and
+# T = 32 / 36, 43.8 / 47.6 us at B = 4 and T = 28 / 32, 61.3 / 66.8 us at B = 8 and T = 28 / 32.
+# The forms meet near T = 44, 34, 30 and 28 for B = 1, 2, 4 and 8: 44 for one sequence,
+# 38 - 2 B for two to four, CHUNKED_MIN_T from five on. Module-level so that tests can force
+# either form, as the reference's CHUNK_THRESHOLD (python/qwen35.py:338, 606-626), which makes
+# the same choice by length.
 CHUNKED_MIN_T = 28
 
 
 def chunked_min_t(B: int) -> int:
     """Fewest tokens of a non-recording call of B sequences that run on the chunked form."""
-    return max(CHUNKED_MIN_T, 38 - 2 * B)
+    return max(CHUNKED_MIN_T, 44 if B == 1 else 38 - 2 * B)
 
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
