@@ -19,11 +19,11 @@
 //   kS = k . s            (per-lane partial dot, then a 16-lane DPP butterfly)
 //   s  = a (s - b kS k) + b v_r k
 //   o_r = q . s           (partial dot + DPP butterfly)
-// Both reductions stay inside a DPP row: no LDS, no atomics. With the conv front end and
-// more than 8 steps each wave computes two steps of a pass (their q, k, v and gates); on
-// 16-row tiles a block that records nothing runs on 8 waves instead, four of them
-// computing the next pass's front end into a second LDS buffer while the other four apply
-// the current pass's steps.
+// Both reductions stay inside a DPP row: no LDS, no atomics. For T > 1 with the conv front
+// end each wave computes two steps of every pass of up to 8 (their q, k, v and gates); on
+// 16-row tiles a block of more than 8 steps that records nothing runs on 8 waves instead,
+// four of them computing the next pass's front end into a second LDS buffer while the
+// other four apply the current pass's steps.
 //
 // Decode (T = 1) orders its memory traffic for latency: the front end's few loads are
 // issued first, then the tile's state loads, so the front-end arithmetic runs while the
