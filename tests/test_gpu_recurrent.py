@@ -375,11 +375,12 @@ def test_ragged_steps_conv_and_zero_inputs(O, gdn, dev, T):
     assert np.array_equal(out2["conv"][0], ref2["xp"][:, -3:])
 
 
-@pytest.mark.parametrize("Hk,Hv,T", [(8, 16, 1), (4, 16, 5), (2, 10, 3)])
+@pytest.mark.parametrize("Hk,Hv,T", [(8, 16, 1), (4, 16, 5), (2, 10, 3), (8, 16, 12), (4, 20, 17)])
 def test_conv_layer_other_head_ratios(O, gdn, dev, Hk, Hv, T):
     """Other sizes of the family: two, four and five v-heads per k-head (the v-head ->
-    k-head map h / (Hv / Hk), model.cpp:603-605), decode and a verify-length block, with
-    the conv front end and a carried conv state."""
+    k-head map h / (Hv / Hk), model.cpp:603-605), decode, a verify-length block and blocks
+    of several passes (T = 12, 17: the 8-wave form that overlaps each pass's front end with
+    the previous steps), with the conv front end and a carried conv state."""
     log_case(f"conv layer Hk={Hk} Hv={Hv} T={T} B=2")
     inp = O.make_inputs(config=3, layer=10 * Hk + Hv + T, B=2, L=T, Hk=Hk, Hv=Hv, conv=True)
     ref = O.reference_layer(inp)
