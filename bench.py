@@ -30,6 +30,30 @@ D = 128
 HK, HV = 16, 48
 C = 2 * HK * D + HV * D          # 10240 conv channels
 METRIC = "gated-delta decode state GB/s (% HBM peak) at B=1,32; prefill tok/s T=4096"
+# Plain memory streams with the kernels' traffic shapes (the ceilings the decode and verify
+# rates are read against): bench instrumentation, not part of the library.
+PROBE_SRC = os.path.join(ROOT, "stream_probe.hip")
+PROBE_LIB = os.path.join(ROOT, "libstream_probe.so")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """Compile stream_probe.hip into libstream_probe.so beside this file (with the library's
+    HIP flags); __graft_entry__.build() calls it."""
+    import importlib.util
+    import subprocess
+    spec = importlib.util.spec_from_file_location("gdn_bench_build_flags",
+                                                  os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "_build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [mod.hipcc(), *mod.HIPCC_FLAGS, "-shared", "-o", tmp, PROBE_SRC]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"probe build failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def bytes_decode_layer(B: int, conv: bool) -> int:
@@ -354,21 +378,26 @@ def bench_copy_ceiling(torch, dev, timer, steps: int = 50):
 
 
 def stream_ceilings(torch, dev, timer, steps: int, b32: bool = False):
-    """Plain memory streams with the decode and verify state traffic's shapes (libgdn_probe.so,
-    no arithmetic): the decode step's 4,608 tiles of 32 KB read and written back in place,
-    and verify's 768 tiles read once and written 5 times, each rotated over 8 buffer sets
-    as the kernels' lines are; with b32, the B=32 step's 147,456 tiles over 2 sets. The
-    kernels' rates are read against these."""
+    """Plain memory streams with the decode and verify state traffic's shapes (libstream_probe.so,
+    no arithmetic): the decode step's 4,608 tiles of 32 KB read and written back in place
+    (302 MB); the same with each workgroup also moving its share of the front end's bytes
+    (x, conv state read and written, conv weights, gate inputs, o: the step's full
+    313.4 MB); the 302 MB read only and written only; and verify's 768 tiles read once and
+    written 5 times -- each rotated over 8 buffer sets as the kernels' lines are. With b32,
+    the B=32 step's 147,456 tiles over 2 sets. The kernels' rates are read against these."""
     import ctypes
-    path = os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "libgdn_probe.so")
-    if not os.path.exists(path):
+    if not os.path.exists(PROBE_LIB):
         return None
-    L = ctypes.CDLL(path)
+    L = ctypes.CDLL(PROBE_LIB)
     L.gdn_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     L.gdn_probe_rmw_split.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     L.gdn_probe_rmw_groups.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     L.gdn_probe_read_write_t.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_void_p]
+    L.gdn_probe_rmw_fe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L.gdn_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    L.gdn_probe_write.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     tile = 8192  # floats (32 KB)
     out = {}
@@ -382,6 +411,28 @@ def stream_ceilings(torch, dev, timer, steps: int, b32: bool = False):
     r = timer.time_calls(lambda it: L.gdn_probe_rmw_groups(bufs[it % 8].data_ptr(), nd, 6, st()), steps, 10)
     out["decode_shape_rmw_stream_kheads"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
                                                  GBps=round(nbytes / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=nbytes)
+    # the step's full bytes: per layer the front end reads 164,416 B (x, conv state, conv
+    # weights, a, b, A_log, dt_bias) and writes 73,728 B (conv state, o), which over the
+    # layer's 96 tiles is 107 float4 read and 48 written per tile (313,417,728 B per step
+    # against the kernel's 313,420,800)
+    fe_rd, fe_wr = 107, 48
+    fe_in = [torch.randn(nd * fe_rd * 4, device=dev) for _ in range(8)]
+    fe_out = [torch.empty(nd * fe_wr * 4, device=dev) for _ in range(8)]
+    r = timer.time_calls(lambda it: L.gdn_probe_rmw_fe(bufs[it % 8].data_ptr(), fe_in[it % 8].data_ptr(),
+                                                       fe_out[it % 8].data_ptr(), nd, fe_rd, fe_wr, 6, st()), steps, 10)
+    fb = nbytes + nd * (fe_rd + fe_wr) * 16
+    out["decode_full_bytes_rmw_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                                               GBps=round(fb / (r["ms_per_step"] * 1e-3) / 1e9, 1), bytes=fb)
+    del fe_in, fe_out
+    sink = torch.zeros(1, device=dev)
+    r = timer.time_calls(lambda it: L.gdn_probe_read(bufs[it % 8].data_ptr(), sink.data_ptr(), nd, st()), steps, 10)
+    out["decode_shape_read_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                                           GBps=round(nbytes / 2 / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+                                           bytes=nbytes // 2)
+    r = timer.time_calls(lambda it: L.gdn_probe_write(bufs[it % 8].data_ptr(), nd, st()), steps, 10)
+    out["decode_shape_write_stream"] = dict(us=round(r["ms_per_step"] * 1e3, 2),
+                                            GBps=round(nbytes / 2 / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+                                            bytes=nbytes // 2)
     del bufs
     if b32:
         # the B=32 step's state traffic: 147,456 tiles (4.8 GB) over 2 sets, as its bench line,
@@ -410,7 +461,7 @@ def launch_floors(torch, dev, timer, steps: int):
     """What a one-layer launch cannot beat, timed the same way: a one-element kernel (the
     launch itself), a device copy of one layer's 3.1 MB state (3.1 MB read + 3.1 MB
     written), and the same state read and written back in place by the decode kernel's
-    one-layer grid (384 workgroups of 16-row tiles in its XCD order, libgdn_probe.so),
+    one-layer grid (384 workgroups of 16-row tiles in its XCD order, libstream_probe.so),
     each back to back over rotating buffers."""
     one = torch.zeros(1, device=dev)
     r = timer.time_calls(lambda it: one.add_(1), steps, 20)
@@ -421,10 +472,9 @@ def launch_floors(torch, dev, timer, steps: int):
     out = dict(empty_kernel_us=round(r["ms_per_step"] * 1e3, 2),
                copy_one_layer_state_us=round(c["ms_per_step"] * 1e3, 2))
     del src, dst
-    path = os.path.join(ROOT, "qwen3.8-27b-mlx_amd", "libgdn_probe.so")
-    if os.path.exists(path):
+    if os.path.exists(PROBE_LIB):
         import ctypes
-        L = ctypes.CDLL(path)
+        L = ctypes.CDLL(PROBE_LIB)
         L.gdn_probe_rmw_small.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
         tiles, group = HV * (D // 16), (HV // HK) * (D // 16)  # 384 tiles of 8 KB, 24 per k-head
         bufs = [torch.randn(n, device=dev) for _ in range(96)]
@@ -592,6 +642,9 @@ def main() -> int:
             if head is not None:
                 best = max(sc["decode_shape_rmw_stream"]["GBps"], sc["decode_shape_rmw_stream_kheads"]["GBps"])
                 sc["decode_vs_rmw_stream"] = round(head["GBps"] / best, 4)
+                # time ratio of the decode step to the stream carrying the same 313.4 MB
+                sc["decode_time_vs_full_bytes_stream"] = round(
+                    sc["decode_full_bytes_rmw_stream"]["us"] / (head["ms_per_step"] * 1e3), 4)
             if "verify_b8_t5" in sec:
                 sc["verify_vs_stream"] = round(sec["verify_b8_t5"]["GBps"] / sc["verify_shape_stream"]["GBps"], 4)
             if "decode_b32_shape_rmw_stream" in sc:
@@ -599,7 +652,10 @@ def main() -> int:
                 sc["decode_b32_vs_rmw_stream"] = round(sec["decode_b32_48_layers"]["GBps"] / best, 4)
             print(f"# same-shape streams: decode RMW {sc['decode_shape_rmw_stream']['us']:.1f} us "
                   f"({sc['decode_shape_rmw_stream']['GBps']:.0f} GB/s; in the kernel's order "
-                  f"{sc['decode_shape_rmw_stream_kheads']['us']:.1f} us), verify "
+                  f"{sc['decode_shape_rmw_stream_kheads']['us']:.1f} us; with the front end's bytes, 313.4 MB, "
+                  f"{sc['decode_full_bytes_rmw_stream']['us']:.1f} us), read only "
+                  f"{sc['decode_shape_read_stream']['GBps']:.0f} GB/s, write only "
+                  f"{sc['decode_shape_write_stream']['GBps']:.0f} GB/s, verify "
                   f"{sc['verify_shape_stream']['us']:.1f} us ({sc['verify_shape_stream']['GBps']:.0f} GB/s)", flush=True)
             if "decode_b32_shape_rmw_stream" in sc:
                 b, b2 = sc["decode_b32_shape_rmw_stream"], sc["decode_b32_shape_rmw_stream_split"]

@@ -1,5 +1,4 @@
-"""Builds libgdn.so (HIP for gfx950) and bench.py's stream probes (libgdn_probe.so) in-tree
-with hipcc."""
+"""Builds libgdn.so (HIP for gfx950) in-tree with hipcc."""
 from __future__ import annotations
 
 import os
@@ -11,9 +10,6 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libgdn.so")
 SOURCES = ["gdn_api.cpp", "gdn_recurrent.hip", "gdn_commit.hip", "gdn_chunked.hip", "gdn_qlinear.hip"]
-# bench.py's memory-stream probes (the ceilings the decode and verify rates are read against)
-PROBE_SRC = "stream_probe.hip"
-PROBE_LIB = os.path.join(PKG_DIR, "libgdn_probe.so")
 
 # -ffp-contract=off: the bf16 front end must round exactly as written (fma only where
 #   the code asks for it with __builtin_fmaf).
@@ -61,14 +57,6 @@ def build(verbose: bool = False) -> str:
         if res.returncode != 0:
             raise RuntimeError(f"link failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
         os.replace(tmp, LIB_PATH)
-        tmp = PROBE_LIB + ".tmp"
-        cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-o", tmp, os.path.join(CSRC, PROBE_SRC)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"probe build failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-        os.replace(tmp, PROBE_LIB)
     finally:
         shutil.rmtree(tmpdir, ignore_errors=True)
     return LIB_PATH

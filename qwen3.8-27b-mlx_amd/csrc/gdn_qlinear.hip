@@ -600,23 +600,27 @@ static __device__ __align__(256) unsigned char scratch[GDN_QLINEAR_NOALLOC_SCRAT
 
 namespace {
 constexpr int kMaxScratchDevices = 64;
-std::once_flag g_scratch_once[kMaxScratchDevices];
+std::mutex g_scratch_mutex[kMaxScratchDevices];
 void* g_scratch_ptr[kMaxScratchDevices];
-hipError_t g_scratch_err[kMaxScratchDevices];
 }  // namespace
 
+// Only a successful lookup is kept: a failure (e.g. before the device's context is usable)
+// is returned to this call, and the next call on that device looks the symbol up again.
 hipError_t qlinear_scratch(void** ptr) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
-  std::call_once(g_scratch_once[dev], [dev] {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex[dev]);
+  if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
-  });
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
   *ptr = g_scratch_ptr[dev];
-  return g_scratch_err[dev];
+  return hipSuccess;
 }
 
 size_t qlinear_workspace_bytes(int n_layers, int m, int k) {

@@ -314,12 +314,19 @@ def _use_chunked(B: int, T: int, record: bool, x, q, tensors) -> bool:
 
 def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
           conv_weight=None, conv_state=None, collect: bool = False, in_place: bool = True,
-          o_dtype=None, Hk: int = 16, stream=None):
+          o_dtype=None, Hk: int = 16, workspace=None, stream=None):
     """The per-layer call of GatedDeltaNet::operator() (cpp/src/model.cpp:585-641) at the
     recurrence: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
     (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
     v (B,T,Hv,128). Returns dict(o, state, states, conv_state). A call that does not record
-    and has at least chunked_min_t(B) tokens runs the chunked form (python/qwen35.py:606-626)."""
+    and has at least chunked_min_t(B) tokens runs the chunked form (python/qwen35.py:606-626)
+    in `workspace` (uint8, at least prefill_workspace_size(B, T, ...) bytes), which is
+    allocated here only when the caller gives none.
+
+    Precision: the chunked form's bf16 MFMA products leave the state about 2e-3 (relative,
+    T = 4096) from the fp32 recurrence, against about 1e-7 for the recurrent kernel the
+    reference's fp32 Metal kernel corresponds to (cpp/src/model.cpp:619-624); later decode
+    steps continue from that state."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
@@ -339,8 +346,10 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     if x is not None and not record:
         conv_out = torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
     chunked = _use_chunked(B, T, record, x, q, (x, conv_state, q, k, v))
-    ws = (torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None), dtype=torch.uint8,
-                      device=dev) if chunked else None)
+    ws = None
+    if chunked:
+        ws = workspace if workspace is not None else torch.empty(
+            prefill_workspace_size(B, T, Hk, Hv, conv=x is not None), dtype=torch.uint8, device=dev)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
                       A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out,
@@ -397,23 +406,34 @@ class DeltaCache:
     recorded block and no state is copied (only the 3-row conv window moves).
 
     The conv state is kept in two buffers that swap roles each call (the library never
-    updates it in place: every workgroup must see the old rows)."""
+    updates it in place: every workgroup must see the old rows).
 
-    def __init__(self, B: int, Hv: int = 48, Hk: int = 16, device="cuda"):
+    Blocks of chunked_min_t(B) .. max_prefill_tokens tokens that are not recorded run the
+    chunked form in a workspace allocated here, once (the reference prefills in windows of
+    1024, cpp/src/session.hpp:136); max_prefill_tokens = 0 keeps every block on the
+    recurrent kernel. As the C++ DeltaCache (include/gdn.hpp), step() then allocates no
+    workspace. The chunked form leaves the state about 2e-3 (relative, T = 4096) from the
+    fp32 recurrence, against about 1e-7 on the recurrent kernel."""
+
+    def __init__(self, B: int, Hv: int = 48, Hk: int = 16, device="cuda", max_prefill_tokens: int = 0):
         import torch
         C = 2 * Hk * HEAD_DIM + Hv * HEAD_DIM
         self.Hk, self.Hv, self.C = Hk, Hv, C
         self.state = torch.zeros((B, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=device)
         self.conv = torch.zeros((B, CONV_TAPS - 1, C), dtype=torch.bfloat16, device=device)
         self._conv_spare = torch.empty_like(self.conv)
+        self.max_prefill_tokens = max_prefill_tokens if max_prefill_tokens >= chunked_min_t(B) else 0
+        self._ws = (torch.empty(prefill_workspace_size(B, self.max_prefill_tokens, Hk, Hv), dtype=torch.uint8,
+                                device=device) if self.max_prefill_tokens else None)
         self.offset = 0
         self.record = False
         self.base_offset = 0
         self.pending = None
 
     def step(self, x, conv_weight, a, b, A_log, dt_bias, o_dtype=None, stream=None):
-        """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache; a block of at
-        least chunked_min_t(B) tokens that is not recorded runs the chunked form."""
+        """One GatedDeltaNet recurrence call (model.cpp:585-638) on this cache; a block of
+        chunked_min_t(B) .. max_prefill_tokens tokens that is not recorded runs the chunked
+        form in the cache's workspace."""
         import torch
         B, T = x.shape[0], x.shape[1]
         o = torch.empty((B, T, self.Hv, HEAD_DIM), dtype=o_dtype or torch.bfloat16,
@@ -429,13 +449,13 @@ class DeltaCache:
             self.base_offset = self.offset
             self.pending = (x, states, T)
         else:
-            chunked = _use_chunked(B, T, False, x, None, (x,))
-            ws = (torch.empty(prefill_workspace_size(B, T, self.Hk, self.Hv), dtype=torch.uint8,
-                              device=x.device) if chunked else None)
+            chunked = (self._ws is not None and T <= self.max_prefill_tokens
+                       and _use_chunked(B, T, False, x, None, (x, o)))
             args = layer_args(B=B, T=T, Hk=self.Hk, Hv=self.Hv, x=x, conv_weight=conv_weight,
                               conv_state_in=self.conv, conv_state_out=self._conv_spare, a=a,
                               b=b, A_log=A_log, dt_bias=dt_bias, state_in=self.state,
-                              state_out=self.state, o=o, workspace=ws, stream=stream)
+                              state_out=self.state, o=o, workspace=self._ws if chunked else None,
+                              stream=stream)
             (call_prefill if chunked else call_run)(args)
             self.conv, self._conv_spare = self._conv_spare, self.conv
             self.offset += T
@@ -521,8 +541,10 @@ def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, strea
 
 def qlinear_noalloc(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
     """qlinear through gdn_qlinear_noalloc: no workspace, the library's per-device scratch
-    instead (one layer at any rows fits; calls overlapping on one device race on it). Only
-    the outputs are allocated here; the library call itself allocates nothing."""
+    of 8 MiB instead -- 512 operand rows at any k, 1,024 rows up to k = 4096; larger shapes
+    return GDN_EINVAL (e.g. M = 4096 at K = 5120 needs 40 MiB). Calls overlapping on one
+    device race on the scratch. Only the outputs are allocated here; the library call itself
+    allocates nothing."""
     args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, stream=stream, alloc_workspace=False)
     call_qlinear_noalloc(args)
     return ys

@@ -2,9 +2,11 @@
 token-by-token recurrence -- the reference's own criterion for its chunked form
 (python/test_model.py:138-156, BUILD_LOG.md:314-315).
 
-Tolerance (from the task statement): outputs within 1e-2 of the token-by-token result in
-the reference's measure max|a-b|/max|b|; the final fp32 state within the same bound. The
-bf16 output rounding (up to 2^-8 relative) is inside that budget.
+Tolerance: outputs within 1e-2 of the token-by-token result in the reference's measure
+max|a-b|/max|b| (the task statement's bound for chunked prefill); the bf16 output rounding
+(up to 2^-8 relative) is inside that budget. The final fp32 state, which later decode steps
+continue from, is held to 5e-3: about twice what the chunked form's bf16 products give at
+T = 4096 (2.1e-3), so that a loss of precision shows.
 """
 from __future__ import annotations
 
@@ -16,6 +18,7 @@ from _util import bf16_to_f32, log_case, to_dev, to_np
 pytestmark = pytest.mark.gpu
 
 PREFILL_TOL = 1e-2
+STATE_TOL = 5e-3
 D = 128
 
 
@@ -40,12 +43,13 @@ def run_prefill(gdn, dev, inp, Hk=16, o_dtype="bf16", precomputed=None):
     return o, to_np(out["state"]), None if out["conv_state"] is None else to_np(out["conv_state"])
 
 
-def check(O, got, ref, what):
+def check(O, got, ref, what, tol=PREFILL_TOL):
     r = O.rel_err(got, ref)
     m = O.max_abs(got, ref)
     print(f"  {what}: rel {r:.2e} max-abs {m:.2e}", flush=True)
     assert np.all(np.isfinite(got)), what
-    assert r <= PREFILL_TOL, (what, r)
+    assert r <= tol, (what, r)
+    return r
 
 
 @pytest.mark.parametrize("T", [1, 5, 63, 64, 65, 130, 200])
@@ -56,7 +60,7 @@ def test_prefill_conv_against_per_token(O, gdn, dev, T):
     ref = O.reference_layer(inp)
     o, S, conv = run_prefill(gdn, dev, inp)
     check(O, o, ref["o"], "o")
-    check(O, S, ref["state"], "state")
+    check(O, S, ref["state"], "state", STATE_TOL)
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
@@ -68,7 +72,7 @@ def test_prefill_continues_from_state_and_conv_state(O, gdn, dev, T):
     ref = O.reference_layer(inp)
     o, S, conv = run_prefill(gdn, dev, inp, o_dtype="f32")
     check(O, o, ref["o"], "o")
-    check(O, S, ref["state"], "state")
+    check(O, S, ref["state"], "state", STATE_TOL)
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
@@ -82,7 +86,7 @@ def test_prefill_qkv_precomputed_gates_equal_heads(O, gdn, dev):
     ro, rS = O.recurrent(q, k, v, al, be, inp.state)
     o, S, _ = run_prefill(gdn, dev, inp, Hk=8, o_dtype="f32", precomputed=(al, be))
     check(O, o, ro, "o")
-    check(O, S, rS, "state")
+    check(O, S, rS, "state", STATE_TOL)
 
 
 @pytest.mark.parametrize("Hk,Hv", [(8, 16), (4, 16), (2, 12), (4, 20)])
@@ -96,7 +100,7 @@ def test_prefill_other_head_ratios(O, gdn, dev, Hk, Hv):
     ref = O.reference_layer(inp)
     o, S, conv = run_prefill(gdn, dev, inp, Hk=Hk, o_dtype="f32")
     check(O, o, ref["o"], "o")
-    check(O, S, ref["state"], "state")
+    check(O, S, ref["state"], "state", STATE_TOL)
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
@@ -108,7 +112,7 @@ def test_prefill_4096_full(O, gdn, dev):
     ref = O.reference_layer(inp)
     o, S, conv = run_prefill(gdn, dev, inp)
     check(O, o, ref["o"], "o")
-    check(O, S, ref["state"], "state")
+    check(O, S, ref["state"], "state", STATE_TOL)
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
@@ -133,7 +137,46 @@ def test_prefill_then_decode_continues(O, gdn, dev):
                     state=state, o_dtype=torch.float32)
     torch.cuda.synchronize()
     check(O, to_np(out["o"]), ref["o"][:, 130:], "decode o after prefill")
-    check(O, to_np(out["state"]), ref["state"], "state after prefill + decode")
+    check(O, to_np(out["state"]), ref["state"], "state after prefill + decode", STATE_TOL)
+
+
+def test_prefill_1024_then_decode_16(O, gdn, dev):
+    """A 1024-token chunked prefill (the reference's prefill window, cpp/src/session.hpp:136)
+    followed by 16 single-token decode steps on the recurrent kernel, every output and the
+    state after every step against the per-token recurrence over all 1040 tokens: the
+    chunked form's state error is carried into decode and must not grow there. The drift
+    is printed per step."""
+    import torch
+    log_case("prefill 1024 then decode 16")
+    T0, N = 1024, 16
+    inp = O.make_inputs(config=4, layer=11, B=1, L=T0 + N, conv=True, conv_state=False,
+                        zero_state=True)
+    sl = lambda a, i, j: np.ascontiguousarray(a[:, i:j])  # noqa: E731
+    head = O.LayerInputs(None, None, None, sl(inp.x, 0, T0), inp.conv_w, None, sl(inp.a, 0, T0),
+                         sl(inp.b, 0, T0), inp.A_log, inp.dt_bias, None)
+    ref0 = O.reference_layer(head)
+    o, S, conv = run_prefill(gdn, dev, head)
+    check(O, o, ref0["o"], "prefill o")
+    check(O, S, ref0["state"], "prefill state", STATE_TOL)
+    state, conv_d = to_dev(S, dev), to_dev(conv, dev)
+    ref_state, ref_conv = ref0["state"], ref0["xp"][:, -3:]
+    d = lambda a: to_dev(a, dev)  # noqa: E731
+    errs = []
+    for t in range(T0, T0 + N):
+        step = O.LayerInputs(None, None, None, sl(inp.x, t, t + 1), inp.conv_w, ref_conv, sl(inp.a, t, t + 1),
+                             sl(inp.b, t, t + 1), inp.A_log, inp.dt_bias, ref_state)
+        ref = O.reference_layer(step)
+        out = gdn.layer(x=d(step.x), conv_weight=d(inp.conv_w), conv_state=conv_d, a=d(step.a), b=d(step.b),
+                        A_log=d(inp.A_log), dt_bias=d(inp.dt_bias), state=state, o_dtype=torch.float32)
+        torch.cuda.synchronize()
+        conv_d = out["conv_state"]
+        eo, es = O.rel_err(to_np(out["o"]), ref["o"]), O.rel_err(to_np(state), ref["state"])
+        errs.append((eo, es))
+        ref_state, ref_conv = ref["state"], ref["xp"][:, -3:]
+    print("  decode drift (o, state) per step: " + ", ".join(f"({a:.1e}, {b:.1e})" for a, b in errs), flush=True)
+    assert max(e[0] for e in errs) <= PREFILL_TOL
+    assert max(e[1] for e in errs) <= STATE_TOL
+    assert np.array_equal(to_np(conv_d), ref_conv)
 
 
 def _from_fragments(blocks, rows: int, cols: int):

@@ -462,10 +462,12 @@ def test_deltacache_spec_equals_plain(O, gdn, dev):
 
 def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
     """A block of at least chunked_min_t(B) tokens that is not recorded runs the chunked form
-    (python/qwen35.py:606-626 makes the same choice by length): a 100-token prefill through
-    DeltaCache.step and then one decode step, against the oracle's token-by-token recurrence
-    at the chunked form's tolerance (1e-2, the prefill tests'); the same calls with the
-    threshold raised run the recurrent kernel, at the recurrent tolerance (1e-4)."""
+    (python/qwen35.py:606-626 makes the same choice by length) in the workspace the cache
+    allocated at construction: a 100-token prefill through DeltaCache.step and then one
+    decode step, against the oracle's token-by-token recurrence at the chunked form's
+    tolerances (outputs 1e-2, state 5e-3: the prefill tests'); the same calls with the
+    threshold raised run the recurrent kernel, at the recurrent tolerance (1e-4). The step
+    allocates no workspace (torch.empty is watched while it runs)."""
     import torch
     mod = gdn.gdn
     calls = []
@@ -477,17 +479,28 @@ def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
     pre = O.reference_layer(O.LayerInputs(None, None, None, np.ascontiguousarray(inp.x[:, :T]), inp.conv_w,
                                           inp.conv_state, np.ascontiguousarray(inp.a[:, :T]),
                                           np.ascontiguousarray(inp.b[:, :T]), inp.A_log, inp.dt_bias, inp.state))
-    for threshold, tol in ((mod.CHUNKED_MIN_T, 1e-2), (10 ** 9, 1e-4)):
+    for threshold, tol, stol in ((mod.CHUNKED_MIN_T, 1e-2, 5e-3), (10 ** 9, 1e-4, 1e-4)):
         monkeypatch.setattr(mod, "CHUNKED_MIN_T", threshold)
         calls.clear()
         log_case(f"length dispatch: T={T} block then 1 token, threshold {threshold}")
-        c = gdn.DeltaCache(B, device=dev)
+        c = gdn.DeltaCache(B, device=dev, max_prefill_tokens=128)
         c.state.copy_(to_dev(inp.state, dev))
         c.conv.copy_(to_dev(inp.conv_state, dev))
         w, Al, dt = to_dev(inp.conv_w, dev), to_dev(inp.A_log, dev), to_dev(inp.dt_bias, dev)
         x, a, b = to_dev(inp.x, dev), to_dev(inp.a, dev), to_dev(inp.b, dev)
-        o1 = c.step(x[:, :T].contiguous(), w, a[:, :T].contiguous(), b[:, :T].contiguous(), Al, dt,
-                    o_dtype=torch.float32)
+        xs, as_, bs = x[:, :T].contiguous(), a[:, :T].contiguous(), b[:, :T].contiguous()
+        big = []
+        real_empty = torch.empty
+
+        def watched(*shape, **kw):   # workspaces are uint8 buffers
+            t = real_empty(*shape, **kw)
+            if t.dtype == torch.uint8:
+                big.append(t.numel())
+            return t
+        monkeypatch.setattr(torch, "empty", watched)
+        o1 = c.step(xs, w, as_, bs, Al, dt, o_dtype=torch.float32)
+        monkeypatch.setattr(torch, "empty", real_empty)
+        assert not big, f"DeltaCache.step allocated {big} bytes"
         torch.cuda.synchronize()
         e_o, e_s = O.rel_err(to_np(o1), pre["o"]), O.rel_err(to_np(c.state), pre["state"])
         o2 = c.step(x[:, T:].contiguous(), w, a[:, T:].contiguous(), b[:, T:].contiguous(), Al, dt,
@@ -497,7 +510,7 @@ def test_length_dispatch_long_block(O, gdn, dev, monkeypatch):
         print(f"  prefill o {e_o:.2e} state {e_s:.2e}; next token o {e_o2:.2e} state {e_s2:.2e}; "
               f"chunked calls {calls}", flush=True)
         assert calls == ([T] if mod.chunked_min_t(B) <= T else [])
-        assert max(e_o, e_s, e_o2, e_s2) <= tol
+        assert max(e_o, e_o2) <= tol and max(e_s, e_s2) <= stol
         assert np.array_equal(to_np(c.conv), ref["xp"][:, -3:])
     # layer() with q, k, v given (bf16) takes the same choice
     monkeypatch.setattr(mod, "CHUNKED_MIN_T", 20)
