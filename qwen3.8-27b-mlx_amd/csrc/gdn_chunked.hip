@@ -14,14 +14,15 @@
 //   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position into bf16 q, k
 //                  (B, T, Hk, 128) and v, which goes straight into the fragment order of
 //                  U's B operand (with q, k, v given by the caller, prefill_vfrag reorders
-//                  v instead).
+//                  v instead). Extra workgroups of the same launch compute the gates and
+//                  each chunk's cumulative log decay G (one wave per (v-head, chunk)).
 //   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
-//                  per CU: K K^T and K Q^T on bf16 MFMA, and for the k-head's v-heads the
-//                  gates, A and M, T = (I + A)^-1 (one wave per v-head, fp32, left in LDS),
+//                  per CU: K K^T and K Q^T on bf16 MFMA, and for the k-head's v-heads
+//                  A and M, T = (I + A)^-1 (one wave per v-head, fp32, left in LDS),
 //                  U = T'V and W = T'diag(e^G)K on bf16 MFMA, every wave building its T'
 //                  fragments from T in LDS (T' split into bf16 hi + lo for U). Results go
 //                  to the workspace, already in the register order of the MFMA operands
-//                  that read them.
+//                  that read them; U as fp16 scaled by a power of two per 16-position tile.
 //   prefill_scan   one workgroup per (batch, v-head, pair of 16-column Dv tiles), serial
 //                  over the chunks. Each of two state waves keeps its tile's fp32 state
 //                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain V' = U - W S,
@@ -61,6 +62,7 @@ typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;             // chunk
 constexpr int kPadB = 8;           // bf16 padding per LDS row
@@ -129,8 +131,11 @@ struct PrefillParams {
   __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
   __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
                   // blocks above the diagonal are left unwritten)
-  float* ws_u;    // (B, Hv, nC): U   (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]
+  _Float16* ws_u;  // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4],
+                   // fp16, each position tile multiplied by a power of two (below)
+  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile
   float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
+  float* ws_gb;   // (B, Hv, nC, kGStride): (G, beta) per position
   __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
                   // block 2 (dv / 16) + pos / 32, lane 16 ((pos % 32) / 8) + dv % 16, element
                   // pos % 8; positions past T are zeros
@@ -187,6 +192,53 @@ struct IntraSmem {
   } u;
 };
 
+// ============================================================================ gates
+
+constexpr int kGateHeads = 4;  // v-heads per gate workgroup (one per wave)
+
+// Gate workgroups per call: (batch, chunk, group of kGateHeads v-heads).
+__host__ __device__ __forceinline__ int gate_blocks(int B, int nC, int Hv) {
+  return B * nC * ((Hv + kGateHeads - 1) / kGateHeads);
+}
+
+// Gates (model.cpp:608-612) and the in-chunk cumulative log decay of one (batch, chunk,
+// v-head) per wave, lane = position: G_i = sum_{m<=i} log clip(alpha_m, 1e-6, 1)
+// (qwen35.py:397-400). Writes (e^G, e^(G63-G)) to ws_g and (G, beta) to ws_gb. Padded
+// steps past T get alpha 1, beta 0 (exact no-ops). Run by extra workgroups of the front-end
+// (or v reorder) launch, which have no barriers, so a wave past Hv just returns.
+__device__ __forceinline__ void gates_block(const PrefillParams& p, int gb) {
+  const int hgroups = (p.Hv + kGateHeads - 1) / kGateHeads;
+  const int hg = gb % hgroups;
+  gb /= hgroups;
+  const int c = gb % p.nC;
+  const int b = gb / p.nC;
+  const int lane = threadIdx.x & 63;
+  const int h = hg * kGateHeads + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (h >= p.Hv) return;
+  const int t0 = c * kC, n = min(kC, p.T - t0);
+  float al = 1.0f, be = 0.0f;
+  if (lane < n) {
+    const size_t gi = ((size_t)b * p.T + t0 + lane) * p.Hv + h;
+    if (p.gate_raw) {
+      d_gates(bf2f(p.a[gi]), bf2f(p.b[gi]), p.A_log[h], p.dt_bias[h], al, be);
+    } else {
+      al = p.alpha[gi];
+      be = p.beta[gi];
+    }
+  }
+  const float ac = al < 1e-6f ? 1e-6f : (al > 1.0f ? 1.0f : al);
+  float G = ac == 1.0f ? 0.0f : d_logf(ac);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float up = __shfl_up(G, off, 64);
+    if (lane >= off) G = G + up;
+  }
+  const float Gl = __shfl(G, 63, 64);
+  const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
+  reinterpret_cast<float2*>(p.ws_g + hc * kGStride)[lane] = make_float2(d_expf(G), d_expf(Gl - G));
+  reinterpret_cast<float2*>(p.ws_gb + hc * kGStride)[lane] = make_float2(G, be);
+}
+
 // ============================================================================ front end
 
 constexpr int kFePos = 32;   // positions per front-end workgroup
@@ -209,10 +261,15 @@ static_assert(kC == 2 * kFePos, "a chunk is two front-end position blocks");
 // VGPRs: four waves per SIMD for this VALU-bound kernel.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_frontend_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) __bf16 vtile[kFeHeads][kD][kFePos + 8];
+  const int ngate = gate_blocks(p.B, p.nC, p.Hv);
+  if ((int)blockIdx.x < ngate) {  // the gate workgroups come first in the grid
+    gates_block(p, blockIdx.x);
+    return;
+  }
   const int nheads = 2 * p.Hk + p.Hv;
   const int hgroups = (nheads + kFeHeads - 1) / kFeHeads;
   const int pblocks = (p.T + kFePos - 1) / kFePos;
-  int bid = blockIdx.x;
+  int bid = blockIdx.x - ngate;
   const int hg = bid % hgroups;
   bid /= hgroups;
   const int pb = bid % pblocks;
@@ -430,11 +487,26 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       qv[it] = *reinterpret_cast<const bf8*>(p.q + gi);
       kv[it] = *reinterpret_cast<const bf8*>(p.k + gi);
     }
+    // the first group's (G, beta, e^G), written by the front end's gate workgroups: wave r
+    // takes v-head r, lane = position (loaded behind q and k, so their waits come first)
+    const int gs0 = min(kGroup, p.rep);
+    float2 gb0 = make_float2(0.0f, 0.0f);
+    float eg0 = 0.0f;
+    if (wave < gs0) {
+      const size_t hc = ((size_t)b * p.Hv + g * p.rep + wave) * p.nC + c;
+      gb0 = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
+      eg0 = p.ws_g[hc * kGStride + 2 * lane];
+    }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
       *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = pos < n ? kv[it] : bf8{};
+    }
+    if (wave < gs0) {
+      s.G[wave][lane] = gb0.x;
+      s.beta[wave][lane] = gb0.y;
+      s.eG[wave][lane] = eg0;
     }
   }
   __syncthreads();
@@ -486,35 +558,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   const int rep_end = ONE_GROUP ? 1 : p.rep;
   for (int r0 = 0; r0 < rep_end; r0 += kGroup) {
     const int gs = min(kGroup, p.rep - r0);
-    // gates and the in-chunk log decay (wave r: v-head r0 + r, lane = position)
-    if (wave < gs) {
-      const int h = g * p.rep + r0 + wave;
-      const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
-      float al = 1.0f, be = 0.0f;  // padded steps: alpha 1, beta 0 (exact no-ops)
-      if (lane < n) {
-        const size_t gi = ((size_t)b * p.T + t0 + lane) * p.Hv + h;
-        if (p.gate_raw) {
-          d_gates(bf2f(p.a[gi]), bf2f(p.b[gi]), p.A_log[h], p.dt_bias[h], al, be);
-        } else {
-          al = p.alpha[gi];
-          be = p.beta[gi];
-        }
+    if (!ONE_GROUP && r0 > 0) {  // a later group's (G, beta, e^G) (the first came with q, k)
+      if (wave < gs) {
+        const size_t hc = ((size_t)b * p.Hv + g * p.rep + r0 + wave) * p.nC + c;
+        const float2 gb = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
+        s.G[wave][lane] = gb.x;
+        s.beta[wave][lane] = gb.y;
+        s.eG[wave][lane] = p.ws_g[hc * kGStride + 2 * lane];
       }
-      const float ac = al < 1e-6f ? 1e-6f : (al > 1.0f ? 1.0f : al);
-      float G = ac == 1.0f ? 0.0f : d_logf(ac);
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float up = __shfl_up(G, off, 64);
-        if (lane >= off) G = G + up;
-      }
-      s.G[wave][lane] = G;
-      s.beta[wave][lane] = be;
-      const float eg = d_expf(G);
-      s.eG[wave][lane] = eg;
-      const float Gl = __shfl(G, 63, 64);
-      reinterpret_cast<float2*>(p.ws_g + hc * kGStride)[lane] = make_float2(eg, d_expf(Gl - G));
+      __syncthreads();
     }
-    __syncthreads();
 
     // A (into LDS as -A^T) and M (hi, lo to the workspace) from the registers
     for (int r = 0; r < gs; ++r) {
@@ -597,7 +650,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
             te[kh][e] = (__bf16)(tv * ej[kh][e]);
           }
         }
-        float* wu = p.ws_u + hc * kChunkElems + lane * 4;
+        // U is stored as fp16 times 2^e, e from the position tile's largest magnitude (so
+        // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
+        f4 ut[kD / 16];
+        uint32_t mx = 0;
 #pragma unroll
         for (int d = 0; d < kD / 16; ++d) {
           f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -605,8 +661,20 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           acc = mfma(al[0], vb[d][0], acc);
           acc = mfma(ah[1], vb[d][1], acc);
           acc = mfma(al[1], vb[d][1], acc);
-          __builtin_nontemporal_store(acc, reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256));
+          ut[d] = acc;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(acc[e]) & 0x7fffffffu);
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+        const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
+        const float sc = bits_f((uint32_t)(127 + ex) << 23);
+        _Float16* wu = p.ws_u + hc * kChunkElems + lane * 4;
+#pragma unroll
+        for (int d = 0; d < kD / 16; ++d)
+          __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
+                                      reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
+        if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
         // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]
         __bf16* ww = p.ws_w + hc * kChunkElems;
 #pragma unroll
@@ -629,8 +697,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
 // then each thread writes four 16-byte pieces of eight consecutive positions.
 __global__ __launch_bounds__(kThreads) void prefill_vfrag_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) __bf16 vt[kD][kC + kPadB];
-  const int c = blockIdx.x % p.nC;
-  const int rest = blockIdx.x / p.nC;
+  const int ngate = gate_blocks(p.B, p.nC, p.Hv);
+  if ((int)blockIdx.x < ngate) {  // whole workgroups: the barrier below is never split
+    gates_block(p, blockIdx.x);
+    return;
+  }
+  const int vb = blockIdx.x - ngate;
+  const int c = vb % p.nC;
+  const int rest = vb / p.nC;
   const int h = rest % p.Hv;
   const int b = rest / p.Hv;
   const int t0 = c * kC, n = min(kC, p.T - t0);
@@ -680,7 +754,9 @@ struct ScanMail {
 struct StateOps {
   bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
   bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
-  f4 u[4];       // U   [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile
+  h4 u[4];       // U   [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile (fp16,
+                 // scaled by 1 / us[pt])
+  f4 us;         // the chunk's U scale factors, one per position tile
   float2 g;      // (e^G, e^(G63-G)) at position `lane`
 };
 
@@ -717,8 +793,9 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
     t[0] = base[lane * 32];
     t[1] = base[(64 + lane) * 32];
   } else {
+    // (this workgroup's two dv tiles of U: 4 KB, 32 lines)
     base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
-    t[0] = base[lane * 32];
+    t[0] = base[(lane & 31) * 32];
     t[1] = reinterpret_cast<const unsigned*>(p.ws_g + hc * kGStride)[(lane & 3) * 32];
   }
 }
@@ -731,9 +808,10 @@ __device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int j
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
-  const float* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
+  const _Float16* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const f4*>(u + pt * 256);
+  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
+  op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
 __device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int i, int lane, StateOps& op) {
@@ -821,7 +899,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
     f4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) P = mfma(own ? op.w[r][ks] : wo[r][ks], sb[ks], P);
-    vpr[pt] = op.u[pt] - P;
+    vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P;
     mb.vpr[i][pt][lane] = vpr[pt];
   }
   bf8 vb[2];
@@ -1073,7 +1151,7 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, w, m, u, g, vf, fq, fk, total;
+  size_t q, kt, w, m, u, g, vf, fq, fk, us, gb, total;
 };
 
 // conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
@@ -1083,7 +1161,7 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
   const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
-  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * 4);
+  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * 2);
   const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
   WorkspaceLayout L;
   L.q = 0;
@@ -1096,7 +1174,9 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
   L.vf = L.g + gg;
   L.fq = L.vf + wm;
   L.fk = L.fq + fqk;
-  L.total = L.fk + fqk;
+  L.us = L.fk + fqk;
+  L.gb = L.us + al((size_t)B * Hv * nC * 4 * 4);
+  L.total = L.gb + gg;
   return L;
 }
 
@@ -1141,7 +1221,9 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
   p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
   p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
-  p.ws_u = reinterpret_cast<float*>(w + L.u);
+  p.ws_u = reinterpret_cast<_Float16*>(w + L.u);
+  p.ws_us = reinterpret_cast<float*>(w + L.us);
+  p.ws_gb = reinterpret_cast<float*>(w + L.gb);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {
@@ -1151,6 +1233,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   }
 
   const dim3 block(kThreads);
+  const size_t ngate = (size_t)gate_blocks(p.B, p.nC, p.Hv);
   const dim3 g1((unsigned)((size_t)p.B * p.Hk * p.nC));
   const dim3 g2((unsigned)((size_t)p.B * p.Hv * kScanGroups));
   // events[0..3] (when given) are recorded before the first kernel and after each
@@ -1160,10 +1243,10 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   mark(0);
   if (conv) {
     const size_t nh = ((size_t)2 * p.Hk + p.Hv + kFeHeads - 1) / kFeHeads;
-    const dim3 g0((unsigned)((size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
+    const dim3 g0((unsigned)(ngate + (size_t)p.B * ((p.T + kFePos - 1) / kFePos) * nh));
     hipLaunchKernelGGL(prefill_frontend_kernel, g0, block, 0, stream, p);
   } else {
-    const dim3 gv((unsigned)((size_t)p.B * p.Hv * p.nC));
+    const dim3 gv((unsigned)(ngate + (size_t)p.B * p.Hv * p.nC));
     hipLaunchKernelGGL(prefill_vfrag_kernel, gv, block, 0, stream, p);
   }
   mark(1);

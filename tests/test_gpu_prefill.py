@@ -256,7 +256,7 @@ def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
     al = lambda n: -(-n // 256) * 256  # noqa: E731  (byte sizes of the workspace pieces)
     nC = 1
     qk, wm = B * Hk * nC * 8192 * 2, B * Hv * nC * 8192 * 2
-    uu, gg = B * Hv * nC * 8192 * 4, B * Hv * nC * 128 * 4
+    uu, gg = B * Hv * nC * 8192 * 2, B * Hv * nC * 128 * 4   # U is fp16
     vf_off = (2 * al(qk) + 2 * al(wm) + al(uu) + al(gg)) // 2
     vf = raw[vf_off:vf_off + Hv * 8192].reshape(Hv, 8192)
     pos = np.arange(T)[:, None]
