@@ -226,22 +226,25 @@ def prefill_flops(T: int, C: int = 64):
     return intra, inter
 
 
-def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096):
+def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096, precision: int = 0):
+    """One layer, B = 1, conv front end; `precision` is gdn_prefill_precision (0, the default
+    fp32-state form, keeps U in fp32 and splits V'' for the state update; 1 is the fast
+    form)."""
     i = make_layer_inputs(torch, dev, 1, 1, T, True, seed=500)
     x = i["x"][0].contiguous()
     o = torch.empty((1, T, HV, D), dtype=torch.bfloat16, device=dev)
     state_out = torch.empty((1, HV, D, D), device=dev)
     conv_out = torch.empty((1, 3, C), dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(gdn.prefill_workspace_size(1, T), dtype=torch.uint8, device=dev)
+    ws = torch.empty(gdn.prefill_workspace_size(1, T, precision=precision), dtype=torch.uint8, device=dev)
     args = gdn.layer_args(B=1, T=T, x=x, conv_weight=i["conv_weight"][0].contiguous(),
                           conv_state_in=None, conv_state_out=conv_out, a=i["a"][0].contiguous(),
                           b=i["b"][0].contiguous(), A_log=i["A_log"][0].contiguous(),
                           dt_bias=i["dt_bias"][0].contiguous(), state_in=None,
-                          state_out=state_out, o=o, workspace=ws)
+                          state_out=state_out, o=o, workspace=ws, precision=precision)
     r = timer.time_calls(lambda it: gdn.call_prefill(args), steps, warmup, host_us_per_call=80.0)
     intra, inter = prefill_flops(T)
     sec = r["ms_per_step"] * 1e-3
-    traffic = load_traffic("prefill_t4096_b1_conv") if T == 4096 else None
+    traffic = load_traffic("prefill_t4096_b1_conv") if T == 4096 and precision == 0 else None
     # each kernel between its own event pair (gdn_prefill_chunked_timed; outside the timed
     # region above: every such call waits for its events). A short spin queued ahead of each
     # call keeps the stream busy while the call is enqueued, so that the first kernel's
@@ -257,7 +260,8 @@ def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096
                 all_products_frac_mfma=(intra + inter) / sec / (MFMA_BF16_PEAK_TFLOPS * 1e12),
                 intra_flop=intra, inter_flop=inter,
                 hbm_bytes=traffic, hbm_GBps=None if traffic is None else traffic / sec / 1e9,
-                per_kernel=prefill_kernel_fracs(event_us) if T == 4096 else None)
+                per_kernel=prefill_kernel_fracs(event_us) if T == 4096 and precision == 0 else None,
+                event_us=[round(u, 2) for u in event_us])
 
 
 def prefill_kernel_fracs(event_us=None):
@@ -614,6 +618,13 @@ def main() -> int:
                   f"intra {ki['event_us']:.1f} us (MFMA {ki['frac_mfma_normative_event']:.4f} normative, "
                   f"{ki['frac_mfma_executed_event']:.4f} executed), scan {ks['event_us']:.1f} us "
                   f"({ks['frac_mfma_executed_event']:.4f} executed)", flush=True)
+        # the fast form (GDN_PREFILL_FAST: bf16 V'' in the state update, U as fp16) beside it
+        rf = bench_prefill(torch, gdn, dev, timer, steps=max(5, args.steps // 10), warmup=3, precision=1)
+        sec["prefill_t4096_fast"] = dict(us_per_call=round(rf["us_per_call"], 2),
+                                         tokens_per_s=round(rf["tokens_per_s"], 1),
+                                         intra_frac_mfma=round(rf["intra_frac_mfma"], 4),
+                                         event_us=rf["event_us"])
+        print(f"# prefill T=4096 fast form: {rf['us_per_call']:.1f} us (kernels {rf['event_us']} us)", flush=True)
     for which in ("in_proj", "out_proj"):
         if want(which):
             r = bench_qlinear(torch, gdn, dev, timer, steps=max(10, args.steps // 4), warmup=5, which=which)

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 4
+#define GDN_ABI_VERSION 5
 #define GDN_HEAD_DIM 128 /* Dk = Dv */
 #define GDN_CONV_TAPS 4  /* conv kernel size; the conv state holds GDN_CONV_TAPS-1 rows */
 
@@ -74,6 +74,23 @@ typedef enum gdn_gate_mode {
   GDN_GATES_RAW = 0,        /* a, b logits with A_log, dt_bias: the gate math runs inside */
   GDN_GATES_PRECOMPUTED = 1 /* alpha, beta given in fp32, as delta::run takes them */
 } gdn_gate_mode;
+
+/* Arithmetic of gdn_prefill_chunked (gdn_run computes in fp32 either way). */
+typedef enum gdn_prefill_precision {
+  GDN_PREFILL_ACCURATE = 0, /* the default: U kept in fp32 and V'' split into bf16 hi + lo
+                               for the state update K^T V'' -- the chunked form's largest
+                               error term (the reference runs an fp32 kernel for every window,
+                               cpp/src/model.cpp:619-624). What remains are the bf16 roundings
+                               of S and W in V' = U - W S, which a chunk forgets as fast as
+                               its gates decay: with the benchmark's gates (alpha <= 0.8) the
+                               state ends within about 5e-6 (max|a-b|/max|b|, T = 1024..4096)
+                               of the fp32 recurrence, up to about 4e-4 when the last chunk
+                               holds a few tokens; with gates near 1 (alpha >= 0.99) about
+                               1.5e-3. Never further than GDN_PREFILL_FAST. */
+  GDN_PREFILL_FAST = 1      /* bf16 V'' in the state update and U kept as fp16: the state ends
+                               about 2e-3 from the fp32 recurrence; a smaller workspace and
+                               about 5 % less time at T = 4096 */
+} gdn_prefill_precision;
 
 typedef enum gdn_states_layout {
   GDN_STATES_BHT = 0, /* (B, Hv, T, Dv, Dk): the reference's S_all order (delta.cpp:88) */
@@ -124,6 +141,9 @@ typedef struct gdn_layer_args {
                             gdn_prefill_workspace_size() bytes, 256-byte aligned */
   size_t workspace_bytes;
   void* stream;          /* hipStream_t */
+  int prefill_precision; /* gdn_prefill_precision (0, GDN_PREFILL_ACCURATE, when zeroed):
+                            gdn_prefill_chunked and gdn_prefill_workspace_size; gdn_run
+                            accepts either value */
 } gdn_layer_args;
 
 /* Recurrent form for any T (decode T = 1; speculative verify with `states`). The
@@ -136,8 +156,9 @@ int gdn_run(const gdn_layer_args* args);
  * except that `states` must be NULL, a workspace is required, o and x and conv_state_in
  * (conv front end) or q, k and v (qkv front end) must be 16-byte aligned, and the qkv
  * front end takes bf16 q, k, v only. Intra-chunk products run on bf16 MFMA with fp32 accumulation;
- * the state hand-off between chunks stays fp32. The workspace contents are scratch: they
- * need no initialisation and are meaningless afterwards. */
+ * the state hand-off between chunks stays fp32; prefill_precision chooses how closely the
+ * final state follows the fp32 recurrence (gdn_prefill_precision). The workspace contents
+ * are scratch: they need no initialisation and are meaningless afterwards. */
 int gdn_prefill_chunked(const gdn_layer_args* args);
 
 /* gdn_prefill_chunked with a HIP event recorded before its first kernel and after each of
@@ -149,8 +170,9 @@ int gdn_prefill_chunked(const gdn_layer_args* args);
 int gdn_prefill_chunked_timed(const gdn_layer_args* args, float* kernel_ms);
 
 /* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
- * counts and front end (the conv front end also stages its bf16 q, k in the workspace);
- * the other fields are not read. */
+ * counts, front end (the conv front end also stages its bf16 q, k in the workspace) and
+ * prefill_precision (GDN_PREFILL_ACCURATE keeps U in fp32); the other fields are not
+ * read. */
 int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {

@@ -104,11 +104,17 @@ class DeltaCache {
   // used in turn: commit(n) adopts step n-1 of the block by pointer (no copy), and the
   // next block is recorded into the other buffer, which no longer holds the live state.
   // Blocks of chunked_min_t(batch) .. max_prefill_tokens tokens (the reference prefills in windows of
-  // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here;
-  // max_prefill_tokens = 0 keeps every block on the recurrent kernel.
-  DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0)
+  // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here, with
+  // `prefill_precision` (gdn_prefill_precision: GDN_PREFILL_ACCURATE, the default, keeps
+  // U in fp32 and splits the state update's V'' into bf16 hi + lo, which leaves the state the
+  // next decode step starts from within about 5e-6 of the fp32 recurrence for fast-decaying
+  // gates and 1.5e-3 for gates near 1; GDN_PREFILL_FAST about 2e-3 either way);
+  // max_prefill_tokens = 0 keeps every block on the exact recurrent kernel.
+  DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0,
+             int prefill_precision = GDN_PREFILL_ACCURATE)
       : p_(p), B_(batch), max_T_(max_record_steps),
-        max_prefill_T_(max_prefill_tokens >= chunked_min_t(batch) ? max_prefill_tokens : 0) {
+        max_prefill_T_(max_prefill_tokens >= chunked_min_t(batch) ? max_prefill_tokens : 0),
+        precision_(prefill_precision) {
     const size_t D = GDN_HEAD_DIM;
     state_bytes_ = (size_t)B_ * p_.num_v_heads * D * D * sizeof(float);
     conv_bytes_ = (size_t)B_ * (GDN_CONV_TAPS - 1) * p_.conv_dim() * 2;
@@ -124,6 +130,7 @@ class DeltaCache {
       w.num_k_heads = p_.num_k_heads;
       w.num_v_heads = p_.num_v_heads;
       w.frontend = GDN_FRONTEND_CONV;
+      w.prefill_precision = precision_;
       check(gdn_prefill_workspace_size(&w, &ws_bytes_));
       check_hip(hipMalloc(&ws_, ws_bytes_), "hipMalloc prefill workspace");
     }
@@ -193,6 +200,7 @@ class DeltaCache {
       if (T >= chunked_min_t(B_) && T <= max_prefill_T_ && aligned) {
         g.workspace = ws_;
         g.workspace_bytes = ws_bytes_;
+        g.prefill_precision = precision_;
         check(gdn_prefill_chunked(&g));
       } else {
         check(gdn_run(&g));
@@ -236,6 +244,7 @@ class DeltaCache {
   int B_;
   int max_T_;
   int max_prefill_T_;
+  int precision_;
   size_t state_bytes_ = 0, conv_bytes_ = 0, ws_bytes_ = 0;
   void* ws_ = nullptr;
   bool holds_state(const float* rec) const {

@@ -2,7 +2,7 @@
 include/gdn.h, with a Python mirror of the reference's per-layer interface."""
 from .gdn import (  # noqa: F401
     CHUNKED_MIN_T, chunked_min_t, CONV_TAPS, DTYPE_BF16, DTYPE_F32, EXPORTS, FRONTEND_CONV, FRONTEND_QKV, GATES_PRECOMPUTED,
-    GATES_RAW, GDN_EDEVICE, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_OK, HEAD_DIM, LIB_PATH,
+    GATES_RAW, GDN_EDEVICE, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_OK, HEAD_DIM, LIB_PATH, PREFILL_FAST, PREFILL_ACCURATE,
     STATES_BHT, STATES_TBH, CommitArgs, DeltaCache, GdnError, LayerArgs, Result, available,
     call_commit, call_prefill, call_prefill_timed, call_qlinear, call_qlinear_noalloc, call_run, commit, last_error, layer, layer_args,
     lib, prefill_chunked, prefill_workspace_size, qlinear, qlinear_args, QLinearArgs,

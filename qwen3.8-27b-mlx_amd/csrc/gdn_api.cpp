@@ -16,7 +16,7 @@
 
 namespace gdn {
 int recurrent_tile_rows(long long heads);
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv);
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv, bool precise);
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
                                   hipEvent_t* events);
 }  // namespace gdn
@@ -114,6 +114,8 @@ int validate_layer(const gdn_layer_args* a, const char* fn, bool allow_states) {
     return fail(GDN_EINVAL, "%s: unknown qkv_dtype %d", fn, a->qkv_dtype);
   if (a->states_layout != GDN_STATES_BHT && a->states_layout != GDN_STATES_TBH)
     return fail(GDN_EINVAL, "%s: unknown states_layout %d", fn, a->states_layout);
+  if (a->prefill_precision != GDN_PREFILL_FAST && a->prefill_precision != GDN_PREFILL_ACCURATE)
+    return fail(GDN_EINVAL, "%s: unknown prefill_precision %d", fn, a->prefill_precision);
   if (!allow_states && a->states)
     return fail(GDN_EINVAL, "%s: per-step states are not produced by this entry point", fn);
 
@@ -362,8 +364,11 @@ int gdn_prefill_workspace_size(const gdn_layer_args* a, size_t* bytes) {
   if (!a || !bytes) return fail(GDN_EINVAL, "gdn_prefill_workspace_size: NULL argument");
   if (a->batch < 0 || a->seq_len < 0 || a->num_k_heads < 1 || a->num_v_heads < 1)
     return fail(GDN_EINVAL, "gdn_prefill_workspace_size: bad shape");
+  if (a->prefill_precision != GDN_PREFILL_FAST && a->prefill_precision != GDN_PREFILL_ACCURATE)
+    return fail(GDN_EINVAL, "gdn_prefill_workspace_size: unknown prefill_precision %d", a->prefill_precision);
   *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads,
-                                        a->frontend == GDN_FRONTEND_CONV);
+                                        a->frontend == GDN_FRONTEND_CONV,
+                                        a->prefill_precision == GDN_PREFILL_ACCURATE);
   return ok();
 }
 
@@ -381,8 +386,9 @@ int prefill_validate(const gdn_layer_args* a) {
   if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16)))
     return fail(GDN_EINVAL, "gdn_prefill_chunked: q, k and v must be 16-byte aligned");
   if (!aligned(a->o, 16)) return fail(GDN_EINVAL, "gdn_prefill_chunked: o must be 16-byte aligned");
-  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads,
-                                                   a->num_v_heads, a->frontend == GDN_FRONTEND_CONV);
+  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads,
+                                                   a->frontend == GDN_FRONTEND_CONV,
+                                                   a->prefill_precision == GDN_PREFILL_ACCURATE);
   if (a->seq_len > 0) {
     if (!a->workspace || a->workspace_bytes < need)
       return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace of %zu bytes required (got %zu)", need,

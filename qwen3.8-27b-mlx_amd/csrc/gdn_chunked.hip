@@ -33,7 +33,9 @@
 //                  registers two chunks ahead of their use, and the output waves touch the
 //                  lines of the chunk four ahead so that they are in L2 when first asked
 //                  for. W S, Q S and K^T V'' use bf16 operands; M V' splits both operands
-//                  into bf16 hi + lo (three MFMAs).
+//                  into bf16 hi + lo (three MFMAs). With GDN_PREFILL_ACCURATE, U stays fp32
+//                  and V'' is split into bf16 hi + lo for K^T V'' (two MFMAs): the state
+//                  then follows the fp32 recurrence to about 1e-6 instead of 2e-3.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
@@ -131,9 +133,10 @@ struct PrefillParams {
   __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
   __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
                   // blocks above the diagonal are left unwritten)
-  _Float16* ws_u;  // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4],
-                   // fp16, each position tile multiplied by a power of two (below)
-  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile
+  void* ws_u;     // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]:
+                  // fp32 (GDN_PREFILL_ACCURATE), or fp16 with each position tile multiplied
+                  // by a power of two (below)
+  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile (fp16 U)
   float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
   float* ws_gb;   // (B, Hv, nC, kGStride): (G, beta) per position
   __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
@@ -461,7 +464,7 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
 // T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
 // scan that reads it back. (The front end's outputs, which this kernel reads, stay
 // cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
-template <bool ONE_GROUP>
+template <bool ONE_GROUP, bool PRECISE>
 __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) IntraSmem s;
   const int c = blockIdx.x % p.nC;
@@ -650,10 +653,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
             te[kh][e] = (__bf16)(tv * ej[kh][e]);
           }
         }
-        // U is stored as fp16 times 2^e, e from the position tile's largest magnitude (so
-        // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
         f4 ut[kD / 16];
-        uint32_t mx = 0;
 #pragma unroll
         for (int d = 0; d < kD / 16; ++d) {
           f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -662,19 +662,31 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           acc = mfma(ah[1], vb[d][1], acc);
           acc = mfma(al[1], vb[d][1], acc);
           ut[d] = acc;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(acc[e]) & 0x7fffffffu);
         }
+        if constexpr (PRECISE) {
+          float* wu = static_cast<float*>(p.ws_u) + hc * kChunkElems + lane * 4;
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
-        const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
-        const float sc = bits_f((uint32_t)(127 + ex) << 23);
-        _Float16* wu = p.ws_u + hc * kChunkElems + lane * 4;
+          for (int d = 0; d < kD / 16; ++d)
+            __builtin_nontemporal_store(ut[d], reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256));
+        } else {
+          // U stored as fp16 times 2^e, e from the position tile's largest magnitude (so
+          // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
+          uint32_t mx = 0;
 #pragma unroll
-        for (int d = 0; d < kD / 16; ++d)
-          __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
-                                      reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
-        if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
+          for (int d = 0; d < kD / 16; ++d)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(ut[d][e]) & 0x7fffffffu);
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+          const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
+          const float sc = bits_f((uint32_t)(127 + ex) << 23);
+          _Float16* wu = static_cast<_Float16*>(p.ws_u) + hc * kChunkElems + lane * 4;
+#pragma unroll
+          for (int d = 0; d < kD / 16; ++d)
+            __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
+                                        reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
+          if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
+        }
         // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]
         __bf16* ww = p.ws_w + hc * kChunkElems;
 #pragma unroll
@@ -751,12 +763,13 @@ struct ScanMail {
 // read them. The two state waves of a workgroup need all of W and K^T; each loads half
 // (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles 4i .. 4i + 3) and passes it
 // to the other through LDS (ScanShared).
+template <bool PRECISE>
 struct StateOps {
   bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
   bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
-  h4 u[4];       // U   [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile (fp16,
-                 // scaled by 1 / us[pt])
-  f4 us;         // the chunk's U scale factors, one per position tile
+  typename std::conditional<PRECISE, f4, h4>::type u[4];  // U [pos tile]: positions 16 pt + 4 lg + e,
+                 // column fr of the wave's tile (fp32, or fp16 scaled by 1 / us[pt])
+  f4 us;         // the chunk's fp16 U scale factors, one per position tile
   float2 g;      // (e^G, e^(G63-G)) at position `lane`
 };
 
@@ -780,6 +793,7 @@ struct OutOps {
 // ahead: the v-head's four workgroups split W, M, Q and K^T between them (group `grp`
 // takes one of the four 16 KB matrices), and each workgroup touches its own U columns and
 // the gate pairs.
+template <bool PRECISE>
 __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, size_t hc, int grp, int jt, int half,
                                             int lane, unsigned (&t)[2]) {
   const unsigned* base;
@@ -793,28 +807,42 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
     t[0] = base[lane * 32];
     t[1] = base[(64 + lane) * 32];
   } else {
-    // (this workgroup's two dv tiles of U: 4 KB, 32 lines)
-    base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
-    t[0] = base[(lane & 31) * 32];
+    // this workgroup's two dv tiles of U: 8 KB (fp32), 64 lines, or 4 KB (fp16), 32 lines
+    if constexpr (PRECISE) {
+      base = reinterpret_cast<const unsigned*>(static_cast<const float*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256);
+      t[0] = base[lane * 32];
+    } else {
+      base = reinterpret_cast<const unsigned*>(static_cast<const _Float16*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256);
+      t[0] = base[(lane & 31) * 32];
+    }
     t[1] = reinterpret_cast<const unsigned*>(p.ws_g + hc * kGStride)[(lane & 3) * 32];
   }
 }
 
 // Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc: state wave
 // i's halves of W (with its tile jt's U and the gates) and of K^T.
-__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int i, int lane, StateOps& op) {
+template <bool PRECISE>
+__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int i, int lane,
+                                        StateOps<PRECISE>& op) {
   const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
-  const _Float16* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
+  if constexpr (PRECISE) {
+    const float* u = static_cast<const float*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
-  op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
+    for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const f4*>(u + pt * 256);
+  } else {
+    const _Float16* u = static_cast<const _Float16*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256 + lane * 4;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
+    op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
+  }
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
-__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int i, int lane, StateOps& op) {
+template <bool PRECISE>
+__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int i, int lane, StateOps<PRECISE>& op) {
   const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -865,10 +893,10 @@ struct ScanShared {
 // mail slot i. `op` holds this wave's share of chunk c's operands and is reloaded with
 // chunk cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk
 // ago) is written to the exchange slot of chunk c + 1.
-template <int NT, int i>
+template <int NT, int i, bool PRECISE>
 __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared& sh, f4 (&S)[kD / 16],
-                                            StateOps& op, const StateOps& nx, size_t gcn, size_t hcn, int jt, int slot,
-                                            int lane) {
+                                            StateOps<PRECISE>& op, const StateOps<PRECISE>& nx, size_t gcn, size_t hcn,
+                                            int jt, int slot, int lane) {
   constexpr int o = i ^ 1;
   // the other wave's halves of this chunk's W and K^T
   bf8 wo[2][4], kto[4][2];
@@ -899,33 +927,55 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
     f4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kD / 32; ++ks) P = mfma(own ? op.w[r][ks] : wo[r][ks], sb[ks], P);
-    vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P;
+    if constexpr (PRECISE) {
+      vpr[pt] = op.u[pt] - P;
+    } else {
+      vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P;
+    }
     mb.vpr[i][pt][lane] = vpr[pt];
   }
-  bf8 vb[2];
+  // V'' = e^(G63 - G) V' in bf16 for K^T V''; with PRECISE also its remainder V''_lo, so
+  // that K^T V''_hi + K^T V''_lo (K^T is exact in bf16) carries V'' into the state at fp32
+  // accuracy. The bf16 rounding of V'' is what moves the state (about 2e-3 from the fp32
+  // recurrence at T = 4096); the roundings of S and W in V' = U - W S are corrected by the
+  // following chunks' delta-rule updates.
+  bf8 vb[2], vbl[2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) vb[ks] = stack_bf8(egr[2 * ks] * vpr[2 * ks], egr[2 * ks + 1] * vpr[2 * ks + 1]);
+  for (int ks = 0; ks < 2; ++ks) {
+    const f4 v0 = egr[2 * ks] * vpr[2 * ks], v1 = egr[2 * ks + 1] * vpr[2 * ks + 1];
+    const bf4 h0 = to_bf4(v0), h1 = to_bf4(v1);
+    vb[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    if constexpr (PRECISE) vbl[ks] = stack_bf8(v0 - from_bf4(h0), v1 - from_bf4(h1));
+  }
   // S = e^G63 S + K^T V'', with the reloads of chunk cn's share spread between its MFMAs
   // (one load after each): loads issued in a burst queue up in the CU's address unit
   // behind the other waves' and hold this wave at the issue.
   __builtin_amdgcn_sched_barrier(0);
-  load_wu(p, hcn, jt, i, lane, op);
+  load_wu<PRECISE>(p, hcn, jt, i, lane, op);
 #pragma unroll
   for (int a = 0; a < kD / 16; ++a) {
     const int r = a & 3;
     const bool own = (a >> 2) == i;
     f4 acc = S[a] * gam;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) acc = mfma(own ? op.kt[r][ks] : kto[r][ks], vb[ks], acc);
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf8 kt = own ? op.kt[r][ks] : kto[r][ks];
+      acc = mfma(kt, vb[ks], acc);
+      if constexpr (PRECISE) acc = mfma(kt, vbl[ks], acc);
+    }
     S[a] = acc;
   }
-  load_kt(p, gcn, i, lane, op);
+  load_kt<PRECISE>(p, gcn, i, lane, op);
+  // 16 (32) MFMAs and 21 (22 with the fp16 U scales) loads
+  constexpr int kMfma = PRECISE ? 32 : 16, kLoads = PRECISE ? 21 : 22;
+  constexpr int kPairs = kMfma < kLoads ? kMfma : kLoads;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
+  for (int k = 0; k < kPairs; ++k) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
   }
-  __builtin_amdgcn_sched_group_barrier(0x020, 5, 0);
+  if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+  if constexpr (kLoads > kPairs) __builtin_amdgcn_sched_group_barrier(0x020, kLoads - kPairs, 0);
   __builtin_amdgcn_sched_barrier(0);
   // chunk c + 1's share for the other wave (the slot was last read in chunk c - 1)
 #pragma unroll
@@ -945,7 +995,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
 // in the order the loop reissues them so that the loop is entered with the same loads in
 // flight as at its back edge. Barriers: one after chunk 0's shares are exchanged, one per
 // chunk, one at the end, as the output waves.
-template <int NT, int i>
+template <int NT, int i, bool PRECISE>
 __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared& sh,
                                                 int b, int h, int g, int jt, int lane) {
   const int fr = lane & 15, lg = lane >> 4;
@@ -964,15 +1014,15 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   }
 
   const int last = p.nC - 1;
-  StateOps A, B;
+  StateOps<PRECISE> A, B;
   __builtin_amdgcn_sched_barrier(0);
-  load_wu(p, hc0, jt, i, lane, A);
+  load_wu<PRECISE>(p, hc0, jt, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt(p, gc0, i, lane, A);
+  load_kt<PRECISE>(p, gc0, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_wu(p, hc0 + min(1, last), jt, i, lane, B);
+  load_wu<PRECISE>(p, hc0 + min(1, last), jt, i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt(p, gc0 + min(1, last), i, lane, B);
+  load_kt<PRECISE>(p, gc0 + min(1, last), i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < 2; ++r)
@@ -985,10 +1035,10 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   __syncthreads();
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
-    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
-    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
+    state_chunk<NT, i, PRECISE>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
+    state_chunk<NT, i, PRECISE>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
   }
-  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
+  if (c < p.nC) state_chunk<NT, i, PRECISE>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
   __syncthreads();
 
   if (p.state_out) {
@@ -1031,7 +1081,7 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile
 // chunk cn's operands and touches the lines of chunk c + 4 (gc4, hc4). The touches issued
 // with this set two chunks ago have long arrived: they are folded into `tacc` only so that
 // they stay live.
-template <int NT, bool OBF16>
+template <int NT, bool OBF16, bool PRECISE>
 __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
                                              OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                              OutOps& op, size_t gcn, size_t hcn, size_t gc4, size_t hc4, int b, int h,
@@ -1077,12 +1127,12 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   }
   __builtin_amdgcn_sched_barrier(0);
   load_qm(p, gcn, hcn, half, lane, op);
-  touch_lines(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
+  touch_lines<PRECISE>(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // done with mail[c % 2]; mail[(c + 1) % 2] is complete
 }
 
-template <int NT, bool OBF16>
+template <int NT, bool OBF16, bool PRECISE>
 __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                                  int b, int h, int g, int jt, int half, int lane) {
@@ -1095,22 +1145,22 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
   OutOps A, B;
   __builtin_amdgcn_sched_barrier(0);
   load_qm(p, gc0, hc0, half, lane, A);
-  touch_lines(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
+  touch_lines<PRECISE>(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
   __builtin_amdgcn_sched_barrier(0);
   load_qm(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
-  touch_lines(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
+  touch_lines<PRECISE>(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the state waves' exchange of chunk 0's shares
   __syncthreads();  // chunk 0's mail
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
-    output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
+    output_chunk<NT, OBF16, PRECISE>(p, mail[0], tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
                             gc0 + min(c + 4, last), hc0 + min(c + 4, last), b, h, jt, half, c, lane, tacc);
-    output_chunk<NT, OBF16>(p, mail[1], tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
+    output_chunk<NT, OBF16, PRECISE>(p, mail[1], tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
                             gc0 + min(c + 5, last), hc0 + min(c + 5, last), b, h, jt, half, c + 1, lane, tacc);
   }
   if (c < p.nC)
-    output_chunk<NT, OBF16>(p, mail[0], tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half, c,
+    output_chunk<NT, OBF16, PRECISE>(p, mail[0], tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half, c,
                             lane, tacc);
   store_tile<NT, OT>(p, tile, b, h, jt, half, p.nC - 1, lane);
   // (never true: T >= 1; it keeps the touches from being dropped as unused)
@@ -1120,7 +1170,7 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
 // Workgroup = (batch, v-head, NT 16-column Dv tiles): waves 0 .. NT-1 carry the state of
 // one tile each, waves NT and NT + 1 make the outputs of position tiles {0, 3} and {1, 2}
 // of each chunk for all NT tiles. All waves pass nC + 2 barriers.
-template <int NT, bool OBF16>
+template <int NT, bool OBF16, bool PRECISE>
 __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   static_assert(NT == 2, "two state waves exchange halves of W and K^T");
@@ -1142,11 +1192,11 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave == 0) {
-    scan_state_wave<NT, 0>(p, mail, shared_ops, b, h, g, jt, lane);
+    scan_state_wave<NT, 0, PRECISE>(p, mail, shared_ops, b, h, g, jt, lane);
   } else if (wave == 1) {
-    scan_state_wave<NT, 1>(p, mail, shared_ops, b, h, g, jt + 1, lane);
+    scan_state_wave<NT, 1, PRECISE>(p, mail, shared_ops, b, h, g, jt + 1, lane);
   } else {
-    scan_output_wave<NT, OBF16>(p, mail, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
+    scan_output_wave<NT, OBF16, PRECISE>(p, mail, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
   }
 }
 
@@ -1156,12 +1206,13 @@ struct WorkspaceLayout {
 
 // conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
 // goes to vf, which the qkv front end fills from the caller's v).
-WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
+// precise: U in fp32 (GDN_PREFILL_ACCURATE), else fp16.
+WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
   const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
-  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * 2);
+  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * (precise ? 4 : 2));
   const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
   WorkspaceLayout L;
   L.q = 0;
@@ -1182,8 +1233,8 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv) {
 
 }  // namespace
 
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv) {
-  return workspace_layout(B, T, Hk, Hv, conv).total;
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv, bool precise) {
+  return workspace_layout(B, T, Hk, Hv, conv, precise).total;
 }
 
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
@@ -1215,13 +1266,14 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.state_out = a.state_out;
   p.o = a.o;
   const bool conv = a.frontend == GDN_FRONTEND_CONV;
-  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv, conv);
+  const bool precise = a.prefill_precision == GDN_PREFILL_ACCURATE;
+  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv, conv, precise);
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
   p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
   p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
-  p.ws_u = reinterpret_cast<_Float16*>(w + L.u);
+  p.ws_u = w + L.u;
   p.ws_us = reinterpret_cast<float*>(w + L.us);
   p.ws_gb = reinterpret_cast<float*>(w + L.gb);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
@@ -1251,15 +1303,20 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   }
   mark(1);
   if (p.rep <= kGroup) {
-    hipLaunchKernelGGL((prefill_intra_kernel<true>), g1, block, 0, stream, p);
+    if (precise) hipLaunchKernelGGL((prefill_intra_kernel<true, true>), g1, block, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_intra_kernel<true, false>), g1, block, 0, stream, p);
   } else {
-    hipLaunchKernelGGL((prefill_intra_kernel<false>), g1, block, 0, stream, p);
+    if (precise) hipLaunchKernelGGL((prefill_intra_kernel<false, true>), g1, block, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_intra_kernel<false, false>), g1, block, 0, stream, p);
   }
   mark(2);
+  const dim3 sb(64 * (kScanNt + 2));
   if (p.o_bf16) {
-    hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
+    if (precise) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true, true>), g2, sb, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true, false>), g2, sb, 0, stream, p);
   } else {
-    hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false>), g2, dim3(64 * (kScanNt + 2)), 0, stream, p);
+    if (precise) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false, true>), g2, sb, 0, stream, p);
+    else hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false, false>), g2, sb, 0, stream, p);
   }
   mark(3);
   return hipGetLastError();

@@ -27,6 +27,7 @@ GDN_OK, GDN_EINVAL, GDN_EUNSUPPORTED, GDN_EDEVICE = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F32 = 0, 1
 FRONTEND_QKV, FRONTEND_CONV = 0, 1
 GATES_RAW, GATES_PRECOMPUTED = 0, 1
+PREFILL_ACCURATE, PREFILL_FAST = 0, 1  # gdn_prefill_precision; the first is the default
 STATES_BHT, STATES_TBH = 0, 1
 HEAD_DIM = 128
 CONV_TAPS = 4
@@ -83,6 +84,7 @@ class LayerArgs(ctypes.Structure):
         ("o", _vp), ("o_dtype", _int),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("stream", _vp),
+        ("prefill_precision", _int),
     ]
 
 
@@ -201,10 +203,12 @@ def qlinear_workspace_size(m: int, k: int, n_layers: int = 1) -> int:
     return n.value
 
 
-def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48, conv: bool = True) -> int:
-    """Workspace bytes of gdn_prefill_chunked; `conv` for the conv front end (x given)."""
+def prefill_workspace_size(B: int, T: int, Hk: int = 16, Hv: int = 48, conv: bool = True,
+                           precision: int = PREFILL_ACCURATE) -> int:
+    """Workspace bytes of gdn_prefill_chunked; `conv` for the conv front end (x given),
+    `precision` a PREFILL_* value."""
     args = LayerArgs(n_layers=1, batch=B, seq_len=T, num_k_heads=Hk, num_v_heads=Hv,
-                     frontend=FRONTEND_CONV if conv else FRONTEND_QKV)
+                     frontend=FRONTEND_CONV if conv else FRONTEND_QKV, prefill_precision=precision)
     out = ctypes.c_size_t(0)
     _check(lib().gdn_prefill_workspace_size(ctypes.byref(args), ctypes.byref(out)))
     return out.value
@@ -280,7 +284,7 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
                conv_state_out=None, a=None, b=None, A_log=None, dt_bias=None, alpha=None,
                beta=None, state_in=None, state_out=None, states=None,
                states_layout: int = STATES_BHT, o=None, workspace=None,
-               stream=None) -> LayerArgs:
+               stream=None, precision: int = PREFILL_ACCURATE) -> LayerArgs:
     """Fill gdn_layer_args from torch tensors (front end and gate mode inferred)."""
     conv = x is not None
     raw = a is not None
@@ -298,7 +302,7 @@ def layer_args(*, B: int, T: int, Hk: int = 16, Hv: int = 48, n_layers: int = 1,
         o=_ptr(o), o_dtype=_dt(o) if o is not None else DTYPE_BF16,
         workspace=_ptr(workspace),
         workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size(),
-        stream=_stream(stream))
+        stream=_stream(stream), prefill_precision=precision)
 
 
 def _use_chunked(B: int, T: int, record: bool, x, q, tensors) -> bool:
@@ -314,7 +318,7 @@ def _use_chunked(B: int, T: int, record: bool, x, q, tensors) -> bool:
 
 def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
           conv_weight=None, conv_state=None, collect: bool = False, in_place: bool = True,
-          o_dtype=None, Hk: int = 16, workspace=None, stream=None):
+          o_dtype=None, Hk: int = 16, workspace=None, stream=None, precision: int = PREFILL_ACCURATE):
     """The per-layer call of GatedDeltaNet::operator() (cpp/src/model.cpp:585-641) at the
     recurrence: (q,k,v | x,conv) + (a,b,A_log,dt_bias) + state ->
     (o, state'). x is (B,T,C) bf16 for the conv front end; otherwise q,k (B,T,Hk,128),
@@ -323,10 +327,13 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     in `workspace` (uint8, at least prefill_workspace_size(B, T, ...) bytes), which is
     allocated here only when the caller gives none.
 
-    Precision: the chunked form's bf16 MFMA products leave the state about 2e-3 (relative,
-    T = 4096) from the fp32 recurrence, against about 1e-7 for the recurrent kernel the
-    reference's fp32 Metal kernel corresponds to (cpp/src/model.cpp:619-624); later decode
-    steps continue from that state."""
+    Precision (`precision`, PREFILL_*): PREFILL_ACCURATE, the default, keeps U in fp32 and
+    splits the state update's V'' into bf16 hi + lo, the chunked form's largest error term
+    against the reference's fp32 Metal kernel (cpp/src/model.cpp:619-624): the state then
+    ends within about 5e-6 (relative, T = 1024..4096) of the fp32 recurrence when the gates
+    decay fast (the benchmark's, alpha <= 0.8), about 1.5e-3 when they are near 1.
+    PREFILL_FAST (bf16 V'', U as fp16) leaves it about 2e-3 off for about 5 % less time. The
+    recurrent kernel is within about 1e-7. Later decode steps continue from that state."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
@@ -349,11 +356,12 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     ws = None
     if chunked:
         ws = workspace if workspace is not None else torch.empty(
-            prefill_workspace_size(B, T, Hk, Hv, conv=x is not None), dtype=torch.uint8, device=dev)
+            prefill_workspace_size(B, T, Hk, Hv, conv=x is not None, precision=precision), dtype=torch.uint8,
+            device=dev)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
                       A_log=A_log, dt_bias=dt_bias, state_in=state, state_out=state_out,
-                      states=states, o=o, workspace=ws, stream=stream)
+                      states=states, o=o, workspace=ws, stream=stream, precision=precision)
     (call_prefill if chunked else call_run)(args)
     return dict(o=o, state=state_out, states=states, conv_state=conv_out)
 
@@ -361,9 +369,10 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
 def prefill_chunked(*, x=None, q=None, k=None, v=None, a=None, b=None, A_log=None,
                     dt_bias=None, alpha=None, beta=None, state=None, conv_weight=None,
                     conv_state=None, o_dtype=None, Hk: int = 16, Hv: int = 48, workspace=None,
-                    stream=None):
+                    stream=None, precision: int = PREFILL_ACCURATE):
     """chunked_delta (python/qwen35.py:365-431) with the conv front end and gates inside.
-    Returns dict(o, state, conv_state). The workspace is allocated here unless given."""
+    Returns dict(o, state, conv_state). The workspace is allocated here unless given;
+    `precision` is a PREFILL_* value (see layer())."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
@@ -373,12 +382,12 @@ def prefill_chunked(*, x=None, q=None, k=None, v=None, a=None, b=None, A_log=Non
     conv_out = (torch.empty((B, CONV_TAPS - 1, x.shape[2]), dtype=torch.bfloat16, device=dev)
                 if x is not None else None)
     if workspace is None and T > 0:
-        workspace = torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None),
+        workspace = torch.empty(prefill_workspace_size(B, T, Hk, Hv, conv=x is not None, precision=precision),
                                 dtype=torch.uint8, device=dev)
     args = layer_args(B=B, T=T, Hk=Hk, Hv=Hv, q=q, k=k, v=v, x=x, conv_weight=conv_weight,
                       conv_state_in=conv_state, conv_state_out=conv_out, a=a, b=b,
                       A_log=A_log, dt_bias=dt_bias, alpha=alpha, beta=beta, state_in=state,
-                      state_out=state_out, o=o, workspace=workspace, stream=stream)
+                      state_out=state_out, o=o, workspace=workspace, stream=stream, precision=precision)
     call_prefill(args)
     return dict(o=o, state=state_out, conv_state=conv_out)
 
@@ -412,10 +421,11 @@ class DeltaCache:
     chunked form in a workspace allocated here, once (the reference prefills in windows of
     1024, cpp/src/session.hpp:136); max_prefill_tokens = 0 keeps every block on the
     recurrent kernel. As the C++ DeltaCache (include/gdn.hpp), step() then allocates no
-    workspace. The chunked form leaves the state about 2e-3 (relative, T = 4096) from the
-    fp32 recurrence, against about 1e-7 on the recurrent kernel."""
+    workspace. `prefill_precision` is PREFILL_ACCURATE (the default) or PREFILL_FAST (see
+    layer()); the recurrent kernel stays within about 1e-7 of the fp32 recurrence."""
 
-    def __init__(self, B: int, Hv: int = 48, Hk: int = 16, device="cuda", max_prefill_tokens: int = 0):
+    def __init__(self, B: int, Hv: int = 48, Hk: int = 16, device="cuda", max_prefill_tokens: int = 0,
+                 prefill_precision: int = PREFILL_ACCURATE):
         import torch
         C = 2 * Hk * HEAD_DIM + Hv * HEAD_DIM
         self.Hk, self.Hv, self.C = Hk, Hv, C
@@ -423,8 +433,10 @@ class DeltaCache:
         self.conv = torch.zeros((B, CONV_TAPS - 1, C), dtype=torch.bfloat16, device=device)
         self._conv_spare = torch.empty_like(self.conv)
         self.max_prefill_tokens = max_prefill_tokens if max_prefill_tokens >= chunked_min_t(B) else 0
-        self._ws = (torch.empty(prefill_workspace_size(B, self.max_prefill_tokens, Hk, Hv), dtype=torch.uint8,
-                                device=device) if self.max_prefill_tokens else None)
+        self.prefill_precision = prefill_precision
+        self._ws = (torch.empty(prefill_workspace_size(B, self.max_prefill_tokens, Hk, Hv,
+                                                       precision=prefill_precision),
+                                dtype=torch.uint8, device=device) if self.max_prefill_tokens else None)
         self.offset = 0
         self.record = False
         self.base_offset = 0
@@ -455,7 +467,7 @@ class DeltaCache:
                               conv_state_in=self.conv, conv_state_out=self._conv_spare, a=a,
                               b=b, A_log=A_log, dt_bias=dt_bias, state_in=self.state,
                               state_out=self.state, o=o, workspace=self._ws if chunked else None,
-                              stream=stream)
+                              stream=stream, precision=self.prefill_precision)
             (call_prefill if chunked else call_run)(args)
             self.conv, self._conv_spare = self._conv_spare, self.conv
             self.offset += T

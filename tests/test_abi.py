@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(gdn):
                          text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s+(gdn_\w+)", out))
     assert set(declared_functions()) <= exported
-    assert L.gdn_abi_version() == 4
+    assert L.gdn_abi_version() == 5
     assert set(gdn.EXPORTS) == set(declared_functions())
 
 
@@ -121,22 +121,30 @@ def test_run_rejects_bad_arguments(gdn, kw, msg):
 
 def test_prefill_workspace_size_and_checks(gdn):
     # per chunk: Q, K^T per k-head (bf16 64 x 128); W, M hi/lo, V in fragment order (bf16)
-    # and U (fp16) per v-head, with one scale per 16-position tile; two pairs of gate
-    # factors per position; with the conv front end also its bf16 q, k; 256-byte aligned
-    # pieces
+    # and U (fp32 in the default precision, fp16 in the fast one) per v-head, with one fp16
+    # scale per 16-position tile; two pairs of gate factors per position; with the conv
+    # front end also its bf16 q, k; 256-byte aligned pieces
     n_qkv = gdn.prefill_workspace_size(1, 4096, conv=False)
-    assert n_qkv == (2 * 16 * 64 * 8192 * 2 + 3 * 48 * 64 * 8192 * 2 + 48 * 64 * 8192 * 2
+    assert n_qkv == (2 * 16 * 64 * 8192 * 2 + 3 * 48 * 64 * 8192 * 2 + 48 * 64 * 8192 * 4
                      + 2 * 48 * 64 * 128 * 4 + 48 * 64 * 4 * 4)
     assert gdn.prefill_workspace_size(1, 4096) == n_qkv + 4096 * (16 + 16) * 128 * 2
     # a ragged T: whole chunks for the per-chunk pieces, T rows for the q, k staging
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     nc = (100 + 63) // 64
     assert gdn.prefill_workspace_size(2, 100) == (
-        2 * al(2 * 16 * nc * 8192 * 2) + 4 * al(2 * 48 * nc * 8192 * 2)
+        2 * al(2 * 16 * nc * 8192 * 2) + 3 * al(2 * 48 * nc * 8192 * 2) + al(2 * 48 * nc * 8192 * 4)
         + 2 * al(2 * 48 * nc * 128 * 4) + al(2 * 48 * nc * 4 * 4) + 2 * al(2 * 100 * 16 * 128 * 2))
+    # GDN_PREFILL_FAST keeps U in fp16: half its bytes, nothing else changes
+    assert gdn.PREFILL_ACCURATE == 0   # a zeroed gdn_layer_args gets the fp32-state form
+    assert gdn.prefill_workspace_size(1, 4096, precision=gdn.PREFILL_FAST) == (
+        gdn.prefill_workspace_size(1, 4096) - 48 * 64 * 8192 * 2)
+    with pytest.raises(gdn.GdnError, match="prefill_precision"):
+        gdn.prefill_workspace_size(1, 64, precision=2)
     L = gdn.lib()
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100)))
     assert rc == gdn.GDN_EINVAL and "workspace" in gdn.last_error()
+    rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, prefill_precision=7)))
+    assert rc == gdn.GDN_EINVAL and "prefill_precision" in gdn.last_error()
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, qkv_dtype=gdn.DTYPE_F32)))
     assert rc == gdn.GDN_EINVAL and "bf16" in gdn.last_error()
     rc = L.gdn_prefill_chunked(ctypes.byref(_args(gdn, seq_len=100, workspace=0x10000010,
