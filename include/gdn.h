@@ -77,19 +77,17 @@ typedef enum gdn_gate_mode {
 
 /* Arithmetic of gdn_prefill_chunked (gdn_run computes in fp32 either way). */
 typedef enum gdn_prefill_precision {
-  GDN_PREFILL_ACCURATE = 0, /* the default: U kept in fp32 and V'' split into bf16 hi + lo
-                               for the state update K^T V'' -- the chunked form's largest
-                               error term (the reference runs an fp32 kernel for every window,
-                               cpp/src/model.cpp:619-624). What remains are the bf16 roundings
-                               of S and W in V' = U - W S, which a chunk forgets as fast as
-                               its gates decay: with the benchmark's gates (alpha <= 0.8) the
-                               state ends within about 5e-6 (max|a-b|/max|b|, T = 1024..4096)
-                               of the fp32 recurrence, up to about 4e-4 when the last chunk
-                               holds a few tokens; with gates near 1 (alpha >= 0.99) about
-                               1.5e-3. Never further than GDN_PREFILL_FAST. */
-  GDN_PREFILL_FAST = 1      /* bf16 V'' in the state update and U kept as fp16: the state ends
-                               about 2e-3 from the fp32 recurrence; a smaller workspace and
-                               about 5 % less time at T = 4096 */
+  GDN_PREFILL_ACCURATE = 0, /* the default, as the reference runs an fp32 kernel for every
+                               window (cpp/src/model.cpp:619-624): the state products carry
+                               fp32 accuracy -- U kept in fp32, W stored with its bf16
+                               remainder and W S formed as W_hi S_hi + W_lo S_hi + W_hi S_lo,
+                               V'' split into bf16 hi + lo for K^T V'' -- so the state the next
+                               window or decode step starts from is within about 1e-5
+                               (max|a-b|/max|b|; measured 3e-6..8e-6) of the fp32 recurrence
+                               whatever the gates */
+  GDN_PREFILL_FAST = 1      /* bf16 operands in the state products and U kept as fp16: the
+                               state ends about 2e-3 from the fp32 recurrence; a smaller
+                               workspace and about two thirds of the time at T = 4096 */
 } gdn_prefill_precision;
 
 typedef enum gdn_states_layout {

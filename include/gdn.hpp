@@ -105,11 +105,10 @@ class DeltaCache {
   // next block is recorded into the other buffer, which no longer holds the live state.
   // Blocks of chunked_min_t(batch) .. max_prefill_tokens tokens (the reference prefills in windows of
   // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here, with
-  // `prefill_precision` (gdn_prefill_precision: GDN_PREFILL_ACCURATE, the default, keeps
-  // U in fp32 and splits the state update's V'' into bf16 hi + lo, which leaves the state the
-  // next decode step starts from within about 5e-6 of the fp32 recurrence for fast-decaying
-  // gates and 1.5e-3 for gates near 1; GDN_PREFILL_FAST about 2e-3 either way);
-  // max_prefill_tokens = 0 keeps every block on the exact recurrent kernel.
+  // `prefill_precision` (gdn_prefill_precision: GDN_PREFILL_ACCURATE, the default, leaves the
+  // state the next decode step starts from within about 1e-5 of the fp32 recurrence,
+  // GDN_PREFILL_FAST about 2e-3 in about two thirds of the time); max_prefill_tokens = 0
+  // keeps every block on the exact recurrent kernel.
   DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0,
              int prefill_precision = GDN_PREFILL_ACCURATE)
       : p_(p), B_(batch), max_T_(max_record_steps),

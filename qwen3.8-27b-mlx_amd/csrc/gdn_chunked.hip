@@ -33,9 +33,10 @@
 //                  registers two chunks ahead of their use, and the output waves touch the
 //                  lines of the chunk four ahead so that they are in L2 when first asked
 //                  for. W S, Q S and K^T V'' use bf16 operands; M V' splits both operands
-//                  into bf16 hi + lo (three MFMAs). With GDN_PREFILL_ACCURATE, U stays fp32
-//                  and V'' is split into bf16 hi + lo for K^T V'' (two MFMAs): the state
-//                  then follows the fp32 recurrence to about 1e-6 instead of 2e-3.
+//                  into bf16 hi + lo (three MFMAs). With GDN_PREFILL_ACCURATE, U stays fp32,
+//                  W is stored with its bf16 remainder and W S takes S split as well (three
+//                  MFMAs), and V'' is split into bf16 hi + lo for K^T V'' (two MFMAs): the
+//                  state then follows the fp32 recurrence to about 1e-6 instead of 2e-3.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
@@ -87,6 +88,12 @@ __device__ __forceinline__ bf8 frag(const __bf16 (*m)[LD], int row, int k) {
 __device__ __forceinline__ bf4 to_bf4(f4 v) { return __builtin_convertvector(v, bf4); }
 __device__ __forceinline__ f4 from_bf4(bf4 v) { return __builtin_convertvector(v, f4); }
 
+// Two accumulator tiles (k rows 0..15 and 16..31 of a block) as one B fragment in the
+// interleaved k order.
+__device__ __forceinline__ bf8 stack_bf8(f4 lo, f4 hi) {
+  return __builtin_shufflevector(to_bf4(lo), to_bf4(hi), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // e^x for x <= 0 from the hardware 2^x (the decay factors inside a chunk).
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
@@ -131,6 +138,7 @@ struct PrefillParams {
   __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128)
   __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64)
   __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
+  __bf16* ws_wl;  // (B, Hv, nC): W - bf16(W) in bf16, same layout (GDN_PREFILL_ACCURATE only)
   __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
                   // blocks above the diagonal are left unwritten)
   void* ws_u;     // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]:
@@ -636,7 +644,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       // U = T' V and W^T = K^T (T' e^G)^T: wave w takes position tile w (rows i = 16 w + fr
       // of T'), all eight dv tiles of U and all eight dk tiles of W; T' split into hi + lo for U
       {
-        bf8 ah[2], al[2], te[2];
+        bf8 ah[2], al[2], te[2], tel[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
           // (column blocks above row block `wave` still hold -A^T: T is zero there)
@@ -650,7 +658,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
             const __bf16 hi = (__bf16)tv;
             ah[kh][e] = hi;
             al[kh][e] = (__bf16)(tv - (float)hi);
-            te[kh][e] = (__bf16)(tv * ej[kh][e]);
+            const float t = tv * ej[kh][e];
+            const __bf16 th = (__bf16)t;
+            te[kh][e] = th;
+            if constexpr (PRECISE) tel[kh][e] = (__bf16)(t - (float)th);
           }
         }
         f4 ut[kD / 16];
@@ -687,16 +698,33 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                         reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
           if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
         }
-        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]
+        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]; with PRECISE from T' e^G split
+        // into bf16 hi + lo, and the remainder W - bf16(W) stored beside W. Tiles a and a + 1
+        // (a even) fill the two halves of the same 16-byte piece of the fragment order (the
+        // interleaved k order), so each pair is stored as one piece: every store writes 1 KB
+        // of whole lines (8-byte halves written apart were partial-line writes).
         __bf16* ww = p.ws_w + hc * kChunkElems;
 #pragma unroll
-        for (int a = 0; a < kD / 16; ++a) {
-          const bf8 k0 = frag(s.kt, 16 * a + fr, fk), k1 = frag(s.kt, 16 * a + fr, 32 + fk);
-          f4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mfma(k0, te[0], acc);
-          acc = mfma(k1, te[1], acc);
-          __builtin_nontemporal_store(to_bf4(acc),
-                                      reinterpret_cast<bf4*>(ww + ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32)));
+        for (int a = 0; a < kD / 16; a += 2) {
+          f4 acc[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const bf8 k0 = frag(s.kt, 16 * (a + h) + fr, fk), k1 = frag(s.kt, 16 * (a + h) + fr, 32 + fk);
+            acc[h] = f4{0.f, 0.f, 0.f, 0.f};
+            acc[h] = mfma(k0, te[0], acc[h]);
+            acc[h] = mfma(k1, te[1], acc[h]);
+            if constexpr (PRECISE) {
+              acc[h] = mfma(k0, tel[0], acc[h]);
+              acc[h] = mfma(k1, tel[1], acc[h]);
+            }
+          }
+          const bf4 w0 = to_bf4(acc[0]), w1 = to_bf4(acc[1]);
+          const int off = ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32);
+          __builtin_nontemporal_store(__builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7),
+                                      reinterpret_cast<bf8*>(ww + off));
+          if constexpr (PRECISE)
+            __builtin_nontemporal_store(stack_bf8(acc[0] - from_bf4(w0), acc[1] - from_bf4(w1)),
+                                        reinterpret_cast<bf8*>(p.ws_wl + hc * kChunkElems + off));
         }
       }
     }
@@ -763,9 +791,14 @@ struct ScanMail {
 // read them. The two state waves of a workgroup need all of W and K^T; each loads half
 // (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles 4i .. 4i + 3) and passes it
 // to the other through LDS (ScanShared).
+struct NoOps {};
+struct WLoOps {
+  bf8 w[2][4];  // W - bf16(W) [own pos tile][dk block]
+};
 template <bool PRECISE>
 struct StateOps {
   bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
+  typename std::conditional<PRECISE, WLoOps, NoOps>::type wl;  // its remainder (PRECISE)
   bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
   typename std::conditional<PRECISE, f4, h4>::type u[4];  // U [pos tile]: positions 16 pt + 4 lg + e,
                  // column fr of the wave's tile (fp32, or fp16 scaled by 1 / us[pt])
@@ -830,6 +863,14 @@ __device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int j
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
   if constexpr (PRECISE) {
+    const __bf16* wl = p.ws_wl + hc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        op.wl.w[r][ks] = *reinterpret_cast<const bf8*>(wl + ((2 * i + r) * 4 + ks) * kFrag);
+  }
+  if constexpr (PRECISE) {
     const float* u = static_cast<const float*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const f4*>(u + pt * 256);
@@ -865,11 +906,6 @@ __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_
   op.eg = p.ws_g[hc * kGStride + 2 * lane];
 }
 
-// Two accumulator tiles (k rows 0..15 and 16..31 of a block) as one B fragment in the
-// interleaved k order.
-__device__ __forceinline__ bf8 stack_bf8(f4 lo, f4 hi) {
-  return __builtin_shufflevector(to_bf4(lo), to_bf4(hi), 0, 1, 2, 3, 4, 5, 6, 7);
-}
 
 // The per-position value v (lane t holds position t) at positions 16 pt + 4 (lane / 16) + e,
 // e < 4: the accumulator-row order.
@@ -882,9 +918,14 @@ __device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
 
 // The W and K^T halves the two state waves exchange, per lane, in two slots: slot c % 2
 // holds chunk c's, written during chunk c - 1.
+struct WLoShared {
+  bf8 w[2][2][2][4][64];   // W - bf16(W), as w below
+};
+template <bool PRECISE>
 struct ScanShared {
   bf8 w[2][2][2][4][64];   // [slot][wave][own pos tile][dk block][lane]
   bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
+  typename std::conditional<PRECISE, WLoShared, NoOps>::type wl;
 };
 
 // State wave i of (batch b, v-head h, Dv tile jt): S[a] holds the state's rows dk = 16 a +
@@ -894,7 +935,8 @@ struct ScanShared {
 // chunk cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk
 // ago) is written to the exchange slot of chunk c + 1.
 template <int NT, int i, bool PRECISE>
-__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared& sh, f4 (&S)[kD / 16],
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared<PRECISE>& sh,
+                                            f4 (&S)[kD / 16],
                                             StateOps<PRECISE>& op, const StateOps<PRECISE>& nx, size_t gcn, size_t hcn,
                                             int jt, int slot, int lane) {
   constexpr int o = i ^ 1;
@@ -908,29 +950,60 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
-  bf8 sb[kD / 32];
+  WLoOps wlo;  // (PRECISE) the other wave's half of W's remainder
+  if constexpr (PRECISE) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) wlo.w[r][ks] = sh.wl.w[slot][o][r][ks][lane];
+  }
+  bf8 sb[kD / 32], sbl[kD / 32];  // S as bf16 and (PRECISE) its remainder
 #pragma unroll
   for (int ks = 0; ks < kD / 32; ++ks) {
     sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
     mb.sb[i][ks][lane] = sb[ks];
+    if constexpr (PRECISE) {
+      const f4 h0 = from_bf4(to_bf4(S[2 * ks])), h1 = from_bf4(to_bf4(S[2 * ks + 1]));
+      sbl[ks] = stack_bf8(S[2 * ks] - h0, S[2 * ks + 1] - h1);
+    }
   }
   f4 egr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) egr[pt] = rows_of(op.g.y, pt, lane);
   const float gam = __shfl(op.g.x, 63, 64);
+  // P = W S for the four position tiles (2i, 2i + 1 this wave's, from registers; the others
+  // came through LDS), the four accumulators interleaved so that no MFMA waits for the one
+  // before it; with PRECISE to fp32 accuracy: W_hi S_hi + W_lo S_hi + W_hi S_lo
+  f4 P[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) P[pt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < kD / 32; ++ks) {
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      const bool own = (pt >> 1) == i;  // (compile-time after unrolling)
+      P[pt] = mfma(own ? op.w[pt & 1][ks] : wo[pt & 1][ks], sb[ks], P[pt]);
+    }
+    if constexpr (PRECISE) {
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const bool own = (pt >> 1) == i;
+        P[pt] = mfma(own ? op.wl.w[pt & 1][ks] : wlo.w[pt & 1][ks], sb[ks], P[pt]);
+      }
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const bool own = (pt >> 1) == i;
+        P[pt] = mfma(own ? op.w[pt & 1][ks] : wo[pt & 1][ks], sbl[ks], P[pt]);
+      }
+    }
+  }
   f4 vpr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) {
-    // position tiles 2i, 2i + 1 are this wave's (registers), the others came through LDS
-    const int r = pt & 1;
-    const bool own = (pt >> 1) == i;  // (compile-time after unrolling)
-    f4 P = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) P = mfma(own ? op.w[r][ks] : wo[r][ks], sb[ks], P);
     if constexpr (PRECISE) {
-      vpr[pt] = op.u[pt] - P;
+      vpr[pt] = op.u[pt] - P[pt];
     } else {
-      vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P;
+      vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P[pt];
     }
     mb.vpr[i][pt][lane] = vpr[pt];
   }
@@ -953,21 +1026,26 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   __builtin_amdgcn_sched_barrier(0);
   load_wu<PRECISE>(p, hcn, jt, i, lane, op);
 #pragma unroll
-  for (int a = 0; a < kD / 16; ++a) {
-    const int r = a & 3;
-    const bool own = (a >> 2) == i;
-    f4 acc = S[a] * gam;
+  for (int a = 0; a < kD / 16; ++a) S[a] = S[a] * gam;
+  // (the eight dk tiles' accumulators interleaved: consecutive MFMAs are independent)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf8 kt = own ? op.kt[r][ks] : kto[r][ks];
-      acc = mfma(kt, vb[ks], acc);
-      if constexpr (PRECISE) acc = mfma(kt, vbl[ks], acc);
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int a = 0; a < kD / 16; ++a) {
+      const bool own = (a >> 2) == i;
+      S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vb[ks], S[a]);
     }
-    S[a] = acc;
+    if constexpr (PRECISE) {
+#pragma unroll
+      for (int a = 0; a < kD / 16; ++a) {
+        const bool own = (a >> 2) == i;
+        S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vbl[ks], S[a]);
+      }
+    }
   }
   load_kt<PRECISE>(p, gcn, i, lane, op);
-  // 16 (32) MFMAs and 21 (22 with the fp16 U scales) loads
-  constexpr int kMfma = PRECISE ? 32 : 16, kLoads = PRECISE ? 21 : 22;
+  // 16 (32) MFMAs and 22 (with the fp16 U scales) or 29 (with W's remainder) loads
+  constexpr int kMfma = PRECISE ? 32 : 16, kLoads = PRECISE ? 29 : 22;
   constexpr int kPairs = kMfma < kLoads ? kMfma : kLoads;
 #pragma unroll
   for (int k = 0; k < kPairs; ++k) {
@@ -986,6 +1064,12 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) sh.kt[slot ^ 1][i][r][ks][lane] = nx.kt[r][ks];
+  if constexpr (PRECISE) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sh.wl.w[slot ^ 1][i][r][ks][lane] = nx.wl.w[r][ks];
+  }
   __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
                     // have read mail[(c + 1) % 2]
 }
@@ -996,7 +1080,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
 // flight as at its back edge. Barriers: one after chunk 0's shares are exchanged, one per
 // chunk, one at the end, as the output waves.
 template <int NT, int i, bool PRECISE>
-__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared& sh,
+__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared<PRECISE>& sh,
                                                 int b, int h, int g, int jt, int lane) {
   const int fr = lane & 15, lg = lane >> 4;
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
@@ -1032,6 +1116,12 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) sh.kt[0][i][r][ks][lane] = A.kt[r][ks];
+  if constexpr (PRECISE) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sh.wl.w[0][i][r][ks][lane] = A.wl.w[r][ks];
+  }
   __syncthreads();
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
@@ -1176,7 +1266,7 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
   static_assert(NT == 2, "two state waves exchange halves of W and K^T");
   __shared__ __attribute__((aligned(16))) ScanMail<NT> mail[2];
   __shared__ __attribute__((aligned(16))) OutTile<NT, OT> tiles[2];
-  __shared__ __attribute__((aligned(16))) ScanShared shared_ops;
+  __shared__ __attribute__((aligned(16))) ScanShared<PRECISE> shared_ops;
   // Workgroups are dispatched to the 8 XCDs round robin (bid % 8); renumber them so that
   // each XCD gets a contiguous range of (batch, v-head, tiles) -- whole v-heads, and whole
   // k-head groups when the count divides -- and the chunk operands those waves share are
@@ -1201,7 +1291,7 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, w, m, u, g, vf, fq, fk, us, gb, total;
+  size_t q, kt, w, m, u, g, vf, fq, fk, us, gb, wl, total;
 };
 
 // conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
@@ -1227,7 +1317,8 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
   L.fk = L.fq + fqk;
   L.us = L.fk + fqk;
   L.gb = L.us + al((size_t)B * Hv * nC * 4 * 4);
-  L.total = L.gb + gg;
+  L.wl = L.gb + gg;
+  L.total = L.wl + (precise ? wm : 0);
   return L;
 }
 
@@ -1276,6 +1367,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_u = w + L.u;
   p.ws_us = reinterpret_cast<float*>(w + L.us);
   p.ws_gb = reinterpret_cast<float*>(w + L.gb);
+  p.ws_wl = reinterpret_cast<__bf16*>(w + L.wl);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {

@@ -327,13 +327,13 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     in `workspace` (uint8, at least prefill_workspace_size(B, T, ...) bytes), which is
     allocated here only when the caller gives none.
 
-    Precision (`precision`, PREFILL_*): PREFILL_ACCURATE, the default, keeps U in fp32 and
-    splits the state update's V'' into bf16 hi + lo, the chunked form's largest error term
-    against the reference's fp32 Metal kernel (cpp/src/model.cpp:619-624): the state then
-    ends within about 5e-6 (relative, T = 1024..4096) of the fp32 recurrence when the gates
-    decay fast (the benchmark's, alpha <= 0.8), about 1.5e-3 when they are near 1.
-    PREFILL_FAST (bf16 V'', U as fp16) leaves it about 2e-3 off for about 5 % less time. The
-    recurrent kernel is within about 1e-7. Later decode steps continue from that state."""
+    Precision (`precision`, PREFILL_*): PREFILL_ACCURATE, the default, carries the state
+    products at fp32 accuracy (U in fp32, W and S split into bf16 hi + lo in W S, V'' split
+    in K^T V''), as the reference's fp32 Metal kernel for every window
+    (cpp/src/model.cpp:619-624): the state ends within about 1e-5 (relative) of the fp32
+    recurrence whatever the gates. PREFILL_FAST (bf16 operands, U as fp16) leaves it about
+    2e-3 off in about two thirds of the time. The recurrent kernel is within about 1e-7.
+    Later decode steps continue from that state."""
     import torch
     src = x if x is not None else q
     B, T = src.shape[0], src.shape[1]
