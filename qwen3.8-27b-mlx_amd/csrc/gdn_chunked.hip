@@ -137,19 +137,24 @@ struct PrefillParams {
   // (Q, K^T, W and M in fragment order with the interleaved k order)
   __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128)
   __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64)
-  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
-  __bf16* ws_wl;  // (B, Hv, nC): W - bf16(W) in bf16, same layout (GDN_PREFILL_ACCURATE only)
   __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
                   // blocks above the diagonal are left unwritten)
-  void* ws_u;     // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4]:
-                  // fp32 (GDN_PREFILL_ACCURATE), or fp16 with each position tile multiplied
-                  // by a power of two (below)
-  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile (fp16 U)
+  // GDN_PREFILL_FAST: the chunk's U and W
+  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
+  _Float16* ws_u; // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4],
+                  // fp16 with each position tile multiplied by a power of two (below)
+  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile
+  // GDN_PREFILL_ACCURATE: K and T' instead, so that the scan forms V' = T' (V - e^G K S)
+  __bf16* ws_kk;  // (B, Hk, nC): K   (64 x 128), as Q
+  __bf16* ws_tp;  // (B, Hv, nC): T' = (I + A)^-1 diag(beta) (64 x 64) split into bf16 hi + lo,
+                  // laid out as M
   float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
   float* ws_gb;   // (B, Hv, nC, kGStride): (G, beta) per position
-  __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as the B operand of U = T' V, in fragment order:
-                  // block 2 (dv / 16) + pos / 32, lane 16 ((pos % 32) / 8) + dv % 16, element
-                  // pos % 8; positions past T are zeros
+  __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as B operand fragments in the interleaved k order
+                  // (the B operand of U = T' V, and two accumulator tiles of the scan's
+                  // V - e^G K S): block 2 (dv / 16) + pos / 32, lane 16 g + dv % 16 with
+                  // g = (pos % 16) / 4, element (pos % 4) + 4 ((pos % 32) / 16); positions
+                  // past T are zeros
 };
 
 // Causal depthwise conv from 4 rows (model.cpp:385-395), bf16 after every op.
@@ -361,8 +366,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
   }
   if (!norm) {
-    // v: the B operand of U = T' V in fragment order (block 2 (dv / 16) + half chunk, lane
-    // 16 (position / 8) + dv % 16); this wave's LDS tile, written above by this wave only
+    // v into ws_vf (block 2 (dv / 16) + half chunk, lane 16 g + dv % 16: positions 4 g .. +3
+    // and 16 + 4 g .. +3 of the half chunk); this wave's LDS tile, written above by this wave
+    // only
     const int hv = hh - 2 * p.Hk;
     const int kh = pb & 1;  // which half of the 64-position chunk (kFePos = kC / 2)
     __bf16* vf = p.ws_vf + (((size_t)b * p.Hv + hv) * p.nC + pb / 2) * kChunkElems;
@@ -370,8 +376,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int i = 0; i < 8; ++i) {
       const int piece = 64 * i + lane;          // (dv tile, lane of the fragment)
       const int dv = 16 * (piece >> 6) + (lane & 15), pg = lane >> 4;
+      const bf4 lo = *reinterpret_cast<const bf4*>(&vt[dv][4 * pg]);
+      const bf4 hi = *reinterpret_cast<const bf4*>(&vt[dv][16 + 4 * pg]);
       *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + kh) * kFrag + lane * 8) =
-          *reinterpret_cast<const bf8*>(&vt[dv][8 * pg]);
+          __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      // the last chunk's second half when it lies wholly past T: zeros (no workgroup has
+      // positions there, and the scan reads V for every position of a chunk)
+      if (kh == 0 && pb == pblocks - 1)
+        *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + 1) * kFrag + lane * 8) = bf8{};
     }
   }
   if (p.conv_out && pb == pblocks - 1) {
@@ -543,6 +555,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       __builtin_nontemporal_store(frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg),
                                   reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
     }
+    if constexpr (PRECISE) {  // K, in the layout of Q, for the scan's K S
+      __bf16* wk = p.ws_kk + gc * kChunkElems + lane * 8;
+#pragma unroll
+      for (int ks = 0; ks < kD / 32; ++ks) {
+        __builtin_nontemporal_store(frag_ilv(s.u.fe.k, 16 * wave + fr, 32 * ks, lg),
+                                    reinterpret_cast<bf8*>(wk + (wave * 4 + ks) * kFrag));
+      }
+    }
     const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
     for (int q8 = 0; q8 < 4; ++q8) {
@@ -620,6 +640,43 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     for (int r = 0; r < gs; ++r) {
       const int h = g * p.rep + r0 + r;
       const size_t hc = ((size_t)b * p.Hv + h) * p.nC + c;
+      // T' = T diag(beta), rows i = 16 wave + fr, as A fragments of the two 32-column
+      // blocks kh in the interleaved k order: lane group lg holds the columns
+      // j = 32 kh + 4 lg + e and 32 kh + 16 + 4 lg + e (e < 4), the first four in x0, the
+      // second in x1. 16-column blocks above row block `wave` still hold -A^T (T is zero
+      // there) and are masked; the diagonal blocks were written with zeros above the
+      // diagonal.
+      auto tprime = [&](int kh, float (&tv)[8]) {
+        const float* xr = &s.u.nat[r][16 * wave + fr][32 * kh + 4 * lg];
+        const f4 x0 = 2 * kh > wave ? f4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const f4*>(xr);
+        const f4 x1 = 2 * kh + 1 > wave ? f4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const f4*>(xr + 16);
+        const f4 b0 = *reinterpret_cast<const f4*>(&s.beta[r][32 * kh + 4 * lg]);
+        const f4 b1 = *reinterpret_cast<const f4*>(&s.beta[r][32 * kh + 16 + 4 * lg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          tv[e] = x0[e] * b0[e];
+          tv[4 + e] = x1[e] * b1[e];
+        }
+      };
+      if constexpr (PRECISE) {
+        // T' split into bf16 hi + lo, blocks (wave, kh) with kh <= wave / 2 (the others are
+        // zero), in the layout of M
+        __bf16* wt = p.ws_tp + hc * kChunkElems + lane * 8;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          if (2 * kh > wave) continue;
+          float tv[8];
+          tprime(kh, tv);
+          bf8 th, tl;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            th[e] = (__bf16)tv[e];
+            tl[e] = (__bf16)(tv[e] - (float)th[e]);
+          }
+          __builtin_nontemporal_store(th, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2) * kFrag));
+          __builtin_nontemporal_store(tl, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2 + 1) * kFrag));
+        }
+      } else {
       // V: the B operand of U, straight from the workspace (a half chunk wholly past T was
       // never written: zeros)
       bf8 vb[kD / 16][2];
@@ -631,37 +688,22 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           for (int kh = 0; kh < 2; ++kh)
             vb[d][kh] = 32 * kh < n ? *reinterpret_cast<const bf8*>(vf + (2 * d + kh) * kFrag) : bf8{};
       }
-      // column factors of T' = T diag(beta) and T' diag(e^G) for this lane's columns
-      // j = 32 kh + fk + e
-      float bj[2][8], ej[2][8];
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bj[kh][e] = s.beta[r][32 * kh + fk + e];
-          ej[kh][e] = s.eG[r][32 * kh + fk + e];
-        }
       // U = T' V and W^T = K^T (T' e^G)^T: wave w takes position tile w (rows i = 16 w + fr
       // of T'), all eight dv tiles of U and all eight dk tiles of W; T' split into hi + lo for U
       {
-        bf8 ah[2], al[2], te[2], tel[2];
+        bf8 ah[2], al[2], te[2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          // (column blocks above row block `wave` still hold -A^T: T is zero there)
-          const bool above = 2 * kh + (lane >> 5) > wave;
-          const float* xr = &s.u.nat[r][16 * wave + fr][32 * kh + fk];
-          f4 x0 = *reinterpret_cast<const f4*>(xr), x1 = *reinterpret_cast<const f4*>(xr + 4);
-          if (above) x0 = x1 = f4{0.f, 0.f, 0.f, 0.f};
+          float tv[8];
+          tprime(kh, tv);
+          const f4 e0 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 4 * lg]);
+          const f4 e1 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 16 + 4 * lg]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float tv = (e < 4 ? x0[e] : x1[e - 4]) * bj[kh][e];
-            const __bf16 hi = (__bf16)tv;
+            const __bf16 hi = (__bf16)tv[e];
             ah[kh][e] = hi;
-            al[kh][e] = (__bf16)(tv - (float)hi);
-            const float t = tv * ej[kh][e];
-            const __bf16 th = (__bf16)t;
-            te[kh][e] = th;
-            if constexpr (PRECISE) tel[kh][e] = (__bf16)(t - (float)th);
+            al[kh][e] = (__bf16)(tv[e] - (float)hi);
+            te[kh][e] = (__bf16)(tv[e] * (e < 4 ? e0[e] : e1[e - 4]));
           }
         }
         f4 ut[kD / 16];
@@ -674,33 +716,25 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           acc = mfma(al[1], vb[d][1], acc);
           ut[d] = acc;
         }
-        if constexpr (PRECISE) {
-          float* wu = static_cast<float*>(p.ws_u) + hc * kChunkElems + lane * 4;
+        // U stored as fp16 times 2^e, e from the position tile's largest magnitude (so
+        // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
+        uint32_t mx = 0;
 #pragma unroll
-          for (int d = 0; d < kD / 16; ++d)
-            __builtin_nontemporal_store(ut[d], reinterpret_cast<f4*>(wu + (d * 4 + wave) * 256));
-        } else {
-          // U stored as fp16 times 2^e, e from the position tile's largest magnitude (so
-          // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
-          uint32_t mx = 0;
+        for (int d = 0; d < kD / 16; ++d)
 #pragma unroll
-          for (int d = 0; d < kD / 16; ++d)
+          for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(ut[d][e]) & 0x7fffffffu);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(ut[d][e]) & 0x7fffffffu);
+        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+        const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
+        const float sc = bits_f((uint32_t)(127 + ex) << 23);
+        _Float16* wu = p.ws_u + hc * kChunkElems + lane * 4;
 #pragma unroll
-          for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
-          const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
-          const float sc = bits_f((uint32_t)(127 + ex) << 23);
-          _Float16* wu = static_cast<_Float16*>(p.ws_u) + hc * kChunkElems + lane * 4;
-#pragma unroll
-          for (int d = 0; d < kD / 16; ++d)
-            __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
-                                        reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
-          if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
-        }
-        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]; with PRECISE from T' e^G split
-        // into bf16 hi + lo, and the remainder W - bf16(W) stored beside W. Tiles a and a + 1
-        // (a even) fill the two halves of the same 16-byte piece of the fragment order (the
+        for (int d = 0; d < kD / 16; ++d)
+          __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
+                                      reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
+        if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
+        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]. Tiles a and a + 1 (a even)
+        // fill the two halves of the same 16-byte piece of the fragment order (the
         // interleaved k order), so each pair is stored as one piece: every store writes 1 KB
         // of whole lines (8-byte halves written apart were partial-line writes).
         __bf16* ww = p.ws_w + hc * kChunkElems;
@@ -709,23 +743,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           f4 acc[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const bf8 k0 = frag(s.kt, 16 * (a + h) + fr, fk), k1 = frag(s.kt, 16 * (a + h) + fr, 32 + fk);
             acc[h] = f4{0.f, 0.f, 0.f, 0.f};
-            acc[h] = mfma(k0, te[0], acc[h]);
-            acc[h] = mfma(k1, te[1], acc[h]);
-            if constexpr (PRECISE) {
-              acc[h] = mfma(k0, tel[0], acc[h]);
-              acc[h] = mfma(k1, tel[1], acc[h]);
-            }
+            acc[h] = mfma(frag_ilv(s.kt, 16 * (a + h) + fr, 0, lg), te[0], acc[h]);
+            acc[h] = mfma(frag_ilv(s.kt, 16 * (a + h) + fr, 32, lg), te[1], acc[h]);
           }
           const bf4 w0 = to_bf4(acc[0]), w1 = to_bf4(acc[1]);
           const int off = ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32);
           __builtin_nontemporal_store(__builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7),
                                       reinterpret_cast<bf8*>(ww + off));
-          if constexpr (PRECISE)
-            __builtin_nontemporal_store(stack_bf8(acc[0] - from_bf4(w0), acc[1] - from_bf4(w1)),
-                                        reinterpret_cast<bf8*>(p.ws_wl + hc * kChunkElems + off));
         }
+      }
       }
     }
     __syncthreads();  // the next group rewrites G, beta and the LDS union
@@ -768,8 +795,10 @@ __global__ __launch_bounds__(kThreads) void prefill_vfrag_kernel(PrefillParams p
   for (int it = 0; it < kIt; ++it) {
     const int e = tid + it * kThreads;        // (block f, lane l) piece
     const int f = e / 64, l = e % 64;
-    const int dv = 16 * (f / 2) + (l & 15), pos = 32 * (f & 1) + 8 * (l >> 4);
-    *reinterpret_cast<bf8*>(vf + e * 8) = *reinterpret_cast<const bf8*>(&vt[dv][pos]);
+    const int dv = 16 * (f / 2) + (l & 15), pos = 32 * (f & 1) + 4 * (l >> 4);
+    const bf4 lo = *reinterpret_cast<const bf4*>(&vt[dv][pos]);
+    const bf4 hi = *reinterpret_cast<const bf4*>(&vt[dv][pos + 16]);
+    *reinterpret_cast<bf8*>(vf + e * 8) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 }
 
@@ -788,23 +817,33 @@ struct ScanMail {
 };
 
 // A state wave's share of one chunk's operands, in the register order of the MFMAs that
-// read them. The two state waves of a workgroup need all of W and K^T; each loads half
-// (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles 4i .. 4i + 3) and passes it
-// to the other through LDS (ScanShared).
-struct NoOps {};
-struct WLoOps {
-  bf8 w[2][4];  // W - bf16(W) [own pos tile][dk block]
-};
-template <bool PRECISE>
-struct StateOps {
+// read them. The two state waves of a workgroup need all of the chunk's shared operands;
+// each loads half and passes it to the other through LDS (ScanShared).
+// GDN_PREFILL_FAST: W and K^T (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles
+// 4i .. 4i + 3), with the wave's own U columns and the gates.
+struct StateOpsFast {
   bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
-  typename std::conditional<PRECISE, WLoOps, NoOps>::type wl;  // its remainder (PRECISE)
   bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
-  typename std::conditional<PRECISE, f4, h4>::type u[4];  // U [pos tile]: positions 16 pt + 4 lg + e,
-                 // column fr of the wave's tile (fp32, or fp16 scaled by 1 / us[pt])
+  h4 u[4];       // U [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile,
+                 // fp16 scaled by 1 / us[pt]
   f4 us;         // the chunk's fp16 U scale factors, one per position tile
   float2 g;      // (e^G, e^(G63-G)) at position `lane`
 };
+// GDN_PREFILL_ACCURATE: K (position tiles 2i, 2i + 1), T' (state wave 0 the hi parts of its
+// six nonzero blocks, wave 1 the lo parts) and K^T (dk tiles 4i .. 4i + 3), with the wave's
+// own V columns and the gates.
+constexpr int kTpBlocks = 6;  // T' blocks (pos tile, pos block): (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+__device__ __forceinline__ constexpr int tp_tile(int bi) { return bi < 2 ? bi : 2 + (bi - 2) / 2; }
+__device__ __forceinline__ constexpr int tp_kb(int bi) { return bi < 2 ? 0 : (bi - 2) % 2; }
+struct StateOpsKtv {
+  bf8 kk[2][4];          // K   [own pos tile][dk block]  (A of K S)
+  bf8 tp[kTpBlocks];     // T'  [block], hi (wave 0) or lo (wave 1)  (A of T' X)
+  bf8 kt[4][2];          // K^T [own dk tile][pos block]  (A of K^T V'')
+  bf8 v[2];              // V   [pos block] of the wave's tile (B order: two accumulator tiles)
+  float2 g;              // (e^G, e^(G63-G)) at position `lane`
+};
+template <bool PRECISE>
+using StateOps = typename std::conditional<PRECISE, StateOpsKtv, StateOpsFast>::type;
 
 // Output wave `half` makes position tiles half and 3 - half of each chunk: M is lower
 // triangular, so the first tile (rows < 32) has one nonzero 32-column block and the second
@@ -832,7 +871,7 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
   const unsigned* base;
   if (half == 0) {
     const int r = grp & 3;
-    const __bf16* m = r == 0 ? p.ws_w + hc * kChunkElems
+    const __bf16* m = r == 0 ? (PRECISE ? p.ws_kk + gc * kChunkElems : p.ws_w + hc * kChunkElems)
                     : r == 1 ? p.ws_m + hc * kChunkElems
                     : r == 2 ? p.ws_q + gc * kChunkElems
                              : p.ws_kt + gc * kChunkElems;
@@ -840,12 +879,15 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
     t[0] = base[lane * 32];
     t[1] = base[(64 + lane) * 32];
   } else {
-    // this workgroup's two dv tiles of U: 8 KB (fp32), 64 lines, or 4 KB (fp16), 32 lines
     if constexpr (PRECISE) {
-      base = reinterpret_cast<const unsigned*>(static_cast<const float*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256);
-      t[0] = base[lane * 32];
+      // a quarter of T' (each of the v-head's four workgroups one) and this workgroup's two
+      // dv tiles of V (4 KB, 32 lines)
+      const unsigned* tb = reinterpret_cast<const unsigned*>(p.ws_tp + hc * kChunkElems);
+      const unsigned* vb = reinterpret_cast<const unsigned*>(p.ws_vf + hc * kChunkElems + jt * 2 * kFrag);
+      t[0] = lane < 32 ? tb[((grp & 3) * 32 + lane) * 32] : vb[(lane - 32) * 32];
     } else {
-      base = reinterpret_cast<const unsigned*>(static_cast<const _Float16*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256);
+      // this workgroup's two dv tiles of U: 4 KB, 32 lines
+      base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
       t[0] = base[(lane & 31) * 32];
     }
     t[1] = reinterpret_cast<const unsigned*>(p.ws_g + hc * kGStride)[(lane & 3) * 32];
@@ -853,42 +895,36 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
 }
 
 // Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc: state wave
-// i's halves of W (with its tile jt's U and the gates) and of K^T.
-template <bool PRECISE>
-__device__ __forceinline__ void load_wu(const PrefillParams& p, size_t hc, int jt, int i, int lane,
-                                        StateOps<PRECISE>& op) {
+// i's half of W with its tile jt's U and the gates (GDN_PREFILL_FAST), or its halves of K
+// and T' with its tile's V and the gates (GDN_PREFILL_ACCURATE); then its half of K^T.
+__device__ __forceinline__ void load_front(const PrefillParams& p, size_t, size_t hc, int jt, int i, int lane,
+                                           StateOpsFast& op) {
   const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
-  if constexpr (PRECISE) {
-    const __bf16* wl = p.ws_wl + hc * kChunkElems + lane * 8;
+  const _Float16* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        op.wl.w[r][ks] = *reinterpret_cast<const bf8*>(wl + ((2 * i + r) * 4 + ks) * kFrag);
-  }
-  if constexpr (PRECISE) {
-    const float* u = static_cast<const float*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256 + lane * 4;
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const f4*>(u + pt * 256);
-  } else {
-    const _Float16* u = static_cast<const _Float16*>(p.ws_u) + hc * kChunkElems + jt * 4 * 256 + lane * 4;
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
-    op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
-  }
+  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
+  op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
-template <bool PRECISE>
-__device__ __forceinline__ void load_kt(const PrefillParams& p, size_t gc, int i, int lane, StateOps<PRECISE>& op) {
-  const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
+__device__ __forceinline__ void load_front(const PrefillParams& p, size_t gc, size_t hc, int jt, int i, int lane,
+                                           StateOpsKtv& op) {
+  const __bf16* kk = p.ws_kk + gc * kChunkElems + lane * 8;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) op.kt[r][ks] = *reinterpret_cast<const bf8*>(kt + ((4 * i + r) * 2 + ks) * kFrag);
+    for (int ks = 0; ks < 4; ++ks) op.kk[r][ks] = *reinterpret_cast<const bf8*>(kk + ((2 * i + r) * 4 + ks) * kFrag);
+  const __bf16* tp = p.ws_tp + hc * kChunkElems + lane * 8;
+#pragma unroll
+  for (int bi = 0; bi < kTpBlocks; ++bi)
+    op.tp[bi] = *reinterpret_cast<const bf8*>(tp + ((tp_tile(bi) * 2 + tp_kb(bi)) * 2 + i) * kFrag);
+  const __bf16* v = p.ws_vf + hc * kChunkElems + lane * 8;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) op.v[kb] = *reinterpret_cast<const bf8*>(v + (2 * jt + kb) * kFrag);
+  op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
 __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_t hc, int half, int lane, OutOps& op) {
   const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
@@ -916,29 +952,127 @@ __device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
   return r;
 }
 
-// The W and K^T halves the two state waves exchange, per lane, in two slots: slot c % 2
+// The operand halves the two state waves exchange, per lane, in two slots: slot c % 2
 // holds chunk c's, written during chunk c - 1.
-struct WLoShared {
-  bf8 w[2][2][2][4][64];   // W - bf16(W), as w below
-};
-template <bool PRECISE>
-struct ScanShared {
+struct ScanSharedFast {
   bf8 w[2][2][2][4][64];   // [slot][wave][own pos tile][dk block][lane]
   bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
-  typename std::conditional<PRECISE, WLoShared, NoOps>::type wl;
 };
+struct ScanSharedKtv {
+  bf8 kk[2][2][2][4][64];          // [slot][wave][own pos tile][dk block][lane]
+  bf8 kt[2][2][4][2][64];          // [slot][wave][own dk tile][pos block][lane]
+  bf8 tp[2][2][kTpBlocks][64];     // [slot][wave (0: hi, 1: lo)][block][lane]
+};
+template <bool PRECISE>
+using ScanShared = typename std::conditional<PRECISE, ScanSharedKtv, ScanSharedFast>::type;
+
+__device__ __forceinline__ void share_out(ScanSharedFast& sh, int slot, int i, int lane, const StateOpsFast& nx) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sh.w[slot][i][r][ks][lane] = nx.w[r][ks];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sh.kt[slot][i][r][ks][lane] = nx.kt[r][ks];
+}
+__device__ __forceinline__ void share_out(ScanSharedKtv& sh, int slot, int i, int lane, const StateOpsKtv& nx) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sh.kk[slot][i][r][ks][lane] = nx.kk[r][ks];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sh.kt[slot][i][r][ks][lane] = nx.kt[r][ks];
+#pragma unroll
+  for (int bi = 0; bi < kTpBlocks; ++bi) sh.tp[slot][i][bi][lane] = nx.tp[bi];
+}
+
+// S as the bf16 B fragments of the four dk blocks (and, with `split`, their remainders);
+// the bf16 parts also go to the output waves' mail.
+template <int NT, bool split>
+__device__ __forceinline__ void pack_state(ScanMail<NT>& mb, int i, int lane, const f4 (&S)[kD / 16],
+                                           bf8 (&sb)[kD / 32], bf8 (&sbl)[kD / 32]) {
+#pragma unroll
+  for (int ks = 0; ks < kD / 32; ++ks) {
+    sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
+    mb.sb[i][ks][lane] = sb[ks];
+    if constexpr (split) {
+      const f4 h0 = from_bf4(to_bf4(S[2 * ks])), h1 = from_bf4(to_bf4(S[2 * ks + 1]));
+      sbl[ks] = stack_bf8(S[2 * ks] - h0, S[2 * ks + 1] - h1);
+    }
+  }
+}
+
+// The chunk's state update S = e^G63 S + K^T V'' of the wave's tile, V'' = e^(G63 - G) V'
+// in bf16 (and, with `split`, its remainder, so that K^T V''_hi + K^T V''_lo carries V''
+// at fp32 accuracy: K^T is exact in bf16), with the reloads of the next chunk's operands
+// spread between the MFMAs (one load after each: loads issued in a burst queue up in the
+// CU's address unit behind the other waves' and hold this wave at the issue). `reload`
+// issues the loads of everything but K^T, which follows the last product.
+template <int i, bool split, int kLoads, typename Ops, typename Reload>
+__device__ __forceinline__ void state_update(const PrefillParams& p, f4 (&S)[kD / 16], const f4 (&vpr)[4],
+                                             const f4 (&egr)[4], float gam, const bf8 (&kto)[4][2], Ops& op,
+                                             size_t gcn, int lane, Reload reload) {
+  bf8 vb[2], vbl[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const f4 v0 = egr[2 * ks] * vpr[2 * ks], v1 = egr[2 * ks + 1] * vpr[2 * ks + 1];
+    const bf4 h0 = to_bf4(v0), h1 = to_bf4(v1);
+    vb[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    if constexpr (split) vbl[ks] = stack_bf8(v0 - from_bf4(h0), v1 - from_bf4(h1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  reload();
+#pragma unroll
+  for (int a = 0; a < kD / 16; ++a) S[a] = S[a] * gam;
+  // (the eight dk tiles' accumulators interleaved: consecutive MFMAs are independent)
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int a = 0; a < kD / 16; ++a) {
+      const bool own = (a >> 2) == i;
+      S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vb[ks], S[a]);
+    }
+    if constexpr (split) {
+#pragma unroll
+      for (int a = 0; a < kD / 16; ++a) {
+        const bool own = (a >> 2) == i;
+        S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vbl[ks], S[a]);
+      }
+    }
+  }
+  {
+    const __bf16* kt = p.ws_kt + gcn * kChunkElems + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) op.kt[r][ks] = *reinterpret_cast<const bf8*>(kt + ((4 * i + r) * 2 + ks) * kFrag);
+  }
+  constexpr int kMfma = split ? 32 : 16;
+  constexpr int kPairs = kMfma < kLoads ? kMfma : kLoads;
+#pragma unroll
+  for (int k = 0; k < kPairs; ++k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+  }
+  if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+  if constexpr (kLoads > kPairs) __builtin_amdgcn_sched_group_barrier(0x020, kLoads - kPairs, 0);
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 // State wave i of (batch b, v-head h, Dv tile jt): S[a] holds the state's rows dk = 16 a +
 // 4 lg + e (lg = lane / 16) of column dv = 16 jt + lane % 16 (S^T as accumulator tiles).
-// Chunk c: V' = U - W S, S = e^G63 S + K^T (e^(G63-G) V'); S before the update and V' go to
-// mail slot i. `op` holds this wave's share of chunk c's operands and is reloaded with
-// chunk cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk
-// ago) is written to the exchange slot of chunk c + 1.
-template <int NT, int i, bool PRECISE>
-__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared<PRECISE>& sh,
-                                            f4 (&S)[kD / 16],
-                                            StateOps<PRECISE>& op, const StateOps<PRECISE>& nx, size_t gcn, size_t hcn,
-                                            int jt, int slot, int lane) {
+// Chunk c: V' and S = e^G63 S + K^T (e^(G63-G) V'); S before the update and V' go to mail
+// slot i. `op` holds this wave's share of chunk c's operands and is reloaded with chunk
+// cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk ago) is
+// written to the exchange slot of chunk c + 1.
+// GDN_PREFILL_FAST: V' = U - W S with bf16 W and S.
+template <int NT, int i>
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedFast& sh,
+                                            f4 (&S)[kD / 16], StateOpsFast& op, const StateOpsFast& nx, size_t gcn,
+                                            size_t hcn, int jt, int slot, int lane) {
   constexpr int o = i ^ 1;
   // the other wave's halves of this chunk's W and K^T
   bf8 wo[2][4], kto[4][2];
@@ -950,30 +1084,15 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
-  WLoOps wlo;  // (PRECISE) the other wave's half of W's remainder
-  if constexpr (PRECISE) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) wlo.w[r][ks] = sh.wl.w[slot][o][r][ks][lane];
-  }
-  bf8 sb[kD / 32], sbl[kD / 32];  // S as bf16 and (PRECISE) its remainder
-#pragma unroll
-  for (int ks = 0; ks < kD / 32; ++ks) {
-    sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
-    mb.sb[i][ks][lane] = sb[ks];
-    if constexpr (PRECISE) {
-      const f4 h0 = from_bf4(to_bf4(S[2 * ks])), h1 = from_bf4(to_bf4(S[2 * ks + 1]));
-      sbl[ks] = stack_bf8(S[2 * ks] - h0, S[2 * ks + 1] - h1);
-    }
-  }
+  bf8 sb[kD / 32], sbl[kD / 32];
+  pack_state<NT, false>(mb, i, lane, S, sb, sbl);
   f4 egr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) egr[pt] = rows_of(op.g.y, pt, lane);
   const float gam = __shfl(op.g.x, 63, 64);
   // P = W S for the four position tiles (2i, 2i + 1 this wave's, from registers; the others
   // came through LDS), the four accumulators interleaved so that no MFMA waits for the one
-  // before it; with PRECISE to fp32 accuracy: W_hi S_hi + W_lo S_hi + W_hi S_lo
+  // before it
   f4 P[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) P[pt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -984,94 +1103,102 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
       const bool own = (pt >> 1) == i;  // (compile-time after unrolling)
       P[pt] = mfma(own ? op.w[pt & 1][ks] : wo[pt & 1][ks], sb[ks], P[pt]);
     }
-    if constexpr (PRECISE) {
-#pragma unroll
-      for (int pt = 0; pt < 4; ++pt) {
-        const bool own = (pt >> 1) == i;
-        P[pt] = mfma(own ? op.wl.w[pt & 1][ks] : wlo.w[pt & 1][ks], sb[ks], P[pt]);
-      }
-#pragma unroll
-      for (int pt = 0; pt < 4; ++pt) {
-        const bool own = (pt >> 1) == i;
-        P[pt] = mfma(own ? op.w[pt & 1][ks] : wo[pt & 1][ks], sbl[ks], P[pt]);
-      }
-    }
   }
   f4 vpr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) {
-    if constexpr (PRECISE) {
-      vpr[pt] = op.u[pt] - P[pt];
-    } else {
-      vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P[pt];
-    }
+    vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P[pt];
     mb.vpr[i][pt][lane] = vpr[pt];
   }
-  // V'' = e^(G63 - G) V' in bf16 for K^T V''; with PRECISE also its remainder V''_lo, so
-  // that K^T V''_hi + K^T V''_lo (K^T is exact in bf16) carries V'' into the state at fp32
-  // accuracy. The bf16 rounding of V'' is what moves the state (about 2e-3 from the fp32
-  // recurrence at T = 4096); the roundings of S and W in V' = U - W S are corrected by the
-  // following chunks' delta-rule updates.
-  bf8 vb[2], vbl[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const f4 v0 = egr[2 * ks] * vpr[2 * ks], v1 = egr[2 * ks + 1] * vpr[2 * ks + 1];
-    const bf4 h0 = to_bf4(v0), h1 = to_bf4(v1);
-    vb[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-    if constexpr (PRECISE) vbl[ks] = stack_bf8(v0 - from_bf4(h0), v1 - from_bf4(h1));
-  }
-  // S = e^G63 S + K^T V'', with the reloads of chunk cn's share spread between its MFMAs
-  // (one load after each): loads issued in a burst queue up in the CU's address unit
-  // behind the other waves' and hold this wave at the issue.
-  __builtin_amdgcn_sched_barrier(0);
-  load_wu<PRECISE>(p, hcn, jt, i, lane, op);
-#pragma unroll
-  for (int a = 0; a < kD / 16; ++a) S[a] = S[a] * gam;
-  // (the eight dk tiles' accumulators interleaved: consecutive MFMAs are independent)
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-    for (int a = 0; a < kD / 16; ++a) {
-      const bool own = (a >> 2) == i;
-      S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vb[ks], S[a]);
-    }
-    if constexpr (PRECISE) {
-#pragma unroll
-      for (int a = 0; a < kD / 16; ++a) {
-        const bool own = (a >> 2) == i;
-        S[a] = mfma(own ? op.kt[a & 3][ks] : kto[a & 3][ks], vbl[ks], S[a]);
-      }
-    }
-  }
-  load_kt<PRECISE>(p, gcn, i, lane, op);
-  // 16 (32) MFMAs and 22 (with the fp16 U scales) or 29 (with W's remainder) loads
-  constexpr int kMfma = PRECISE ? 32 : 16, kLoads = PRECISE ? 29 : 22;
-  constexpr int kPairs = kMfma < kLoads ? kMfma : kLoads;
-#pragma unroll
-  for (int k = 0; k < kPairs; ++k) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
-  }
-  if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
-  if constexpr (kLoads > kPairs) __builtin_amdgcn_sched_group_barrier(0x020, kLoads - kPairs, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  // chunk c + 1's share for the other wave (the slot was last read in chunk c - 1)
+  // 16 MFMAs and 22 loads (W half 8, U 4, its scales, the gates, K^T half 8)
+  state_update<i, false, 22>(p, S, vpr, egr, gam, kto, op, gcn, lane,
+                             [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
+  share_out(sh, slot ^ 1, i, lane, nx);  // (the slot was last read in chunk c - 1)
+  __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
+                    // have read mail[(c + 1) % 2]
+}
+
+// GDN_PREFILL_ACCURATE: V' = T' (V - e^G . (K S)) at fp32 accuracy: K is exact in bf16 and
+// S is split into bf16 hi + lo (K S_hi + K S_lo), X = V - e^G . K S is formed in fp32 and
+// split into hi + lo, and T' X = T'_hi X_hi + T'_lo X_hi + T'_hi X_lo (the dropped
+// T'_lo X_lo is 2^-16 relative). With U = T' V and W = T' diag(e^G) K this is U - W S.
+template <int NT, int i>
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedKtv& sh,
+                                            f4 (&S)[kD / 16], StateOpsKtv& op, const StateOpsKtv& nx, size_t gcn,
+                                            size_t hcn, int jt, int slot, int lane) {
+  constexpr int o = i ^ 1;
+  // the other wave's halves of this chunk's K and K^T, and its part of T'
+  bf8 kko[2][4], kto[4][2], tpo[kTpBlocks];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sh.w[slot ^ 1][i][r][ks][lane] = nx.w[r][ks];
+    for (int ks = 0; ks < 4; ++ks) kko[r][ks] = sh.kk[slot][o][r][ks][lane];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) sh.kt[slot ^ 1][i][r][ks][lane] = nx.kt[r][ks];
-  if constexpr (PRECISE) {
+    for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+  for (int bi = 0; bi < kTpBlocks; ++bi) tpo[bi] = sh.tp[slot][o][bi][lane];
+  bf8 sb[kD / 32], sbl[kD / 32];
+  pack_state<NT, true>(mb, i, lane, S, sb, sbl);
+  f4 eg[4], egr[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sh.wl.w[slot ^ 1][i][r][ks][lane] = nx.wl.w[r][ks];
+  for (int pt = 0; pt < 4; ++pt) {
+    eg[pt] = rows_of(op.g.x, pt, lane);
+    egr[pt] = rows_of(op.g.y, pt, lane);
   }
-  __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
-                    // have read mail[(c + 1) % 2]
+  const float gam = __shfl(op.g.x, 63, 64);
+  // P = K S_hi + K S_lo for the four position tiles, the accumulators interleaved
+  f4 P[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) P[pt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < kD / 32; ++ks) {
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      const bool own = (pt >> 1) == i;
+      P[pt] = mfma(own ? op.kk[pt & 1][ks] : kko[pt & 1][ks], sb[ks], P[pt]);
+    }
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      const bool own = (pt >> 1) == i;
+      P[pt] = mfma(own ? op.kk[pt & 1][ks] : kko[pt & 1][ks], sbl[ks], P[pt]);
+    }
+  }
+  // X = V - e^G . K S as two B fragments (position blocks) split into bf16 hi + lo
+  bf8 xb[2], xbl[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const f4 v0 = from_bf4(__builtin_shufflevector(op.v[kb], op.v[kb], 0, 1, 2, 3));
+    const f4 v1 = from_bf4(__builtin_shufflevector(op.v[kb], op.v[kb], 4, 5, 6, 7));
+    const f4 x0 = v0 - eg[2 * kb] * P[2 * kb], x1 = v1 - eg[2 * kb + 1] * P[2 * kb + 1];
+    const bf4 h0 = to_bf4(x0), h1 = to_bf4(x1);
+    xb[kb] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+    xbl[kb] = stack_bf8(x0 - from_bf4(h0), x1 - from_bf4(h1));
+  }
+  // V' = T' X over the six nonzero blocks, three products each, in an order that keeps
+  // consecutive MFMAs on different accumulators
+  f4 vpr[4];
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) vpr[pt] = f4{0.f, 0.f, 0.f, 0.f};
+  constexpr int kOrder[kTpBlocks] = {0, 2, 4, 1, 3, 5};
+#pragma unroll
+  for (int term = 0; term < 3; ++term) {
+#pragma unroll
+    for (int j = 0; j < kTpBlocks; ++j) {
+      const int bi = kOrder[j], pt = tp_tile(bi), kb = tp_kb(bi);
+      const bf8 th = i == 0 ? op.tp[bi] : tpo[bi];
+      const bf8 tl = i == 0 ? tpo[bi] : op.tp[bi];
+      vpr[pt] = mfma(term == 1 ? tl : th, term == 2 ? xbl[kb] : xb[kb], vpr[pt]);
+    }
+  }
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) mb.vpr[i][pt][lane] = vpr[pt];
+  // 32 MFMAs and 25 loads (K half 8, T' part 6, V 2, the gates, K^T half 8)
+  state_update<i, true, 25>(p, S, vpr, egr, gam, kto, op, gcn, lane,
+                            [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
+  share_out(sh, slot ^ 1, i, lane, nx);
+  __syncthreads();
 }
 
 // Operands are loaded two chunks ahead, in two register sets used by alternate chunks (an
@@ -1099,36 +1226,30 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
 
   const int last = p.nC - 1;
   StateOps<PRECISE> A, B;
+  auto load_kt = [&](size_t gc, StateOps<PRECISE>& op) {
+    const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) op.kt[r][ks] = *reinterpret_cast<const bf8*>(kt + ((4 * i + r) * 2 + ks) * kFrag);
+  };
   __builtin_amdgcn_sched_barrier(0);
-  load_wu<PRECISE>(p, hc0, jt, i, lane, A);
+  load_front(p, gc0, hc0, jt, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt<PRECISE>(p, gc0, i, lane, A);
+  load_kt(gc0, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_wu<PRECISE>(p, hc0 + min(1, last), jt, i, lane, B);
+  load_front(p, gc0 + min(1, last), hc0 + min(1, last), jt, i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
-  load_kt<PRECISE>(p, gc0 + min(1, last), i, lane, B);
+  load_kt(gc0 + min(1, last), B);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sh.w[0][i][r][ks][lane] = A.w[r][ks];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) sh.kt[0][i][r][ks][lane] = A.kt[r][ks];
-  if constexpr (PRECISE) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sh.wl.w[0][i][r][ks][lane] = A.wl.w[r][ks];
-  }
+  share_out(sh, 0, i, lane, A);
   __syncthreads();
   int c = 0;
   for (; c + 2 <= p.nC; c += 2) {
-    state_chunk<NT, i, PRECISE>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
-    state_chunk<NT, i, PRECISE>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
+    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
+    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
   }
-  if (c < p.nC) state_chunk<NT, i, PRECISE>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
+  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
   __syncthreads();
 
   if (p.state_out) {
@@ -1291,34 +1412,39 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, w, m, u, g, vf, fq, fk, us, gb, wl, total;
+  size_t q, kt, m, g, vf, fq, fk, gb, w, u, us, kk, tp, total;
 };
 
 // conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
 // goes to vf, which the qkv front end fills from the caller's v).
-// precise: U in fp32 (GDN_PREFILL_ACCURATE), else fp16.
+// precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise W, U (fp16) and U's scales.
 WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
   const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
-  const size_t uu = al((size_t)B * Hv * nC * kChunkElems * (precise ? 4 : 2));
   const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
-  WorkspaceLayout L;
+  const size_t fqk = conv ? al((size_t)B * T * Hk * kD * 2) : 0;
+  WorkspaceLayout L{};
   L.q = 0;
   L.kt = L.q + qk;
-  L.w = L.kt + qk;
-  L.m = L.w + wm;
-  L.u = L.m + wm;
-  L.g = L.u + uu;
-  const size_t fqk = conv ? al((size_t)B * T * Hk * kD * 2) : 0;
+  L.m = L.kt + qk;
+  L.g = L.m + wm;
   L.vf = L.g + gg;
   L.fq = L.vf + wm;
   L.fk = L.fq + fqk;
-  L.us = L.fk + fqk;
-  L.gb = L.us + al((size_t)B * Hv * nC * 4 * 4);
-  L.wl = L.gb + gg;
-  L.total = L.wl + (precise ? wm : 0);
+  L.gb = L.fk + fqk;
+  const size_t end = L.gb + gg;
+  if (precise) {
+    L.kk = end;
+    L.tp = L.kk + qk;
+    L.total = L.tp + wm;
+  } else {
+    L.w = end;
+    L.u = L.w + wm;
+    L.us = L.u + wm;
+    L.total = L.us + al((size_t)B * Hv * nC * 4 * 4);
+  }
   return L;
 }
 
@@ -1362,12 +1488,16 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
-  p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
   p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
-  p.ws_u = w + L.u;
-  p.ws_us = reinterpret_cast<float*>(w + L.us);
+  if (precise) {
+    p.ws_kk = reinterpret_cast<__bf16*>(w + L.kk);
+    p.ws_tp = reinterpret_cast<__bf16*>(w + L.tp);
+  } else {
+    p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
+    p.ws_u = reinterpret_cast<_Float16*>(w + L.u);
+    p.ws_us = reinterpret_cast<float*>(w + L.us);
+  }
   p.ws_gb = reinterpret_cast<float*>(w + L.gb);
-  p.ws_wl = reinterpret_cast<__bf16*>(w + L.wl);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {

@@ -283,8 +283,8 @@ def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
     finite bf16 value, bit for bit against the oracle: conv weights (0, 0, 0, 1) make the
     conv output equal to x, the v channels of T = 16 positions hold all 65,280 finite bf16
     patterns, and v is read back from the workspace (its fragment order: block
-    2 (dv / 16) + position / 32, lane 16 ((position % 32) / 8) + dv % 16, element
-    position % 8)."""
+    2 (dv / 16) + position / 32, lane 16 ((position % 16) / 4) + dv % 16, element
+    position % 4 + 4 ((position % 32) / 16))."""
     import torch
     log_case("prefill front end silu on every finite bf16, B=1 T=16")
     B, T, Hk, Hv = 1, 16, 16, 48
@@ -308,13 +308,13 @@ def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
     raw = to_np(ws).view(np.uint16)
     al = lambda n: -(-n // 256) * 256  # noqa: E731  (byte sizes of the workspace pieces)
     nC = 1
-    qk, wm = B * Hk * nC * 8192 * 2, B * Hv * nC * 8192 * 2
-    uu, gg = B * Hv * nC * 8192 * 4, B * Hv * nC * 128 * 4   # U is fp32 in the default precision
-    vf_off = (2 * al(qk) + 2 * al(wm) + al(uu) + al(gg)) // 2
+    qk, wm, gg = B * Hk * nC * 8192 * 2, B * Hv * nC * 8192 * 2, B * Hv * nC * 128 * 4
+    vf_off = (2 * al(qk) + al(wm) + al(gg)) // 2    # after Q, K^T, M and the gate factors
     vf = raw[vf_off:vf_off + Hv * 8192].reshape(Hv, 8192)
     pos = np.arange(T)[:, None]
     dv = np.arange(D)[None, :]
-    idx = (2 * (dv >> 4) + (pos >> 5)) * 512 + (16 * ((pos & 31) >> 3) + (dv & 15)) * 8 + (pos & 7)
+    idx = ((2 * (dv >> 4) + (pos >> 5)) * 512 + (16 * ((pos & 15) >> 2) + (dv & 15)) * 8
+           + (pos & 3) + 4 * ((pos & 31) >> 4))
     v_got = vf[:, idx].transpose(1, 0, 2)                      # (T, Hv, D)
     v_want = v_ref.view(np.uint16)[0]
     bad = int((v_got != v_want).sum())
