@@ -534,8 +534,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   }
   __syncthreads();
 
-  // ---- K K^T and K Q^T on MFMA (wave w: rows j = 16w..; kept in registers), Q to the
-  // workspace, K^T into LDS ----
+  // ---- K K^T and (fast form) K Q^T on MFMA (wave w: rows j = 16w..; kept in registers), Q
+  // to the workspace, K^T into LDS ----
   f4 gr[4], kq[4];  // lane: (j = 16 wave + 4 lg + e, i = 16 ct + fr): (K K^T)_ji, (Q K^T)_ij
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     for (int ks = 0; ks < kD / 32; ++ks) {
       const bf8 ak = frag(s.u.fe.k, 16 * wave + fr, 32 * ks + fk);
       gr[ct] = mfma(ak, frag(s.u.fe.k, 16 * ct + fr, 32 * ks + fk), gr[ct]);
-      kq[ct] = mfma(ak, frag(s.u.fe.q, 16 * ct + fr, 32 * ks + fk), kq[ct]);
+      if constexpr (!PRECISE) kq[ct] = mfma(ak, frag(s.u.fe.q, 16 * ct + fr, 32 * ks + fk), kq[ct]);
     }
   }
   {
@@ -600,10 +600,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       __syncthreads();
     }
 
-    // A (into LDS as -A^T) and M (hi, lo to the workspace) from the registers
+    // A (into LDS as -A^T) and, in the fast form, M (hi, lo to the workspace; the accurate
+    // form's scan builds M itself) from the registers
     for (int r = 0; r < gs; ++r) {
       const size_t hc = ((size_t)b * p.Hv + g * p.rep + r0 + r) * p.nC + c;
-      __bf16* wm = p.ws_m + hc * kChunkElems;
+      __bf16* wm = PRECISE ? nullptr : p.ws_m + hc * kChunkElems;
       const int j0 = 16 * wave + 4 * lg;
       const f4 Gj = *reinterpret_cast<const f4*>(&s.G[r][j0]);
 #pragma unroll
@@ -618,6 +619,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           mv[e] = dr * kq[ct][e];
           s.u.nat[r][j][i] = j < i ? -((bi * dr) * gr[ct][e]) : 0.0f;
         }
+        if constexpr (PRECISE) continue;
         const bf4 hi = to_bf4(mv);
         const bf4 lo = to_bf4(mv - from_bf4(hi));
         // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating.
@@ -854,7 +856,9 @@ __device__ __forceinline__ int out_tile(int half, int i) { return i == 0 ? half 
 struct OutOps {
   bf8 q[2][4];     // Q [pos tile][dk block]          (A of Q S)
   bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V'); [0][1] is zero, never loaded
+                   // (GDN_PREFILL_FAST; the accurate form builds M from K and Q)
   float eg;        // e^G at position `lane`
+  float gv;        // G at position `lane` (GDN_PREFILL_ACCURATE)
   unsigned touch[2];  // the cache-line touches issued with this set (see touch_lines)
 };
 
@@ -862,9 +866,9 @@ struct OutOps {
 // line finds it already there: every workgroup of a v-head asks for the same lines at the
 // same time, so a line fetched on demand costs all of them the full memory latency. The
 // output waves therefore touch (one dword per 128-byte line) the lines of the chunk four
-// ahead: the v-head's four workgroups split W, M, Q and K^T between them (group `grp`
-// takes one of the four 16 KB matrices), and each workgroup touches its own U columns and
-// the gate pairs.
+// ahead: the v-head's four workgroups split the four 16 KB matrices between them (group
+// `grp` takes one: W, M, Q, K^T in the fast form, K, T', Q, K^T in the accurate one), and
+// each workgroup touches its own U (or V) columns and the gate pairs.
 template <bool PRECISE>
 __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, size_t hc, int grp, int jt, int half,
                                             int lane, unsigned (&t)[2]) {
@@ -872,7 +876,7 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
   if (half == 0) {
     const int r = grp & 3;
     const __bf16* m = r == 0 ? (PRECISE ? p.ws_kk + gc * kChunkElems : p.ws_w + hc * kChunkElems)
-                    : r == 1 ? p.ws_m + hc * kChunkElems
+                    : r == 1 ? (PRECISE ? p.ws_tp : p.ws_m) + hc * kChunkElems
                     : r == 2 ? p.ws_q + gc * kChunkElems
                              : p.ws_kt + gc * kChunkElems;
     base = reinterpret_cast<const unsigned*>(m);
@@ -880,11 +884,10 @@ __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, s
     t[1] = base[(64 + lane) * 32];
   } else {
     if constexpr (PRECISE) {
-      // a quarter of T' (each of the v-head's four workgroups one) and this workgroup's two
-      // dv tiles of V (4 KB, 32 lines)
-      const unsigned* tb = reinterpret_cast<const unsigned*>(p.ws_tp + hc * kChunkElems);
+      // this workgroup's two dv tiles of V (4 KB, 32 lines) and the (G, beta) pairs
       const unsigned* vb = reinterpret_cast<const unsigned*>(p.ws_vf + hc * kChunkElems + jt * 2 * kFrag);
-      t[0] = lane < 32 ? tb[((grp & 3) * 32 + lane) * 32] : vb[(lane - 32) * 32];
+      const unsigned* gb = reinterpret_cast<const unsigned*>(p.ws_gb + hc * kGStride);
+      t[0] = lane < 32 ? vb[lane * 32] : gb[(lane & 3) * 32];
     } else {
       // this workgroup's two dv tiles of U: 4 KB, 32 lines
       base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
@@ -926,20 +929,25 @@ __device__ __forceinline__ void load_front(const PrefillParams& p, size_t gc, si
   for (int kb = 0; kb < 2; ++kb) op.v[kb] = *reinterpret_cast<const bf8*>(v + (2 * jt + kb) * kFrag);
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
+template <bool PRECISE>
 __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_t hc, int half, int lane, OutOps& op) {
   const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
-  const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int pt = out_tile(half, i);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.q[i][ks] = *reinterpret_cast<const bf8*>(q + (pt * 4 + ks) * kFrag);
+    if constexpr (!PRECISE) {
+      const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
 #pragma unroll
-    for (int ks = 0; ks <= i; ++ks)
+      for (int ks = 0; ks <= i; ++ks)
 #pragma unroll
-      for (int hl = 0; hl < 2; ++hl) op.m[i][ks][hl] = *reinterpret_cast<const bf8*>(m + ((pt * 2 + ks) * 2 + hl) * kFrag);
+        for (int hl = 0; hl < 2; ++hl)
+          op.m[i][ks][hl] = *reinterpret_cast<const bf8*>(m + ((pt * 2 + ks) * 2 + hl) * kFrag);
+    }
   }
   op.eg = p.ws_g[hc * kGStride + 2 * lane];
+  if constexpr (PRECISE) op.gv = p.ws_gb[hc * kGStride + 2 * lane];
 }
 
 
@@ -959,14 +967,15 @@ struct ScanSharedFast {
   bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
 };
 struct ScanSharedKtv {
-  bf8 kk[2][2][2][4][64];          // [slot][wave][own pos tile][dk block][lane]
+  bf8 kk[3][2][2][4][64];          // [chunk % 3][wave][own pos tile][dk block][lane] (three
+                                   // slots: the output waves read chunk c's K during c + 1)
   bf8 kt[2][2][4][2][64];          // [slot][wave][own dk tile][pos block][lane]
   bf8 tp[2][2][kTpBlocks][64];     // [slot][wave (0: hi, 1: lo)][block][lane]
 };
 template <bool PRECISE>
 using ScanShared = typename std::conditional<PRECISE, ScanSharedKtv, ScanSharedFast>::type;
 
-__device__ __forceinline__ void share_out(ScanSharedFast& sh, int slot, int i, int lane, const StateOpsFast& nx) {
+__device__ __forceinline__ void share_out(ScanSharedFast& sh, int slot, int, int i, int lane, const StateOpsFast& nx) {
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -976,11 +985,12 @@ __device__ __forceinline__ void share_out(ScanSharedFast& sh, int slot, int i, i
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) sh.kt[slot][i][r][ks][lane] = nx.kt[r][ks];
 }
-__device__ __forceinline__ void share_out(ScanSharedKtv& sh, int slot, int i, int lane, const StateOpsKtv& nx) {
+__device__ __forceinline__ void share_out(ScanSharedKtv& sh, int slot, int kslot, int i, int lane,
+                                          const StateOpsKtv& nx) {
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sh.kk[slot][i][r][ks][lane] = nx.kk[r][ks];
+    for (int ks = 0; ks < 4; ++ks) sh.kk[kslot][i][r][ks][lane] = nx.kk[r][ks];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -1072,7 +1082,7 @@ __device__ __forceinline__ void state_update(const PrefillParams& p, f4 (&S)[kD 
 template <int NT, int i>
 __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedFast& sh,
                                             f4 (&S)[kD / 16], StateOpsFast& op, const StateOpsFast& nx, size_t gcn,
-                                            size_t hcn, int jt, int slot, int lane) {
+                                            size_t hcn, int jt, int slot, int, int lane) {
   constexpr int o = i ^ 1;
   // the other wave's halves of this chunk's W and K^T
   bf8 wo[2][4], kto[4][2];
@@ -1113,7 +1123,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   // 16 MFMAs and 22 loads (W half 8, U 4, its scales, the gates, K^T half 8)
   state_update<i, false, 22>(p, S, vpr, egr, gam, kto, op, gcn, lane,
                              [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
-  share_out(sh, slot ^ 1, i, lane, nx);  // (the slot was last read in chunk c - 1)
+  share_out(sh, slot ^ 1, 0, i, lane, nx);  // (the slot was last read in chunk c - 1)
   __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
                     // have read mail[(c + 1) % 2]
 }
@@ -1125,14 +1135,14 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
 template <int NT, int i>
 __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedKtv& sh,
                                             f4 (&S)[kD / 16], StateOpsKtv& op, const StateOpsKtv& nx, size_t gcn,
-                                            size_t hcn, int jt, int slot, int lane) {
+                                            size_t hcn, int jt, int slot, int kslot, int lane) {
   constexpr int o = i ^ 1;
   // the other wave's halves of this chunk's K and K^T, and its part of T'
   bf8 kko[2][4], kto[4][2], tpo[kTpBlocks];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kko[r][ks] = sh.kk[slot][o][r][ks][lane];
+    for (int ks = 0; ks < 4; ++ks) kko[r][ks] = sh.kk[kslot][o][r][ks][lane];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -1197,7 +1207,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   // 32 MFMAs and 25 loads (K half 8, T' part 6, V 2, the gates, K^T half 8)
   state_update<i, true, 25>(p, S, vpr, egr, gam, kto, op, gcn, lane,
                             [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
-  share_out(sh, slot ^ 1, i, lane, nx);
+  share_out(sh, slot ^ 1, kslot == 2 ? 0 : kslot + 1, i, lane, nx);
   __syncthreads();
 }
 
@@ -1242,14 +1252,16 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   __builtin_amdgcn_sched_barrier(0);
   load_kt(gc0 + min(1, last), B);
   __builtin_amdgcn_sched_barrier(0);
-  share_out(sh, 0, i, lane, A);
+  share_out(sh, 0, 0, i, lane, A);
   __syncthreads();
-  int c = 0;
+  int c = 0, kslot = 0;  // kslot = c % 3 (the accurate form's three K slots)
   for (; c + 2 <= p.nC; c += 2) {
-    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, lane);
-    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, lane);
+    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, kslot, lane);
+    kslot = kslot == 2 ? 0 : kslot + 1;
+    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, kslot, lane);
+    kslot = kslot == 2 ? 0 : kslot + 1;
   }
-  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, lane);
+  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, kslot, lane);
   __syncthreads();
 
   if (p.state_out) {
@@ -1294,9 +1306,10 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile
 // they stay live.
 template <int NT, bool OBF16, bool PRECISE>
 __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
+                                             const ScanShared<PRECISE>& sh,
                                              OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                              OutOps& op, size_t gcn, size_t hcn, size_t gc4, size_t hc4, int b, int h,
-                                             int jt, int half, int c, int lane, unsigned& tacc) {
+                                             int jt, int half, int c, int kslot, int lane, unsigned& tacc) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const int fr = lane & 15, lg = lane >> 4;
   if (c > 0) store_tile<NT, OT>(p, tile, b, h, jt, half, c - 1, lane);
@@ -1304,6 +1317,41 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   f4 eg[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) eg[i] = rows_of(op.eg, out_tile(half, i), lane);
+  if constexpr (PRECISE) {
+    // M = e^(G_i - G_j) (Q K^T)_ij (j <= i) of this wave's position tiles, from the chunk's K
+    // (the state waves' K slot, still unchanged) and Q, as the intra kernel makes it for the
+    // fast form: tile (j tile, i tile) of K Q^T as an accumulator (rows j), decayed, split
+    // into bf16 hi + lo; two stacked j tiles are the A fragment of M's rows i over one
+    // 32-position block of j in the interleaved k order.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int pt = out_tile(half, i);
+      const float gi = __shfl(op.gv, 16 * pt + fr, 64);
+#pragma unroll
+      for (int kb = 0; kb <= i; ++kb) {
+        f4 mt[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int jt2 = 2 * kb + hh;
+          f4 acc = {0.f, 0.f, 0.f, 0.f};
+          if (jt2 <= pt) {
+#pragma unroll
+            for (int ks = 0; ks < kD / 32; ++ks)
+              acc = mfma(sh.kk[kslot][jt2 >> 1][jt2 & 1][ks][lane], op.q[i][ks], acc);
+          }
+          const f4 gj = rows_of(op.gv, jt2, lane);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = 16 * jt2 + 4 * lg + e;
+            mt[hh][e] = j <= 16 * pt + fr ? fast_exp(gi - gj[e]) * acc[e] : 0.0f;
+          }
+        }
+        const f4 h0 = from_bf4(to_bf4(mt[0])), h1 = from_bf4(to_bf4(mt[1]));
+        op.m[i][kb][0] = stack_bf8(mt[0], mt[1]);
+        op.m[i][kb][1] = stack_bf8(mt[0] - h0, mt[1] - h1);
+      }
+    }
+  }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     bf8 sb[kD / 32];
@@ -1337,7 +1385,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  load_qm(p, gcn, hcn, half, lane, op);
+  load_qm<PRECISE>(p, gcn, hcn, half, lane, op);
   touch_lines<PRECISE>(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // done with mail[c % 2]; mail[(c + 1) % 2] is complete
@@ -1345,6 +1393,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
 
 template <int NT, bool OBF16, bool PRECISE>
 __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
+                                                 const ScanShared<PRECISE>& sh,
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                                  int b, int h, int g, int jt, int half, int lane) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
@@ -1355,24 +1404,26 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
   unsigned tacc = 0;
   OutOps A, B;
   __builtin_amdgcn_sched_barrier(0);
-  load_qm(p, gc0, hc0, half, lane, A);
+  load_qm<PRECISE>(p, gc0, hc0, half, lane, A);
   touch_lines<PRECISE>(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
   __builtin_amdgcn_sched_barrier(0);
-  load_qm(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
+  load_qm<PRECISE>(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
   touch_lines<PRECISE>(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the state waves' exchange of chunk 0's shares
   __syncthreads();  // chunk 0's mail
-  int c = 0;
+  int c = 0, kslot = 0;  // kslot = c % 3
   for (; c + 2 <= p.nC; c += 2) {
-    output_chunk<NT, OBF16, PRECISE>(p, mail[0], tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
-                            gc0 + min(c + 4, last), hc0 + min(c + 4, last), b, h, jt, half, c, lane, tacc);
-    output_chunk<NT, OBF16, PRECISE>(p, mail[1], tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
-                            gc0 + min(c + 5, last), hc0 + min(c + 5, last), b, h, jt, half, c + 1, lane, tacc);
+    output_chunk<NT, OBF16, PRECISE>(p, mail[0], sh, tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
+                            gc0 + min(c + 4, last), hc0 + min(c + 4, last), b, h, jt, half, c, kslot, lane, tacc);
+    kslot = kslot == 2 ? 0 : kslot + 1;
+    output_chunk<NT, OBF16, PRECISE>(p, mail[1], sh, tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
+                            gc0 + min(c + 5, last), hc0 + min(c + 5, last), b, h, jt, half, c + 1, kslot, lane, tacc);
+    kslot = kslot == 2 ? 0 : kslot + 1;
   }
   if (c < p.nC)
-    output_chunk<NT, OBF16, PRECISE>(p, mail[0], tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half, c,
-                            lane, tacc);
+    output_chunk<NT, OBF16, PRECISE>(p, mail[0], sh, tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half,
+                            c, kslot, lane, tacc);
   store_tile<NT, OT>(p, tile, b, h, jt, half, p.nC - 1, lane);
   // (never true: T >= 1; it keeps the touches from being dropped as unused)
   if (tacc == 0x9e3779b9u && p.T < 0) static_cast<float*>(p.o)[lane] = 0.0f;
@@ -1407,17 +1458,17 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
   } else if (wave == 1) {
     scan_state_wave<NT, 1, PRECISE>(p, mail, shared_ops, b, h, g, jt + 1, lane);
   } else {
-    scan_output_wave<NT, OBF16, PRECISE>(p, mail, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
+    scan_output_wave<NT, OBF16, PRECISE>(p, mail, shared_ops, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
   }
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, m, g, vf, fq, fk, gb, w, u, us, kk, tp, total;
+  size_t q, kt, g, vf, fq, fk, gb, m, w, u, us, kk, tp, total;
 };
 
 // conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
 // goes to vf, which the qkv front end fills from the caller's v).
-// precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise W, U (fp16) and U's scales.
+// precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise M, W, U (fp16) and U's scales.
 WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -1428,8 +1479,7 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
   WorkspaceLayout L{};
   L.q = 0;
   L.kt = L.q + qk;
-  L.m = L.kt + qk;
-  L.g = L.m + wm;
+  L.g = L.kt + qk;
   L.vf = L.g + gg;
   L.fq = L.vf + wm;
   L.fk = L.fq + fqk;
@@ -1440,7 +1490,8 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
     L.tp = L.kk + qk;
     L.total = L.tp + wm;
   } else {
-    L.w = end;
+    L.m = end;
+    L.w = L.m + wm;
     L.u = L.w + wm;
     L.us = L.u + wm;
     L.total = L.us + al((size_t)B * Hv * nC * 4 * 4);
@@ -1488,11 +1539,11 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
-  p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
   if (precise) {
     p.ws_kk = reinterpret_cast<__bf16*>(w + L.kk);
     p.ws_tp = reinterpret_cast<__bf16*>(w + L.tp);
   } else {
+    p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
     p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
     p.ws_u = reinterpret_cast<_Float16*>(w + L.u);
     p.ws_us = reinterpret_cast<float*>(w + L.us);

@@ -308,8 +308,8 @@ def test_prefill_frontend_silu_every_finite_bf16(O, gdn, dev):
     raw = to_np(ws).view(np.uint16)
     al = lambda n: -(-n // 256) * 256  # noqa: E731  (byte sizes of the workspace pieces)
     nC = 1
-    qk, wm, gg = B * Hk * nC * 8192 * 2, B * Hv * nC * 8192 * 2, B * Hv * nC * 128 * 4
-    vf_off = (2 * al(qk) + al(wm) + al(gg)) // 2    # after Q, K^T, M and the gate factors
+    qk, gg = B * Hk * nC * 8192 * 2, B * Hv * nC * 128 * 4
+    vf_off = (2 * al(qk) + al(gg)) // 2    # after Q, K^T and the gate factors
     vf = raw[vf_off:vf_off + Hv * 8192].reshape(Hv, 8192)
     pos = np.arange(T)[:, None]
     dv = np.arange(D)[None, :]
