@@ -850,7 +850,7 @@ using StateOps = typename std::conditional<PRECISE, StateOpsKtv, StateOpsFast>::
 // Output wave `half` makes position tiles half and 3 - half of each chunk: M is lower
 // triangular, so the first tile (rows < 32) has one nonzero 32-column block and the second
 // two, and both waves get three of the six.
-__device__ __forceinline__ int out_tile(int half, int i) { return i == 0 ? half : 3 - half; }
+__device__ __forceinline__ constexpr int out_tile(int half, int i) { return i == 0 ? half : 3 - half; }
 
 // An output wave's operands of one chunk: its two position tiles out_tile(half, 0 / 1).
 struct OutOps {
@@ -1323,6 +1323,30 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
     // fast form: tile (j tile, i tile) of K Q^T as an accumulator (rows j), decayed, split
     // into bf16 hi + lo; two stacked j tiles are the A fragment of M's rows i over one
     // 32-position block of j in the interleaved k order.
+    // (half is a compile-time constant here: the tiles below the diagonal are known, and
+    // their MFMAs, all K fragments read first, interleave)
+    constexpr int kJt = 4;
+    bf8 kf[kJt][kD / 32];
+#pragma unroll
+    for (int jt2 = 0; jt2 < kJt; ++jt2)
+#pragma unroll
+      for (int ks = 0; ks < kD / 32; ++ks)
+        if (jt2 <= out_tile(half, 1)) kf[jt2][ks] = sh.kk[kslot][jt2 >> 1][jt2 & 1][ks][lane];
+    f4 acc[2][kJt];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jt2 = 0; jt2 < kJt; ++jt2) acc[i][jt2] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kD / 32; ++ks)
+#pragma unroll
+      for (int jt2 = 0; jt2 < kJt; ++jt2)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if (jt2 <= out_tile(half, i)) acc[i][jt2] = mfma(kf[jt2][ks], op.q[i][ks], acc[i][jt2]);
+    f4 gj[kJt];
+#pragma unroll
+    for (int jt2 = 0; jt2 < kJt; ++jt2) gj[jt2] = rows_of(op.gv, jt2, lane);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int pt = out_tile(half, i);
@@ -1333,17 +1357,10 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int jt2 = 2 * kb + hh;
-          f4 acc = {0.f, 0.f, 0.f, 0.f};
-          if (jt2 <= pt) {
-#pragma unroll
-            for (int ks = 0; ks < kD / 32; ++ks)
-              acc = mfma(sh.kk[kslot][jt2 >> 1][jt2 & 1][ks][lane], op.q[i][ks], acc);
-          }
-          const f4 gj = rows_of(op.gv, jt2, lane);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int j = 16 * jt2 + 4 * lg + e;
-            mt[hh][e] = j <= 16 * pt + fr ? fast_exp(gi - gj[e]) * acc[e] : 0.0f;
+            mt[hh][e] = jt2 <= pt && j <= 16 * pt + fr ? fast_exp(gi - gj[jt2][e]) * acc[i][jt2][e] : 0.0f;
           }
         }
         const f4 h0 = from_bf4(to_bf4(mt[0])), h1 = from_bf4(to_bf4(mt[1]));
@@ -1391,11 +1408,12 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   __syncthreads();  // done with mail[c % 2]; mail[(c + 1) % 2] is complete
 }
 
-template <int NT, bool OBF16, bool PRECISE>
+template <int NT, bool OBF16, bool PRECISE, int HALF>
 __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
                                                  const ScanShared<PRECISE>& sh,
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
-                                                 int b, int h, int g, int jt, int half, int lane) {
+                                                 int b, int h, int g, int jt, int lane) {
+  constexpr int half = HALF;
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
   const size_t hc0 = ((size_t)b * p.Hv + h) * p.nC;
@@ -1457,8 +1475,10 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
     scan_state_wave<NT, 0, PRECISE>(p, mail, shared_ops, b, h, g, jt, lane);
   } else if (wave == 1) {
     scan_state_wave<NT, 1, PRECISE>(p, mail, shared_ops, b, h, g, jt + 1, lane);
+  } else if (wave == NT) {
+    scan_output_wave<NT, OBF16, PRECISE, 0>(p, mail, shared_ops, tiles[0], b, h, g, jt, lane);
   } else {
-    scan_output_wave<NT, OBF16, PRECISE>(p, mail, shared_ops, tiles[wave - NT], b, h, g, jt, wave - NT, lane);
+    scan_output_wave<NT, OBF16, PRECISE, 1>(p, mail, shared_ops, tiles[1], b, h, g, jt, lane);
   }
 }
 
