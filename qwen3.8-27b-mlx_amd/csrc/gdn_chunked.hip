@@ -951,13 +951,14 @@ __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_
 }
 
 
-// The per-position value v (lane t holds position t) at positions 16 pt + 4 (lane / 16) + e,
-// e < 4: the accumulator-row order.
-__device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
-  f4 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = __shfl(v, 16 * pt + 4 * (lane >> 4) + e, 64);
-  return r;
+// The per-position pairs of a wave's gate row `row` (written by this wave) at positions
+// 16 pt + 4 (lane / 16) + e, e < 4 (the accumulator-row order): two 16-byte LDS reads, each
+// the same address for a lane group (a broadcast) instead of eight lane shuffles.
+__device__ __forceinline__ void pair_rows(const float2* row, int pt, int lane, f4& x, f4& y) {
+  const f4 a = *reinterpret_cast<const f4*>(row + 16 * pt + 4 * (lane >> 4));
+  const f4 b = *reinterpret_cast<const f4*>(row + 16 * pt + 4 * (lane >> 4) + 2);
+  x = f4{a[0], a[2], b[0], b[2]};
+  y = f4{a[1], a[3], b[1], b[3]};
 }
 
 // The operand halves the two state waves exchange, per lane, in two slots: slot c % 2
@@ -965,12 +966,14 @@ __device__ __forceinline__ f4 rows_of(float v, int pt, int lane) {
 struct ScanSharedFast {
   bf8 w[2][2][2][4][64];   // [slot][wave][own pos tile][dk block][lane]
   bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
+  float2 gt[4][64];        // [wave][position]: the wave's per-position gate pair of its chunk
 };
 struct ScanSharedKtv {
   bf8 kk[3][2][2][4][64];          // [chunk % 3][wave][own pos tile][dk block][lane] (three
                                    // slots: the output waves read chunk c's K during c + 1)
   bf8 kt[2][2][4][2][64];          // [slot][wave][own dk tile][pos block][lane]
   bf8 tp[2][2][kTpBlocks][64];     // [slot][wave (0: hi, 1: lo)][block][lane]
+  float2 gt[4][64];                // [wave][position]: the wave's per-position gate pair
 };
 template <bool PRECISE>
 using ScanShared = typename std::conditional<PRECISE, ScanSharedKtv, ScanSharedFast>::type;
@@ -1096,10 +1099,14 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
     for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
   bf8 sb[kD / 32], sbl[kD / 32];
   pack_state<NT, false>(mb, i, lane, S, sb, sbl);
+  sh.gt[i][lane] = op.g;
   f4 egr[4];
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt) egr[pt] = rows_of(op.g.y, pt, lane);
-  const float gam = __shfl(op.g.x, 63, 64);
+  for (int pt = 0; pt < 4; ++pt) {
+    f4 unused;
+    pair_rows(sh.gt[i], pt, lane, unused, egr[pt]);
+  }
+  const float gam = sh.gt[i][63].x;
   // P = W S for the four position tiles (2i, 2i + 1 this wave's, from registers; the others
   // came through LDS), the four accumulators interleaved so that no MFMA waits for the one
   // before it
@@ -1151,13 +1158,11 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   for (int bi = 0; bi < kTpBlocks; ++bi) tpo[bi] = sh.tp[slot][o][bi][lane];
   bf8 sb[kD / 32], sbl[kD / 32];
   pack_state<NT, true>(mb, i, lane, S, sb, sbl);
+  sh.gt[i][lane] = op.g;
   f4 eg[4], egr[4];
 #pragma unroll
-  for (int pt = 0; pt < 4; ++pt) {
-    eg[pt] = rows_of(op.g.x, pt, lane);
-    egr[pt] = rows_of(op.g.y, pt, lane);
-  }
-  const float gam = __shfl(op.g.x, 63, 64);
+  for (int pt = 0; pt < 4; ++pt) pair_rows(sh.gt[i], pt, lane, eg[pt], egr[pt]);
+  const float gam = sh.gt[i][63].x;
   // P = K S_hi + K S_lo for the four position tiles, the accumulators interleaved
   f4 P[4];
 #pragma unroll
@@ -1306,7 +1311,7 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile
 // they stay live.
 template <int NT, bool OBF16, bool PRECISE>
 __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
-                                             const ScanShared<PRECISE>& sh,
+                                             ScanShared<PRECISE>& sh,
                                              OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                              OutOps& op, size_t gcn, size_t hcn, size_t gc4, size_t hc4, int b, int h,
                                              int jt, int half, int c, int kslot, int lane, unsigned& tacc) {
@@ -1314,9 +1319,12 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   const int fr = lane & 15, lg = lane >> 4;
   if (c > 0) store_tile<NT, OT>(p, tile, b, h, jt, half, c - 1, lane);
   tacc ^= op.touch[0] ^ op.touch[1];
-  f4 eg[2];
+  // (e^G, G) per position through this wave's gate row
+  float2* grow = sh.gt[NT + half];
+  grow[lane] = make_float2(op.eg, PRECISE ? op.gv : 0.0f);
+  f4 eg[2], gr[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) eg[i] = rows_of(op.eg, out_tile(half, i), lane);
+  for (int i = 0; i < 2; ++i) pair_rows(grow, out_tile(half, i), lane, eg[i], gr[i]);
   if constexpr (PRECISE) {
     // M = e^(G_i - G_j) (Q K^T)_ij (j <= i) of this wave's position tiles, from the chunk's K
     // (the state waves' K slot, still unchanged) and Q, as the intra kernel makes it for the
@@ -1346,11 +1354,18 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
           if (jt2 <= out_tile(half, i)) acc[i][jt2] = mfma(kf[jt2][ks], op.q[i][ks], acc[i][jt2]);
     f4 gj[kJt];
 #pragma unroll
-    for (int jt2 = 0; jt2 < kJt; ++jt2) gj[jt2] = rows_of(op.gv, jt2, lane);
+    for (int jt2 = 0; jt2 < kJt; ++jt2) {
+      if (jt2 == out_tile(half, 0)) gj[jt2] = gr[0];
+      else if (jt2 == out_tile(half, 1)) gj[jt2] = gr[1];
+      else {
+        f4 unused;
+        pair_rows(grow, jt2, lane, unused, gj[jt2]);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int pt = out_tile(half, i);
-      const float gi = __shfl(op.gv, 16 * pt + fr, 64);
+      const float gi = grow[16 * pt + fr].y;
 #pragma unroll
       for (int kb = 0; kb <= i; ++kb) {
         f4 mt[2];
@@ -1410,7 +1425,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
 
 template <int NT, bool OBF16, bool PRECISE, int HALF>
 __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
-                                                 const ScanShared<PRECISE>& sh,
+                                                 ScanShared<PRECISE>& sh,
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                                  int b, int h, int g, int jt, int lane) {
   constexpr int half = HALF;
