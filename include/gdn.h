@@ -79,15 +79,15 @@ typedef enum gdn_gate_mode {
 typedef enum gdn_prefill_precision {
   GDN_PREFILL_ACCURATE = 0, /* the default, as the reference runs an fp32 kernel for every
                                window (cpp/src/model.cpp:619-624): the state products carry
-                               fp32 accuracy -- U kept in fp32, W stored with its bf16
-                               remainder and W S formed as W_hi S_hi + W_lo S_hi + W_hi S_lo,
-                               V'' split into bf16 hi + lo for K^T V'' -- so the state the next
-                               window or decode step starts from is within about 1e-5
-                               (max|a-b|/max|b|; measured 3e-6..8e-6) of the fp32 recurrence
-                               whatever the gates */
+                               fp32 accuracy -- V' formed as T' (V - e^G K S) with S, the
+                               fp32 X = V - e^G K S and T' split into bf16 hi + lo, and V''
+                               split for K^T V'' -- so the state the next window or decode
+                               step starts from is within about 1e-5 (max|a-b|/max|b|;
+                               measured 3e-6..8e-6) of the fp32 recurrence whatever the
+                               gates; the smaller workspace */
   GDN_PREFILL_FAST = 1      /* bf16 operands in the state products and U kept as fp16: the
-                               state ends about 2e-3 from the fp32 recurrence; a smaller
-                               workspace and about two thirds of the time at T = 4096 */
+                               state ends about 2e-3 from the fp32 recurrence; about 0.9 of
+                               the time at T = 4096 */
 } gdn_prefill_precision;
 
 typedef enum gdn_states_layout {
