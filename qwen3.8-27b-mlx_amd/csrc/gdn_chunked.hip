@@ -94,6 +94,44 @@ __device__ __forceinline__ bf8 stack_bf8(f4 lo, f4 hi) {
   return __builtin_shufflevector(to_bf4(lo), to_bf4(hi), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Eight fp32 values (two f4, as stack_bf8 orders them) split into bf16 hi (round to nearest
+// even) and the bf16 of the remainder, so that hi + lo carries the value to about 2^-16.
+// Each pair is converted once (one v_cvt_pk_bf16_f32); the two rounded values the remainder
+// needs come back out of the packed word with a shift and a mask (converting each value a
+// second time on its own, as from_bf4(to_bf4(x)) compiles, doubled the conversions).
+__device__ __forceinline__ void split_bf8(f4 a, f4 b, bf8& hi, bf8& lo) {
+  u32x4v w;
+  f4 ra, rb;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){a[2 * j], a[2 * j + 1]}, bf2v));
+    w[2 + j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){b[2 * j], b[2 * j + 1]}, bf2v));
+    ra[2 * j] = a[2 * j] - __builtin_bit_cast(float, w[j] << 16);
+    ra[2 * j + 1] = a[2 * j + 1] - __builtin_bit_cast(float, w[j] & 0xFFFF0000u);
+    rb[2 * j] = b[2 * j] - __builtin_bit_cast(float, w[2 + j] << 16);
+    rb[2 * j + 1] = b[2 * j + 1] - __builtin_bit_cast(float, w[2 + j] & 0xFFFF0000u);
+  }
+  hi = __builtin_bit_cast(bf8, w);
+  lo = stack_bf8(ra, rb);
+}
+// The same for four values.
+__device__ __forceinline__ void split_bf4(f4 a, bf4& hi, bf4& lo) {
+  uint32_t w[2];
+  f4 ra;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    w[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){a[2 * j], a[2 * j + 1]}, bf2v));
+    ra[2 * j] = a[2 * j] - __builtin_bit_cast(float, w[j] << 16);
+    ra[2 * j + 1] = a[2 * j + 1] - __builtin_bit_cast(float, w[j] & 0xFFFF0000u);
+  }
+  hi = __builtin_bit_cast(bf4, w);
+  lo = to_bf4(ra);
+}
+
 // e^x for x <= 0 from the hardware 2^x (the decay factors inside a chunk).
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
@@ -620,8 +658,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           s.u.nat[r][j][i] = j < i ? -((bi * dr) * gr[ct][e]) : 0.0f;
         }
         if constexpr (PRECISE) continue;
-        const bf4 hi = to_bf4(mv);
-        const bf4 lo = to_bf4(mv - from_bf4(hi));
+        bf4 hi, lo;
+        split_bf4(mv, hi, lo);
         // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating.
         // Blocks (0, 1) and (1, 1) lie above the diagonal: zero, neither stored nor read.
         const int off = ilv_off(i, j0, 2);
@@ -670,11 +708,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           float tv[8];
           tprime(kh, tv);
           bf8 th, tl;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            th[e] = (__bf16)tv[e];
-            tl[e] = (__bf16)(tv[e] - (float)th[e]);
-          }
+          split_bf8(f4{tv[0], tv[1], tv[2], tv[3]}, f4{tv[4], tv[5], tv[6], tv[7]}, th, tl);
           __builtin_nontemporal_store(th, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2) * kFrag));
           __builtin_nontemporal_store(tl, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2 + 1) * kFrag));
         }
@@ -700,13 +734,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
           tprime(kh, tv);
           const f4 e0 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 4 * lg]);
           const f4 e1 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 16 + 4 * lg]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const __bf16 hi = (__bf16)tv[e];
-            ah[kh][e] = hi;
-            al[kh][e] = (__bf16)(tv[e] - (float)hi);
-            te[kh][e] = (__bf16)(tv[e] * (e < 4 ? e0[e] : e1[e - 4]));
-          }
+          split_bf8(f4{tv[0], tv[1], tv[2], tv[3]}, f4{tv[4], tv[5], tv[6], tv[7]}, ah[kh], al[kh]);
+          te[kh] = stack_bf8(f4{tv[0], tv[1], tv[2], tv[3]} * e0, f4{tv[4], tv[5], tv[6], tv[7]} * e1);
         }
         f4 ut[kD / 16];
 #pragma unroll
@@ -1009,12 +1038,9 @@ __device__ __forceinline__ void pack_state(ScanMail<NT>& mb, int i, int lane, co
                                            bf8 (&sb)[kD / 32], bf8 (&sbl)[kD / 32]) {
 #pragma unroll
   for (int ks = 0; ks < kD / 32; ++ks) {
-    sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
+    if constexpr (split) split_bf8(S[2 * ks], S[2 * ks + 1], sb[ks], sbl[ks]);
+    else sb[ks] = stack_bf8(S[2 * ks], S[2 * ks + 1]);
     mb.sb[i][ks][lane] = sb[ks];
-    if constexpr (split) {
-      const f4 h0 = from_bf4(to_bf4(S[2 * ks])), h1 = from_bf4(to_bf4(S[2 * ks + 1]));
-      sbl[ks] = stack_bf8(S[2 * ks] - h0, S[2 * ks + 1] - h1);
-    }
   }
 }
 
@@ -1032,9 +1058,8 @@ __device__ __forceinline__ void state_update(const PrefillParams& p, f4 (&S)[kD 
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const f4 v0 = egr[2 * ks] * vpr[2 * ks], v1 = egr[2 * ks + 1] * vpr[2 * ks + 1];
-    const bf4 h0 = to_bf4(v0), h1 = to_bf4(v1);
-    vb[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-    if constexpr (split) vbl[ks] = stack_bf8(v0 - from_bf4(h0), v1 - from_bf4(h1));
+    if constexpr (split) split_bf8(v0, v1, vb[ks], vbl[ks]);
+    else vb[ks] = stack_bf8(v0, v1);
   }
   __builtin_amdgcn_sched_barrier(0);
   reload();
@@ -1187,9 +1212,7 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
     const f4 v0 = from_bf4(__builtin_shufflevector(op.v[kb], op.v[kb], 0, 1, 2, 3));
     const f4 v1 = from_bf4(__builtin_shufflevector(op.v[kb], op.v[kb], 4, 5, 6, 7));
     const f4 x0 = v0 - eg[2 * kb] * P[2 * kb], x1 = v1 - eg[2 * kb + 1] * P[2 * kb + 1];
-    const bf4 h0 = to_bf4(x0), h1 = to_bf4(x1);
-    xb[kb] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-    xbl[kb] = stack_bf8(x0 - from_bf4(h0), x1 - from_bf4(h1));
+    split_bf8(x0, x1, xb[kb], xbl[kb]);
   }
   // V' = T' X over the six nonzero blocks, three products each, in an order that keeps
   // consecutive MFMAs on different accumulators
@@ -1378,9 +1401,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
             mt[hh][e] = jt2 <= pt && j <= 16 * pt + fr ? fast_exp(gi - gj[jt2][e]) * acc[i][jt2][e] : 0.0f;
           }
         }
-        const f4 h0 = from_bf4(to_bf4(mt[0])), h1 = from_bf4(to_bf4(mt[1]));
-        op.m[i][kb][0] = stack_bf8(mt[0], mt[1]);
-        op.m[i][kb][1] = stack_bf8(mt[0] - h0, mt[1] - h1);
+        split_bf8(mt[0], mt[1], op.m[i][kb][0], op.m[i][kb][1]);
       }
     }
   }
@@ -1395,9 +1416,7 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
     bf8 vh[2], vl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf4 h0 = to_bf4(vpr[2 * ks]), h1 = to_bf4(vpr[2 * ks + 1]);
-      vh[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-      vl[ks] = stack_bf8(vpr[2 * ks] - from_bf4(h0), vpr[2 * ks + 1] - from_bf4(h1));
+      split_bf8(vpr[2 * ks], vpr[2 * ks + 1], vh[ks], vl[ks]);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
