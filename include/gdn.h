@@ -214,7 +214,8 @@ int gdn_commit(const gdn_commit_args* args);
  * quantized_matmul below 512 rows and dequantizes and multiplies above, model.hpp:137,
  * model.cpp:358-362, in windows of 1024 tokens, session.hpp:136) run on MFMA with the same
  * exact arithmetic at every row count, up to GDN_QLINEAR_MAX_ROWS, and take a workspace of
- * gdn_qlinear_workspace_size() bytes for the operand in MFMA fragment order. */
+ * gdn_qlinear_workspace_size() bytes for the operand in MFMA fragment order and its sums per
+ * row and 64 values. */
 #define GDN_QLINEAR_MAX_SEGS 4
 #define GDN_QLINEAR_GEMV_ROWS 4
 #define GDN_QLINEAR_MAX_ROWS 4096
@@ -256,12 +257,13 @@ int gdn_qlinear_workspace_size(const gdn_qlinear_args* args, size_t* bytes);
  * the reference (MLX allocates inside quantized_matmul): for callers that cannot allocate
  * device memory -- code under HIP graph capture, serving loops and harnesses that forbid
  * hipMalloc. Same arguments, kernels and results as gdn_qlinear, except that `workspace`
- * must be NULL and `workspace_bytes` 0: the MFMA path's operand goes to a scratch array
- * the library holds on each device (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES, kept until the
- * process ends), so calls whose gdn_qlinear_workspace_size() exceeds that are GDN_EINVAL
- * (one layer of up to 512 rows at any k fits; 1024 rows fit for k up to 4096). Every call on a device shares that device's scratch:
- * calls that overlap in time on one device (different streams or threads) race. */
-#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+ * must be NULL and `workspace_bytes` 0: the MFMA path's operand and its group sums go to a
+ * scratch array the library holds on each device (GDN_QLINEAR_NOALLOC_SCRATCH_BYTES, kept
+ * until the process ends), so calls whose gdn_qlinear_workspace_size() exceeds that are
+ * GDN_EINVAL (one layer of up to 512 rows at any k fits; 1024 rows fit for k up to 4096).
+ * Every call on a device shares that device's scratch: calls that overlap in time on one
+ * device (different streams or threads) race. */
+#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)9 << 20)
 int gdn_qlinear_noalloc(const gdn_qlinear_args* args);
 
 /* 1 if the current HIP device is a gfx950 the kernels were built for, else 0. */

@@ -19,10 +19,10 @@
 //
 // More rows (verify blocks, batched decode) run on MFMA (v_mfma_f32_16x16x32_bf16) with the
 // same arithmetic: qprep writes the operand once into the workspace in the MFMA fragment
-// order (the norm prologue applied there, as above), then in qgemm each lane's weight row
-// gives B fragments straight from its nibble words and the operand fragments come from
-// the workspace; per 64-value group acc = sum x (128 + q) and, from a ones operand, sum x,
-// both fp32, then y += s * acc + (b - 128 s) * sum x. A workgroup's 4 waves split K and add
+// order (the norm prologue applied there, as above) together with each row's sum x per
+// 64-value group, then in qgemm each lane's weight row gives B fragments straight from its
+// nibble words and the operand fragments come from the workspace; per group
+// acc = sum x (128 + q) (fp32, MFMA), then y += s * acc + (b - 128 s) * sum x. A workgroup's 4 waves split K and add
 // their partial sums in LDS at the end, so each wave reads a quarter of the operand.
 #include "../../include/gdn.h"
 #include "gdn_device_math.h"
@@ -67,6 +67,9 @@ struct QParams {
   // k = 64 g + 16 g4 + 8 s + (0, 4, 1, 5, 2, 6, 3, 7) (the nibble pair order); rows past M
   // are zeros
   uint16_t* xfrag;
+  // MFMA path: sum x of each 64-value group, fp32, (L, K / 64, 16 mtiles): row-contiguous
+  // per group, so a workgroup's m tiles of one group are one run
+  float* xsum;
   int mtiles;
   int mgroups;  // MFMA path: groups of MT m-tiles (the grid is layers x tiles x mgroups)
   int remap;    // MFMA path: XCD-aware workgroup order (see qgemm_kernel)
@@ -289,6 +292,16 @@ __global__ __launch_bounds__(kThreads) void qprep_kernel(QParams p, int layers) 
   for (int e = 0; e < 4; ++e) q[e] = pack_bf2(v[e], v[e + 4]);
   const int f = 2 * (c / 2) + (j & 1), ln = 16 * (2 * (c & 1) + j / 2) + (mrow & 15);
   *reinterpret_cast<u32x4*>(blk + ((size_t)f * 64 + ln) * 8) = q;
+  // the group's sum x: the 64 values of (row, group c / 2) are the 8 values of each of 8
+  // consecutive threads (pieces c, c + 1 of a group are adjacent: nch is even), added in
+  // a fixed order (each thread's 8 in sequence, then a butterfly over the 8 threads)
+  float sx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sx += v[e];
+  sx += __shfl_xor(sx, 1, 8);
+  sx += __shfl_xor(sx, 2, 8);
+  sx += __shfl_xor(sx, 4, 8);
+  if ((tt & 7) == 0) p.xsum[((size_t)layer * (p.K / 64) + c / 2) * rows + mrow] = sx;
 }
 
 __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
@@ -398,6 +411,8 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
     uint32_t sb[kRows * (kMaxG + 1)];
     f4 red[3][MT * NT][64];
   } sm;
+  // the operand's group sums for this workgroup's MT m tiles, all groups: [group][16 MT]
+  __shared__ __attribute__((aligned(16))) float xs_l[kMaxG * 16 * MT];
   // Workgroup = (layer, weight tile, m group), m groups fastest. Workgroups are dispatched to
   // the 8 XCDs round robin; the ids are renumbered (p.remap) so that each XCD runs a
   // contiguous range: with several m groups, all m groups of a weight tile on one XCD, one
@@ -437,7 +452,6 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
     wr[nt] = (g_u32x2*)(rl.w) + (lane & 3);  // + 4 g: words 8 g + 2 c, +1
   }
   const bf8* xa = reinterpret_cast<const bf8*>(p.xfrag + ((size_t)layer * p.mtiles + mt0) * nch * 512) + lane;
-  const bf8 ones = __builtin_bit_cast(bf8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   const NibbleConsts nk = nibble_consts();
 
   // A ring of kRing slots, one group each (operand fragments and nibble words): slot j
@@ -479,6 +493,12 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
         sm.sb[r * sbs + g + e] = s16 | (b16 << 16);
       }
     }
+    // the group sums: 4 MT float4 per group, contiguous in xsum
+    const float* xsg = p.xsum + (size_t)layer * G * (16 * p.mtiles) + 16 * mt0;
+    for (int q = threadIdx.x; q < 4 * MT * G; q += kThreads) {
+      const int g = q / (4 * MT), o = 4 * (q % (4 * MT));
+      *reinterpret_cast<f4*>(&xs_l[g * 16 * MT + o]) = *reinterpret_cast<const f4*>(xsg + (size_t)g * 16 * p.mtiles + o);
+    }
   }
   __syncthreads();
 
@@ -491,12 +511,9 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   // the wave's i-th group from slot sl, then sl reloaded with its (i + kRing)-th
   auto step = [&](int i, Slot& sl) {
     const int g = 4 * i + wave;
-    f4 xs[MT];
+    f4 xs[MT];  // sum x of the group for this lane's rows 4 g4 .. + 3 of each m tile
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      xs[mt] = mfma(sl.a[mt][0], ones, f4{0.f, 0.f, 0.f, 0.f});
-      xs[mt] = mfma(sl.a[mt][1], ones, xs[mt]);
-    }
+    for (int mt = 0; mt < MT; ++mt) xs[mt] = *reinterpret_cast<const f4*>(&xs_l[g * 16 * MT + 16 * mt + 4 * g4]);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const uint32_t sbv = sm.sb[(16 * nt + nn) * sbs + g];
@@ -623,10 +640,16 @@ hipError_t qlinear_scratch(void** ptr) {
   return hipSuccess;
 }
 
-size_t qlinear_workspace_bytes(int n_layers, int m, int k) {
-  if (qlinear_uses_gemv(m, k)) return 0;
+// the operand in fragment order (1 KB per 16 rows x 32 values), then its group sums (fp32
+// per row and 64 values)
+size_t qlinear_xfrag_bytes(int n_layers, int m, int k) {
   const size_t b = (size_t)n_layers * qgemm_mtiles(m) * (k / 32) * 1024;
   return (b + 255) / 256 * 256;
+}
+size_t qlinear_workspace_bytes(int n_layers, int m, int k) {
+  if (qlinear_uses_gemv(m, k)) return 0;
+  const size_t xs = (size_t)n_layers * 16 * qgemm_mtiles(m) * (k / 64) * 4;
+  return qlinear_xfrag_bytes(n_layers, m, k) + (xs + 255) / 256 * 256;
 }
 
 hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
@@ -665,6 +688,7 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   const int MT = qgemm_mt(a.m);
   p.mtiles = qgemm_mtiles(a.m);
   p.xfrag = static_cast<uint16_t*>(a.workspace);
+  p.xsum = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + qlinear_xfrag_bytes(a.n_layers, a.m, a.k));
   const size_t prep_threads = (size_t)a.n_layers * 16 * p.mtiles * (a.k / 32) * 4;
   const dim3 gp((unsigned)((prep_threads + kThreads - 1) / kThreads));
   if (norm) hipLaunchKernelGGL(qprep_kernel<true>, gp, dim3(kThreads), 0, stream, p, a.n_layers);

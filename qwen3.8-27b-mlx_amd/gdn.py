@@ -52,7 +52,7 @@ def chunked_min_t(B: int) -> int:
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4
 QLINEAR_MAX_ROWS = 4096
-QLINEAR_NOALLOC_SCRATCH_BYTES = 8 << 20
+QLINEAR_NOALLOC_SCRATCH_BYTES = 9 << 20
 
 EXPORTS = ("gdn_run", "gdn_prefill_chunked", "gdn_prefill_chunked_timed", "gdn_prefill_workspace_size", "gdn_commit",
            "gdn_qlinear", "gdn_qlinear_workspace_size", "gdn_qlinear_noalloc", "gdn_available",
@@ -553,8 +553,8 @@ def qlinear(mats, x=None, *, norm=None, n_layers: int = 1, workspace=None, strea
 
 def qlinear_noalloc(mats, x=None, *, norm=None, n_layers: int = 1, stream=None):
     """qlinear through gdn_qlinear_noalloc: no workspace, the library's per-device scratch
-    of 8 MiB instead -- 512 operand rows at any k, 1,024 rows up to k = 4096; larger shapes
-    return GDN_EINVAL (e.g. M = 4096 at K = 5120 needs 40 MiB). Calls overlapping on one
+    of 9 MiB instead -- 512 operand rows at any k, 1,024 rows up to k = 4096; larger shapes
+    return GDN_EINVAL (e.g. M = 4096 at K = 5120 needs 41.25 MiB). Calls overlapping on one
     device race on the scratch. Only the outputs are allocated here; the library call itself
     allocates nothing."""
     args, ys = qlinear_args(mats, x, norm=norm, n_layers=n_layers, stream=stream, alloc_workspace=False)

@@ -302,18 +302,22 @@ def test_qlinear_rejects_bad_arguments(gdn, kw, msg):
 def test_qlinear_workspace_size(gdn):
     """GEMV path (m <= 4 and m k <= 30720): none. MFMA path: the operand in fragment order,
     1 KB per (16-row tile, 32 values), the tile count rounded up to the tiles a workgroup
-    takes (up to 4)."""
+    takes (up to 4), then the operand's fp32 sum per (row, 64 values); both 256-byte
+    aligned."""
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+
+    def ws(tiles, k, layers=1):
+        return al(layers * tiles * (k // 32) * 1024) + al(layers * 16 * tiles * (k // 64) * 4)
     assert gdn.qlinear_workspace_size(4, 5120) == 0
     assert gdn.qlinear_workspace_size(1, 8192) == 0
-    assert gdn.qlinear_workspace_size(4, 8192) == al(1 * (8192 // 32) * 1024)
-    assert gdn.qlinear_workspace_size(5, 5120) == 160 * 1024
-    assert gdn.qlinear_workspace_size(40, 5120) == 3 * 160 * 1024
-    assert gdn.qlinear_workspace_size(40, 6144, n_layers=2) == 2 * 3 * 192 * 1024
-    assert gdn.qlinear_workspace_size(65, 5120) == 8 * 160 * 1024  # 5 tiles -> 2 x 4
-    assert gdn.qlinear_workspace_size(512, 1024) == 32 * 32 * 1024
-    assert gdn.qlinear_workspace_size(1024, 5120) == 64 * 160 * 1024
-    assert gdn.qlinear_workspace_size(4096, 8192) == 256 * 256 * 1024
+    assert gdn.qlinear_workspace_size(4, 8192) == ws(1, 8192)
+    assert gdn.qlinear_workspace_size(5, 5120) == ws(1, 5120)
+    assert gdn.qlinear_workspace_size(40, 5120) == ws(3, 5120) == 3 * 160 * 1024 + 3 * 16 * 80 * 4
+    assert gdn.qlinear_workspace_size(40, 6144, n_layers=2) == ws(3, 6144, 2)
+    assert gdn.qlinear_workspace_size(65, 5120) == ws(8, 5120)  # 5 tiles -> 2 x 4
+    assert gdn.qlinear_workspace_size(512, 1024) == ws(32, 1024)
+    assert gdn.qlinear_workspace_size(1024, 5120) == ws(64, 5120)
+    assert gdn.qlinear_workspace_size(4096, 8192) == ws(256, 8192)
     with pytest.raises(gdn.GdnError):
         gdn.qlinear_workspace_size(4097, 5120)
 
@@ -321,9 +325,9 @@ def test_qlinear_workspace_size(gdn):
 @pytest.mark.parametrize("kw,msg", [
     (dict(m=40, workspace=0x8000000, workspace_bytes=1 << 30), "takes no workspace"),
     (dict(m=4, workspace_bytes=16), "takes no workspace"),
-    (dict(n_layers=2, m=512, k=8192), "more than the 8388608"),
-    (dict(n_layers=48, m=40, k=5120), "more than the 8388608"),
-    (dict(m=1024, k=8192), "more than the 8388608"),
+    (dict(n_layers=2, m=512, k=8192), "more than the 9437184"),
+    (dict(n_layers=48, m=40, k=5120), "more than the 9437184"),
+    (dict(m=1024, k=8192), "more than the 9437184"),
     (dict(m=4097), "bad shape"),
     (dict(x=None), "exactly one"),
 ])
@@ -338,10 +342,14 @@ def test_qlinear_noalloc_rejects_bad_arguments(gdn, kw, msg):
 
 
 def test_qlinear_noalloc_scratch_fits_one_layer(gdn):
-    """One layer at the largest rows and k fits the scratch exactly."""
-    assert gdn.qlinear_workspace_size(512, 8192) == gdn.QLINEAR_NOALLOC_SCRATCH_BYTES
+    """One layer at 512 rows and the largest k (8 MiB of operand, 256 KiB of group sums)
+    fits the scratch, as do 1024 rows up to k = 4096; two layers at 512 rows do not."""
+    assert gdn.qlinear_workspace_size(512, 8192) == (8 << 20) + (256 << 10)
+    assert gdn.qlinear_workspace_size(512, 8192) <= gdn.QLINEAR_NOALLOC_SCRATCH_BYTES
+    assert gdn.qlinear_workspace_size(1024, 4096) <= gdn.QLINEAR_NOALLOC_SCRATCH_BYTES
+    assert gdn.qlinear_workspace_size(512, 8192, n_layers=2) > gdn.QLINEAR_NOALLOC_SCRATCH_BYTES
     text = open(HEADER).read()
-    assert "#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)" in text
+    assert "#define GDN_QLINEAR_NOALLOC_SCRATCH_BYTES ((size_t)9 << 20)" in text
 
 
 def test_length_dispatch_follows_the_measured_crossover(gdn):
