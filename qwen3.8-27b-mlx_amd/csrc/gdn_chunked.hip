@@ -1341,6 +1341,12 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const int fr = lane & 15, lg = lane >> 4;
   if (c > 0) store_tile<NT, OT>(p, tile, b, h, jt, half, c - 1, lane);
+  // Accurate form: every wave starts its step with LDS reads (the state waves their partner's
+  // operand halves, on the chain; these waves K and the mail, ~28 KB each), and the state
+  // waves are the critical ones, so these start ~190 cycles later and leave the LDS to the
+  // exchange first (T = 4096: scan 120 -> 117 us in an A/B run; a longer pause, ~380 cycles,
+  // gained nothing). The fast form's output waves are as busy as its state waves: no pause.
+  if constexpr (PRECISE) __builtin_amdgcn_s_sleep(3);
   tacc ^= op.touch[0] ^ op.touch[1];
   // (e^G, G) per position through this wave's gate row
   float2* grow = sh.gt[NT + half];
