@@ -237,6 +237,31 @@ def qlinear(x_bf16, w_u32, scales_bf16, biases_bf16):
     return y
 
 
+def qlinear_dequant_bf16(x_bf16, w_u32, scales_bf16, biases_bf16, rows: int = 2048):
+    """The reference's Linear at 512 rows and more (cpp/src/model.cpp:358-362, kDequantRows
+    = 512 in cpp/src/model.hpp:137): mx::dequantize to bf16 -- each weight s q + b rounded
+    once to bf16 (MLX evaluates bf16 arithmetic in fp32 and rounds the result) -- then the
+    bf16 matmul, modelled with an fp64 accumulation (MLX's order is not pinned) -> (M, N)
+    fp64, before the output's bf16 rounding. Differs from qlinear by one bf16 rounding of
+    every weight; tests/test_oracle.py pins it where those roundings are exact."""
+    x = from_bf16(np.ascontiguousarray(x_bf16, np.uint16)).astype(np.float64)
+    w = np.ascontiguousarray(w_u32, dtype=np.uint32)
+    s = from_bf16(np.ascontiguousarray(scales_bf16, np.uint16)).astype(np.float64)
+    b = from_bf16(np.ascontiguousarray(biases_bf16, np.uint16)).astype(np.float64)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape == (N, K // 8) and s.shape == (N, K // 64) and b.shape == (N, K // 64)
+    shifts = 4 * np.arange(8, dtype=np.uint32)
+    y = np.empty((M, N), np.float64)
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        q = ((w[r0:r1, :, None] >> shifts) & 0xF).reshape(r1 - r0, K).astype(np.float64)
+        Wd = (q.reshape(r1 - r0, K // 64, 64) * s[r0:r1, :, None] + b[r0:r1, :, None]).reshape(r1 - r0, K)
+        Wb = from_bf16(to_bf16(Wd.astype(np.float32))).astype(np.float64)
+        y[:, r0:r1] = x @ Wb.T
+    return y
+
+
 def qlinear_blocked(x_bf16, w_u32, scales_bf16, biases_bf16, rows: int = 2048):
     """The same product as qlinear for large shapes: W dequantized to fp64 with numpy bit
     ops (value i of a word in nibble i, python/mlp_kernel.py:54-56) a block of rows at a

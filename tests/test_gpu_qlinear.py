@@ -282,6 +282,31 @@ def test_qlinear_in_proj_prefill_window_1024_rows(O, gdn, dev):
         check(to_np(y), O.qlinear_blocked(x[0], w, s, b), bound(O, x[0], s, b), f"segment {i}")
 
 
+def test_qlinear_1024_rows_against_the_dequantize_path(O, gdn, dev):
+    """At 512 rows and more the reference dequantizes each weight to bf16 and multiplies
+    (model.cpp:358-362); this path keeps the exact per-group arithmetic. Measured here on a
+    1024-token in_proj_qkv-shaped block (N reduced to 1024): the kernel's output against the
+    oracle's emulation of the dequantize path (`qlinear_dequant_bf16`), and the emulation's
+    own distance from the exact product -- relative to the output's largest magnitude, and
+    held to the model's 1e-2."""
+    import torch
+    log_case("qlinear M=1024 against the reference's dequantize-then-matmul form, K=5120")
+    M, N, K = 1024, 1024, 5120
+    x, w, s, b = quant_inputs(O, 1, M, N, K, seed=830)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w[0], s[0], b[0])], to_dev(x[0], dev))
+    torch.cuda.synchronize()
+    got = bf16_to_f32(to_np(y)).astype(np.float64)
+    deq = O.qlinear_dequant_bf16(x[0], w[0], s[0], b[0])
+    exact = O.qlinear_blocked(x[0], w[0], s[0], b[0])
+    scale = np.abs(exact).max()
+    d_kernel = np.abs(got - deq).max() / scale
+    d_paths = np.abs(exact - deq).max() / scale
+    d_exact = np.abs(got - exact).max() / scale
+    print(f"  kernel vs dequantize path {d_kernel:.2e}, kernel vs exact {d_exact:.2e}, "
+          f"dequantize path vs exact {d_paths:.2e} (max-abs / max |y|)", flush=True)
+    assert d_kernel < 1e-2 and d_paths < 1e-2
+
+
 def test_qlinear_out_proj_prefill_window_1024_rows(O, gdn, dev):
     """out_proj(GatedRMSNorm(o, z)) over a 1024-token window: K = 6144, N = 5120 (full size),
     the norm applied while the operand goes to the workspace; same tolerance as the M <= 512

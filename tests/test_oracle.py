@@ -411,6 +411,32 @@ def test_qlinear_blocked_equals_qlinear(O):
     assert np.abs(got - ref).max() <= 1e-12 * np.abs(ref).max()
 
 
+def test_qlinear_dequant_bf16_pins(O):
+    """The reference's dequantize-then-matmul form (512 rows and more): where every weight
+    s q + b is exact in bf16 (scales a power of two, biases on a coarse grid) it equals the
+    exact product; with scales that are not, it differs from it by exactly the bf16 rounding
+    of each weight (checked against weights rounded independently here), and the difference
+    is a small fraction of the output."""
+    x, w, s, b = _qlin_inputs(O, 3, 40, 256, 7)
+    s_exact = O.to_bf16(np.full(s.shape, 0.25, np.float32))
+    b_exact = O.to_bf16(np.round(O.from_bf16(b) * 4) / 4)
+    ref = O.qlinear(x, w, s_exact, b_exact)
+    assert np.abs(O.qlinear_dequant_bf16(x, w, s_exact, b_exact, rows=100) - ref).max() <= 1e-12 * np.abs(ref).max()
+    # general scales: the weights rounded to bf16 one by one (round to nearest even on the
+    # fp32 value, as torch rounds), then an fp64 product
+    q = _unpack_np(w)
+    Wd = (q * np.repeat(O.from_bf16(s).astype(np.float64), 64, axis=1)
+          + np.repeat(O.from_bf16(b).astype(np.float64), 64, axis=1))
+    import torch
+    Wb = torch.from_numpy(Wd.astype(np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+    want = O.from_bf16(x).astype(np.float64) @ Wb.T
+    got = O.qlinear_dequant_bf16(x, w, s, b, rows=100)
+    assert np.abs(got - want).max() <= 1e-12 * np.abs(want).max()
+    exact = O.qlinear(x, w, s, b)
+    gap = np.abs(got - exact).max() / np.abs(exact).max()
+    assert 0 < gap < 2 ** -7
+
+
 def test_qlinear_nibble_order_known_answers(O):
     """A single nonzero nibble at value position i of word j selects x[8j + i]; scale 1,
     bias 0; an all-zero w with bias b gives b * sum(x) per group."""
