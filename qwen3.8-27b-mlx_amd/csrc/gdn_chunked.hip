@@ -10,33 +10,41 @@
 //   y  = e^G . (Q S) + M V'                              (= MU0 + Qeff S)
 //   S  = e^{G_63} S + K^T (e^{G_63 - G} . V')
 //
+// GDN_PREFILL_FAST runs exactly this. GDN_PREFILL_ACCURATE forms the same V' as
+//   V' = T' (V - e^G . (K S))                            (= U - W S)
+// with the state products at fp32 accuracy (below), so W and U are never formed.
+//
 // Three kernels, one stream:
 //   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position into bf16 q, k
-//                  (B, T, Hk, 128) and v, which goes straight into the fragment order of
-//                  U's B operand (with q, k, v given by the caller, prefill_vfrag reorders
-//                  v instead). Extra workgroups of the same launch compute the gates and
-//                  each chunk's cumulative log decay G (one wave per (v-head, chunk)).
+//                  (B, T, Hk, 128) and v, which goes straight into B-operand fragments in
+//                  the interleaved k order (with q, k, v given by the caller,
+//                  prefill_vfrag reorders v instead). Extra workgroups of the same launch
+//                  compute the gates and each chunk's cumulative log decay G (one wave per
+//                  (v-head, chunk)).
 //   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
-//                  per CU: K K^T and K Q^T on bf16 MFMA, and for the k-head's v-heads
-//                  A and M, T = (I + A)^-1 (one wave per v-head, fp32, left in LDS),
-//                  U = T'V and W = T'diag(e^G)K on bf16 MFMA, every wave building its T'
-//                  fragments from T in LDS (T' split into bf16 hi + lo for U). Results go
-//                  to the workspace, already in the register order of the MFMA operands
-//                  that read them; U as fp16 scaled by a power of two per 16-position tile.
+//                  per CU: K K^T (and, fast form, K Q^T) on bf16 MFMA, and for the
+//                  k-head's v-heads A (and M), T = (I + A)^-1 (one wave per v-head, fp32,
+//                  left in LDS), then each wave's T' fragments from T in LDS: stored split
+//                  into bf16 hi + lo (accurate form, with K), or used for U = T'V and
+//                  W = T'diag(e^G)K on bf16 MFMA (fast form; U stored as fp16 scaled by a
+//                  power of two per 16-position tile). Results go to the workspace, already
+//                  in the register order of the MFMA operands that read them.
 //   prefill_scan   one workgroup per (batch, v-head, pair of 16-column Dv tiles), serial
 //                  over the chunks. Each of two state waves keeps its tile's fp32 state
-//                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain V' = U - W S,
-//                  S = e^G63 S + K^T V'' with every operand in registers; two output waves
-//                  (position tiles {0, 3} and {1, 2} of a chunk) run one chunk behind on the S and
-//                  V' that the state waves leave in a double-buffered LDS mailbox: one
-//                  barrier per chunk. Operands go from the workspace straight into
-//                  registers two chunks ahead of their use, and the output waves touch the
-//                  lines of the chunk four ahead so that they are in L2 when first asked
-//                  for. W S, Q S and K^T V'' use bf16 operands; M V' splits both operands
-//                  into bf16 hi + lo (three MFMAs). With GDN_PREFILL_ACCURATE, U stays fp32,
-//                  W is stored with its bf16 remainder and W S takes S split as well (three
-//                  MFMAs), and V'' is split into bf16 hi + lo for K^T V'' (two MFMAs): the
-//                  state then follows the fp32 recurrence to about 1e-6 instead of 2e-3.
+//                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain (fast: V' =
+//                  U - W S; accurate: K S, X = V - e^G K S, V' = T' X), S = e^G63 S +
+//                  K^T V'' with every operand in registers; two output waves (position
+//                  tiles {0, 3} and {1, 2} of a chunk) run one chunk behind on the S and V'
+//                  that the state waves leave in a double-buffered LDS mailbox: one barrier
+//                  per chunk. Operands go from the workspace straight into registers two
+//                  chunks ahead of their use, and the output waves touch the lines of the
+//                  chunk four ahead so that they are in L2 when first asked for. Fast form:
+//                  W S, Q S and K^T V'' use bf16 operands, M V' splits both operands into
+//                  bf16 hi + lo (three MFMAs), and M comes from the intra kernel. Accurate
+//                  form: S is split into bf16 hi + lo for K S (K is exact in bf16), X and T'
+//                  for T' X (three MFMAs), V'' for K^T V'' (two MFMAs), so that the state
+//                  follows the fp32 recurrence to about 1e-5 instead of 2e-3, and the
+//                  output waves build M from the chunk's K and Q.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
@@ -49,7 +57,7 @@
 // along k (rows 0..15 and 16..31 of a 32-row k block) give lane l the rows 4(l/16)+i and
 // 16+4(l/16)+i, i < 4, of column l%16 -- eight values of the B fragment when the k block
 // is read in the order k' = 8g + i <-> k = (i < 4 ? 4g + i : 16 + 4g + i - 4), g = l/16.
-// The A operands of those products (W and Q over dk, K^T and M over positions) are stored
+// The A operands of those products (W, K and Q over dk, K^T, T' and M over positions) are stored
 // in fragment order with their k blocks in that same order, so an accumulator tile turns
 // into a B fragment with two conversions and no data movement between lanes.
 #include <type_traits>
