@@ -86,31 +86,35 @@ def test_prefill_continues_from_state_and_conv_state(O, gdn, dev, T, precision):
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
-def test_prefill_qkv_precomputed_gates_equal_heads(O, gdn, dev):
-    """qkv front end (bf16), alpha/beta given (delta::run's form), Hk = Hv = 8."""
-    log_case("prefill qkv precomputed gates Hk=Hv=8 T=150")
+@pytest.mark.parametrize("precision", [ACC, FAST], ids=["accurate", "fast"])
+def test_prefill_qkv_precomputed_gates_equal_heads(O, gdn, dev, precision):
+    """qkv front end (bf16: v reordered by prefill_vfrag), alpha/beta given (delta::run's
+    form), Hk = Hv = 8, a last chunk of 22 positions."""
+    log_case(f"prefill qkv precomputed gates Hk=Hv=8 T=150, precision {precision}")
     inp = O.make_inputs(config=4, layer=7, B=1, L=150, Hk=8, Hv=8, state_std=0.1)
     al = O.uniform(77, (1, 150, 8), 0.85, 1.0)
     be = O.uniform(78, (1, 150, 8), 0.0, 1.0)
     q, k, v = O.from_bf16(inp.q), O.from_bf16(inp.k), O.from_bf16(inp.v)
     ro, rS = O.recurrent(q, k, v, al, be, inp.state)
-    o, S, _ = run_prefill(gdn, dev, inp, Hk=8, o_dtype="f32", precomputed=(al, be))
+    o, S, _ = run_prefill(gdn, dev, inp, Hk=8, o_dtype="f32", precomputed=(al, be), precision=precision)
     check(O, o, ro, "o")
-    check(O, S, rS, "state", STATE_TOL)
+    check(O, S, rS, "state", STATE_TOL_ACC if precision == ACC else STATE_TOL)
 
 
 @pytest.mark.parametrize("Hk,Hv", [(8, 16), (4, 16), (2, 12), (4, 20)])
-def test_prefill_other_head_ratios(O, gdn, dev, Hk, Hv):
+@pytest.mark.parametrize("precision", [ACC, FAST], ids=["accurate", "fast"])
+def test_prefill_other_head_ratios(O, gdn, dev, Hk, Hv, precision):
     """Other sizes of the family: two v-heads per k-head (one group of two), four (groups of
     three and one: the intra kernel's general form), six (two full groups) and five (three
-    and two); conv front end, carried state and conv state, ragged last chunk."""
-    log_case(f"prefill conv Hk={Hk} Hv={Hv} T=150 B=1 with state")
+    and two); conv front end, carried state and conv state, ragged last chunk; both
+    precisions."""
+    log_case(f"prefill conv Hk={Hk} Hv={Hv} T=150 B=1 with state, precision {precision}")
     inp = O.make_inputs(config=4, layer=100 * Hk + Hv, B=1, L=150, Hk=Hk, Hv=Hv, conv=True,
                         state_std=0.05)
     ref = O.reference_layer(inp)
-    o, S, conv = run_prefill(gdn, dev, inp, Hk=Hk, o_dtype="f32")
+    o, S, conv = run_prefill(gdn, dev, inp, Hk=Hk, o_dtype="f32", precision=precision)
     check(O, o, ref["o"], "o")
-    check(O, S, ref["state"], "state", STATE_TOL)
+    check(O, S, ref["state"], "state", STATE_TOL_ACC if precision == ACC else STATE_TOL)
     assert np.array_equal(conv, ref["xp"][:, -3:])
 
 
