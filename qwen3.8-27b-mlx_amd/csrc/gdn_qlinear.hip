@@ -22,8 +22,11 @@
 // order (the norm prologue applied there, as above) together with each row's sum x per
 // 64-value group, then in qgemm each lane's weight row gives B fragments straight from its
 // nibble words and the operand fragments come from the workspace; per group
-// acc = sum x (128 + q) (fp32, MFMA), then y += s * acc + (b - 128 s) * sum x. A workgroup's 4 waves split K and add
-// their partial sums in LDS at the end, so each wave reads a quarter of the operand.
+// acc = sum x (128 + q) (fp32, MFMA), then y += s * acc + (b - 128 s) * sum x. In qgemm a
+// workgroup's 4 waves split K and add their partial sums in LDS at the end, so each wave
+// reads a quarter of the operand; calls of many weight rows and one m group (up to 64 rows,
+// e.g. 8 layers of in_proj at once) take qgemm_ns instead, whose workgroup of 256 weight rows
+// reads the operand into LDS once for its four waves.
 #include "../../include/gdn.h"
 #include "gdn_device_math.h"
 #include "gdn_internal.h"
@@ -565,6 +568,201 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   }
 }
 
+// MFMA path for calls of many weight rows and few operand rows (one m group, up to 64 rows;
+// 8 layers or more per call): workgroup = 256 weight rows, wave w owns 64 of them (kNsTiles
+// 16-row tiles) over the whole of K, and the four waves share the operand, which passes
+// through an LDS ring once per workgroup (qgemm_kernel reads it from L2 once per 64 rows).
+// A step is two groups. Direct-to-LDS loads (`global_load_lds_dwordx4`: lane l's 16 bytes
+// land at the destination + 16 l, no VGPRs) fill the ring kNsAhead steps ahead: each wave
+// issues one of the step's four 1 KB blocks of every m tile and a quarter of the two
+// groups' sums x, waits for its own loads, and one barrier per step then makes the slot
+// whole for all four. Each wave also loads the scale and bias words of its rows, 8 groups
+// at a time, into its own pair of LDS buffers (read by that wave only: no barrier). The
+// weight words stay in a register ring, loaded and moved into fragment order as in
+// qgemm_kernel. Loads complete in issue order and the waits count them, so every step issues
+// the same loads (past the last step they repeat it). Arithmetic per group as in
+// qgemm_kernel; each wave adds its groups in order and rounds its rows once.
+constexpr int kNsTiles = 4;
+constexpr int kNsRows = 4 * 16 * kNsTiles;  // weight rows per workgroup
+constexpr int kNsAhead = 2;                 // steps between a load and its use
+typedef __attribute__((address_space(3))) void lds_void;
+// Direct-to-LDS loads written as asm: the compiler, which cannot tell which LDS bytes such a
+// load writes, otherwise waits for every one in flight before each later LDS access and
+// each later such load (vmcnt(0)), which would undo the ring. The asm statements have a
+// memory clobber (no memory access moves across them); the kernel waits for them itself.
+// M0 holds the LDS destination; nothing else in the kernel uses M0.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+
+template <int MT>
+__global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
+  constexpr int NT = kNsTiles, D = kNsAhead, S = D + 1;
+  constexpr int kOp = MT * 4 * 1024;       // a slot's operand: [m tile][group of the step][k step] 1 KB blocks
+  constexpr int kXs = 2 * 64 * 4;          // then the two groups' sums x: [group][64] fp32 (16 MT used)
+  constexpr int kSlot = kOp + kXs;
+  constexpr int kPerStep = MT + 1 + 2 * NT;  // vector-memory instructions per wave and step
+  __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
+  __shared__ __attribute__((aligned(16))) uint16_t sbl[4][2][2][64 * 8];  // [wave][buffer][s, b][row][8 groups]
+
+  int bid = blockIdx.x;
+  if (p.remap) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
+  const int layer = bid / p.tiles, tile = bid % p.tiles;
+  const int lane = threadIdx.x & 63, g4 = lane >> 4, nn = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = p.K, G = K / 64, nch = K / 32, nsteps = G / 2, nblk = G / 8;
+  const int rbase = (tile * 4 + wave) * 16 * NT;
+  const int bsrc = (4 * nn + g4) * 4;  // as in qgemm_kernel
+  g_u32x2* wr[NT];
+  uint16_t* yr[NT];
+  int ystride[NT];
+  bool valid[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int grow = rbase + 16 * nt + nn;
+    valid[nt] = grow < p.R;
+    const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
+    yr[nt] = rp.y;
+    ystride[nt] = rp.ystride;
+    const int lrow = rbase + 16 * nt + (lane >> 2);
+    const RowPtrs rl = row_ptrs(p, layer, lrow < p.R ? lrow : p.R - 1);
+    wr[nt] = (g_u32x2*)(rl.w) + (lane & 3);
+  }
+  // lane l loads the scale and bias words of the wave's row l
+  const RowPtrs rsb = row_ptrs(p, layer, min(rbase + lane, p.R - 1));
+  const char* s_src = reinterpret_cast<const char*>(rsb.s);
+  const char* b_src = reinterpret_cast<const char*>(rsb.b);
+  const char* xa = reinterpret_cast<const char*>(p.xfrag + (size_t)layer * MT * nch * 512) + 16 * lane;
+  // lane l of wave w loads sum l of group 2 j + w % 2 (lanes past 16 MT repeat the last one:
+  // waves w and w + 2 write the same bytes, so every wave issues the same loads and no lane
+  // is masked off -- divergent code here would split the loop into blocks)
+  const char* xsrc = reinterpret_cast<const char*>(p.xsum + (size_t)layer * G * 16 * MT) + 4 * (16 * MT * (wave & 1) + min(lane, 16 * MT - 1));
+  const NibbleConsts nk = nibble_consts();
+
+  // step j's loads: the wave's block (group 2 j + wave / 2, k step wave % 2) of every m tile
+  // and its share of the sums into ring slot sl; its weight words into ws
+  const uint32_t ring_l = lds_addr(ring);
+  auto issue_op = [&](int j, int sl) {
+    const uint32_t dst = ring_l + sl * kSlot;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) dma16(xa + ((size_t)i * nch + 4 * j + wave) * 1024, dst + (4 * i + wave) * 1024);
+    dma4(xsrc + (size_t)j * 2 * 16 * MT * 4, dst + kOp + 256 * (wave & 1));
+  };
+  struct WStep {
+    u32x2 w[2][NT];
+  };
+  auto issue_w = [&](int j, WStep& ws) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      g_u32x2* wj = wr[nt] + 8 * j;
+      ws.w[0][nt] = wj[0];
+      ws.w[1][nt] = wj[4];
+    }
+  };
+  // scale and bias words of groups 8 blk .. + 7 into buffer buf
+  const uint32_t sbl_l = lds_addr(&sbl[wave][0][0][0]);
+  auto issue_sb = [&](int blk, int buf) {
+    dma16(s_src + 16 * blk, sbl_l + buf * 2048);
+    dma16(b_src + 16 * blk, sbl_l + buf * 2048 + 1024);
+  };
+
+  f4 y[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int j, const unsigned char* slot, const uint16_t* sbw, const WStep& ws) {
+    // the scale and bias words of the step's two groups, one 4-byte read each per tile
+    uint32_t sw[NT], bw[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int o = (16 * nt + nn) * 8 + ((2 * j) & 7);
+      sw[nt] = *reinterpret_cast<const uint32_t*>(sbw + o);
+      bw[nt] = *reinterpret_cast<const uint32_t*>(sbw + 64 * 8 + o);
+    }
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      bf8 a[MT][2];
+      f4 xs[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) a[mt][s] = *reinterpret_cast<const bf8*>(slot + (4 * mt + 2 * gg + s) * 1024 + 16 * lane);
+        xs[mt] = *reinterpret_cast<const f4*>(slot + kOp + 256 * gg + 4 * (16 * mt + 4 * g4));
+      }
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float sc = __builtin_bit_cast(float, gg ? sw[nt] & 0xFFFF0000u : sw[nt] << 16);
+        const float off = __builtin_bit_cast(float, gg ? bw[nt] & 0xFFFF0000u : bw[nt] << 16) - 128.0f * sc;
+        const uint32_t w0 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)ws.w[gg][nt][0]);
+        const uint32_t w1 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)ws.w[gg][nt][1]);
+        const bf8 b0 = nibbles_bf16(w0, nk), b1 = nibbles_bf16(w1, nk);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          f4 acc = mfma(a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
+          acc = mfma(a[mt][1], b1, acc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // a group's products and sums stay together
+    }
+  };
+
+  WStep W[2];
+  issue_sb(0, 0);
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    issue_op(j, j);
+    issue_w(j, W[j]);
+  }
+  int sl = 0;  // ring slot of step j
+  for (int j0 = 0; j0 < nsteps; j0 += 4) {  // nsteps is a multiple of 4 (G of 8)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = j0 + r;
+      // step j's loads are done once no more than the loads issued after them are in flight:
+      // step j + 1's, and also the scale and bias pair issued at step 4 b after step
+      // 4 b + 2's (in flight at steps 4 b + 1 and 4 b + 2); then every wave's are (the
+      // barrier). The wait and the barrier are one asm statement with a memory clobber, so no
+      // load moves across them.
+      if (r == 1 || r == 2)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep + 2) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep) : "memory");
+      compute(j, ring + sl * kSlot, &sbl[wave][(j >> 2) & 1][0][0], W[r & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      // refill what step j - 1 read (every wave is past it: the barrier above)
+      const int jn = min(j + D, nsteps - 1);
+      issue_op(jn, sl == 0 ? S - 1 : sl - 1);
+      issue_w(jn, W[r & 1]);
+      if (r == 0) issue_sb(min((j >> 2) + 1, nblk - 1), ((j >> 2) + 1) & 1);
+      sl = sl == S - 1 ? 0 : sl + 1;
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated loads, before the LDS goes away
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (valid[nt]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = mt * 16 + 4 * g4 + i;
+          if (m < p.M) yr[nt][(size_t)m * ystride[nt]] = f2bf(y[mt][nt][i]);
+        }
+      }
+    }
+}
+
 template <bool NORM>
 hipError_t launch_j(int J, const QParams& p, dim3 grid, size_t smem, hipStream_t stream) {
   switch (J) {
@@ -695,8 +893,29 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
   else hipLaunchKernelGGL(qprep_kernel<false>, gp, dim3(kThreads), 0, stream, p, a.n_layers);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // weight rows per workgroup: 64, 32 or 16 -- the most that still gives 512 workgroups
   const int gy = p.mtiles / MT;
+  // one m group and enough 256-row workgroups for two per CU: the operand-sharing kernel
+  // (its scale and bias loads take 16 bytes a lane)
+  bool sb16 = true;
+  for (int q = 0; q < a.n_segs; ++q)
+    sb16 = sb16 && reinterpret_cast<uintptr_t>(a.segs[q].scales) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.segs[q].biases) % 16 == 0;
+  const int ns_tiles = (R + kNsRows - 1) / kNsRows;
+  if (gy == 1 && sb16 && (size_t)a.n_layers * ns_tiles >= 512) {
+    p.tiles = ns_tiles;
+    p.mgroups = 1;
+    const size_t nwg = (size_t)a.n_layers * ns_tiles;
+    p.remap = a.n_layers >= 8 && nwg % 8 == 0;
+    const dim3 grid((unsigned)nwg);
+    switch (MT) {
+      case 1: hipLaunchKernelGGL(qgemm_ns_kernel<1>, grid, dim3(kThreads), 0, stream, p); break;
+      case 2: hipLaunchKernelGGL(qgemm_ns_kernel<2>, grid, dim3(kThreads), 0, stream, p); break;
+      case 3: hipLaunchKernelGGL(qgemm_ns_kernel<3>, grid, dim3(kThreads), 0, stream, p); break;
+      default: hipLaunchKernelGGL(qgemm_ns_kernel<4>, grid, dim3(kThreads), 0, stream, p); break;
+    }
+    return hipGetLastError();
+  }
+  // weight rows per workgroup: 64, 32 or 16 -- the most that still gives 512 workgroups
   int NT = 4;
   while (NT > 1 && (size_t)a.n_layers * ((R + 16 * NT - 1) / (16 * NT)) * gy < 512) NT /= 2;
   p.tiles = (R + 16 * NT - 1) / (16 * NT);

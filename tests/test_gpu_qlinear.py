@@ -247,6 +247,71 @@ def test_qlinear_mfma_eight_layers_whole_layers_per_xcd(O, gdn, dev, M, nseg):
             check(got[l], O.qlinear(x[l], w[l], s[l], b[l]), bound(O, x[l], s[l], b[l]), f"segment {i} layer {l}")
 
 
+# ---- 256 weight rows per workgroup, the operand shared by its four waves through LDS ----
+# One m group (M <= 64) and n_layers * ceil(R / 256) >= 512 select qgemm_ns_kernel: e.g.
+# 8 layers of in_proj (65 workgroups a layer) or 26 of out_proj (20 a layer).
+
+def sampled_rows(N, rng, n=768):
+    """The first and last 256 rows and n - 512 others: every workgroup boundary case plus a
+    spread, so the fp64 check stays short at K = 5120."""
+    mid = rng.choice(np.arange(256, N - 256), size=n - 512, replace=False)
+    return np.sort(np.concatenate([np.arange(256), np.arange(N - 256, N), mid]))
+
+
+@pytest.mark.parametrize("M,K", [(5, 1024), (17, 1024), (40, 1024), (64, 1024), (40, 5120)])
+def test_qlinear_mfma_in_proj_rows_shared_operand(O, gdn, dev, M, K):
+    """8 layers of the in_proj row count (16,480 rows in its four matrices: segment bounds
+    inside workgroups, the last workgroup partly past the rows), 520 workgroups of 256 rows,
+    M from one to four m tiles; K = 1024 (8 steps of two groups, both scale and bias
+    buffers, the repeated loads of the last steps) and K = 5120 (40 steps). At K = 5120 a
+    sample of rows of every layer and segment is checked."""
+    import torch
+    log_case(f"qlinear (MFMA path, 256-row workgroups) in_proj 4 segments x 8 layers, M={M}, K={K}")
+    L, nseg = 8, [10240, 6144, 48, 48]
+    rng = np.random.default_rng(1500 + M + K)
+    mats, host, x = [], [], None
+    for i, n in enumerate(nseg):
+        xi, w, s, b = quant_inputs(O, L, M, n, K, seed=1500 + 10 * M + K + i)
+        x = xi if x is None else x
+        mats.append(dev_mat(gdn, dev, w, s, b))
+        host.append((w, s, b))
+    ys = gdn.qlinear(mats, to_dev(x, dev), n_layers=L)
+    torch.cuda.synchronize()
+    for i, ((w, s, b), y) in enumerate(zip(host, ys)):
+        got = to_np(y)
+        n = w.shape[1]
+        rows = sampled_rows(n, rng) if K > 1024 and n > 1024 else np.arange(n)
+        for l in range(L):
+            ws_, ss, bs = w[l][rows], s[l][rows], b[l][rows]
+            check(got[l][:, rows], O.qlinear_blocked(x[l], ws_, ss, bs), bound(O, x[l], ss, bs),
+                  f"segment {i} layer {l}")
+
+
+def test_qlinear_mfma_out_proj_rows_shared_operand(O, gdn, dev):
+    """out_proj(GatedRMSNorm(o, z)) over 26 layers (5,120 rows: 20 workgroups of 256 a
+    layer, 520 in all), M = 40, K = 1024: the norm applied in the preparation kernel, the
+    product in the operand-sharing kernel."""
+    import torch
+    log_case("qlinear (MFMA path, 256-row workgroups) out_proj with GatedRMSNorm x 26 layers, M=40, K=1024")
+    L, M, K, N = 26, 40, 1024, 5120
+    rng = np.random.default_rng(1600)
+    o = (rng.standard_normal((L, M, K)) * 0.3).astype(np.float32)
+    z = O.to_bf16(rng.standard_normal((L, M, K)).astype(np.float32))
+    gamma = rng.uniform(0.5, 1.5, (L, 128)).astype(np.float32)
+    _, w, s, b = quant_inputs(O, L, M, N, K, seed=1601)
+    (y,) = gdn.qlinear([dev_mat(gdn, dev, w, s, b)],
+                       norm=(to_dev(o, dev), to_dev(z, dev), to_dev(gamma, dev), 1e-6), n_layers=L)
+    torch.cuda.synchronize()
+    got = to_np(y)
+    for l in range(L):
+        xn = O.gated_rmsnorm(o[l].reshape(M * (K // 128), 128), z[l].reshape(M * (K // 128), 128),
+                             gamma[l], 1e-6).reshape(M, K)
+        ref = O.qlinear_blocked(xn, w[l], s[l], b[l])
+        W = (np.abs(np.repeat(bf16_to_f32(s[l]), 64, axis=1)) * 15 + np.abs(np.repeat(bf16_to_f32(b[l]), 64, axis=1)))
+        flip = 3 * 2.0 ** -8 * (np.abs(bf16_to_f32(xn)).max(axis=1, keepdims=True) * W.max(axis=1)[None, :])
+        check(got[l], ref, bound(O, xn, s[l], b[l]) + flip, f"layer {l}")
+
+
 def test_qlinear_mfma_512_rows(O, gdn, dev):
     """The most rows the quantized path takes (512 = 32 m-tiles in 8 groups of 4), N = 4096:
     64 tiles of 64 rows x 8 = 512 workgroups, so the 64-row form with 4 m-tiles runs."""
