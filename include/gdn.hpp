@@ -45,12 +45,13 @@ inline bool available() { return gdn_available() != 0; }
 
 // Blocks of B sequences that are not recorded and carry at least chunked_min_t(B) tokens run
 // the chunked form (gdn_prefill_chunked), shorter ones the recurrent kernel: the two meet near
-// T = 44, 34, 30 and 28 for B = 1, 2, 4 and 8 on MI355X (one layer, conv front end): 44 for one
-// sequence, 38 - 2 B for two to four, kChunkedMinT from five on. The reference chooses by
-// length the same way (python/qwen35.py:338, 606-626).
+// T = 36, 32, 30 and 32 for B = 1, 2, 4 and 8 on MI355X (one layer, conv front end, the
+// accurate chunked precision). The reference chooses by length the same way
+// (python/qwen35.py:338, 606-626).
 constexpr int kChunkedMinT = 28;
 constexpr int chunked_min_t(int B) {
-  return B == 1 ? 44 : (38 - 2 * B > kChunkedMinT ? 38 - 2 * B : kChunkedMinT);
+  const int t = B == 1 ? 36 : B == 2 ? 32 : B == 3 ? 31 : B == 4 ? 30 : 32;
+  return t > kChunkedMinT ? t : kChunkedMinT;
 }
 
 // delta::run (delta.hpp:66-68) on device buffers: q, k (B,L,H,128), v (B,L,H,128), alpha,

@@ -33,21 +33,22 @@ HEAD_DIM = 128
 CONV_TAPS = 4
 
 # Calls that do not record and carry at least chunked_min_t(B) tokens run the chunked form
-# (gdn_prefill_chunked); shorter ones the recurrent kernel (gdn_run), serial in T. Measured on
-# MI355X with one layer and the conv front end (bench.py --only crossover): the chunked form
-# takes 31 / 38 / 45 / 61 us at B = 1 / 2 / 4 / 8 (66 us at B = 8 from T = 36); the recurrent
-# kernel 28.1 / 31.2 / 32.7 us at B = 1 and T = 40 / 44 / 48, 34.8 / 39.7 us at B = 2 and
-# T = 32 / 36, 43.8 / 47.6 us at B = 4 and T = 28 / 32, 61.3 / 66.8 us at B = 8 and T = 28 / 32.
-# The forms meet near T = 44, 34, 30 and 28 for B = 1, 2, 4 and 8: 44 for one sequence,
-# 38 - 2 B for two to four, CHUNKED_MIN_T from five on. Module-level so that tests can force
-# either form, as the reference's CHUNK_THRESHOLD (python/qwen35.py:338, 606-626), which makes
-# the same choice by length.
+# (gdn_prefill_chunked, the accurate precision); shorter ones the recurrent kernel (gdn_run),
+# serial in T. Measured on MI355X with one layer and the conv front end (bench.py's
+# crossover: recurrent against chunked, T = 24 .. 96): the chunked form takes 26.2-26.7 /
+# 33.5-34.4 / 42.6-43.9 / 63.5-68.6 us at B = 1 / 2 / 4 / 8 up to T = 64; the recurrent kernel
+# 23.2 / 26.4 / 27.6 us at B = 1 and T = 32 / 36 / 40, 32.2 / 33.8 / 38.8 us at B = 2 and
+# T = 28 / 32 / 36, 42.7 / 46.5 us at B = 4 and T = 28 / 32, 59.3 / 64.8 / 74.1 us at B = 8
+# and T = 28 / 32 / 36. The forms meet near T = 36, 32, 30 and 32 for B = 1, 2, 4 and 8.
+# Module-level so that tests can force either form, as the reference's CHUNK_THRESHOLD
+# (python/qwen35.py:338, 606-626), which makes the same choice by length.
 CHUNKED_MIN_T = 28
+_CHUNKED_MIN_T_BY_B = {1: 36, 2: 32, 3: 31, 4: 30}
 
 
 def chunked_min_t(B: int) -> int:
     """Fewest tokens of a non-recording call of B sequences that run on the chunked form."""
-    return max(CHUNKED_MIN_T, 44 if B == 1 else 38 - 2 * B)
+    return max(CHUNKED_MIN_T, _CHUNKED_MIN_T_BY_B.get(B, 32))
 
 QLINEAR_MAX_SEGS = 4
 QLINEAR_GEMV_ROWS = 4

@@ -353,13 +353,13 @@ def test_qlinear_noalloc_scratch_fits_one_layer(gdn):
 
 
 def test_length_dispatch_follows_the_measured_crossover(gdn):
-    """A non-recording call runs the chunked form from the measured crossover on (about 44,
-    34, 30, 28 tokens for 1, 2, 4, 8 sequences; 28 from 5 on), shorter ones and recording
+    """A non-recording call runs the chunked form from the measured crossover on (about 36,
+    32, 30, 32 tokens for 1, 2, 4, 8 sequences; 32 from 5 on), shorter ones and recording
     ones the recurrent kernel (python/qwen35.py:606-626 chooses by length the same way)."""
     import torch
     x = torch.zeros(64, dtype=torch.bfloat16)  # 16-byte aligned host buffer: the choice only reads its address
     use = gdn.gdn._use_chunked
-    for B, first in ((1, 44), (2, 34), (3, 32), (4, 30), (5, 28), (8, 28), (64, 28)):
+    for B, first in ((1, 36), (2, 32), (3, 31), (4, 30), (5, 32), (8, 32), (64, 32)):
         assert gdn.chunked_min_t(B) == first
         assert not use(B, first - 1, False, x, None, (x,))
         assert use(B, first, False, x, None, (x,))

@@ -19,9 +19,9 @@ pytestmark = pytest.mark.gpu
 
 PREFILL_TOL = 1e-2
 STATE_TOL = 5e-3
-# GDN_PREFILL_ACCURATE (the state products at fp32 accuracy: U in fp32, W and S split into
-# bf16 hi + lo in W S, V'' split in K^T V''): measured 3e-6 to 8e-6 at every tested length,
-# carried state and gate regime
+# GDN_PREFILL_ACCURATE (V' = T' (V - e^G K S) with S, X = V - e^G K S, T' and V'' split into
+# bf16 hi + lo: the state products at fp32 accuracy): measured 3e-6 to 8e-6 at every tested
+# length, carried state and gate regime
 STATE_TOL_ACC = 2e-5
 D = 128
 
