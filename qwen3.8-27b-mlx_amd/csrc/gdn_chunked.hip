@@ -74,6 +74,7 @@ typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kC = 64;             // chunk
 constexpr int kPadB = 8;           // bf16 padding per LDS row
@@ -95,6 +96,16 @@ __device__ __forceinline__ bf8 frag(const __bf16 (*m)[LD], int row, int k) {
 
 __device__ __forceinline__ bf4 to_bf4(f4 v) { return __builtin_convertvector(v, bf4); }
 __device__ __forceinline__ f4 from_bf4(bf4 v) { return __builtin_convertvector(v, f4); }
+// Four fp32 values that already hold bf16 values (low 16 bits zero) as bf16: their high
+// halves, two per v_perm_b32 -- the conversion instruction would round them again (2.4
+// issue slots a pair, against 1). The elements are copied to scalars first: this compiler
+// folds __builtin_bit_cast of an element of a vector value into a cast of element 0.
+__device__ __forceinline__ bf4 bf4_of_rounded(f4 v) {
+  const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+  const uint32_t lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, v1), __builtin_bit_cast(uint32_t, v0), 0x07060302u);
+  const uint32_t hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, v3), __builtin_bit_cast(uint32_t, v2), 0x07060302u);
+  return __builtin_bit_cast(bf4, (u32x2){lo, hi});
+}
 
 // Two accumulator tiles (k rows 0..15 and 16..31 of a block) as one B fragment in the
 // interleaved k order.
@@ -367,6 +378,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (is_q) dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
   else if (norm) dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
   const size_t pstride = (size_t)p.Hk * kD;
+  const bool full_block = (pb + 1) * kFePos <= p.T;  // every position of the block is < T
   const float scale_b = rbf(1.0f / sqrtf((float)kD));
   const float eps_b = rbf(1e-6f);
   auto& vt = vtile[wave];
@@ -399,15 +411,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       }
       if (pos < p.T) {
         __bf16* o = dst + (size_t)pos * pstride;
-        *reinterpret_cast<bf4*>(o + 4 * m) = to_bf4(y0);
-        *reinterpret_cast<bf4*>(o + 64 + 4 * m) = to_bf4(y1);
+        *reinterpret_cast<bf4*>(o + 4 * m) = bf4_of_rounded(y0);
+        *reinterpret_cast<bf4*>(o + 64 + 4 * m) = bf4_of_rounded(y1);
       }
     } else {
+      // u holds bf16 values: their high halves go to the tile as they are (a 16-bit store of
+      // the high half); positions past T are zeros (only the last block has any)
+      // (stored as __bf16, the type the tile is read back as)
       const int tp = 8 * (lane >> 4) + t;  // position within the block
+      auto hi16 = [](uint32_t b) { return __builtin_bit_cast(__bf16, (uint16_t)(b >> 16)); };
+      if (full_block) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[4 * m + e][tp] = pos < p.T ? (__bf16)u[e] : (__bf16)0.0f;
-        vt[64 + 4 * m + e][tp] = pos < p.T ? (__bf16)u[4 + e] : (__bf16)0.0f;
+        for (int e = 0; e < 4; ++e) {
+          vt[4 * m + e][tp] = hi16(__builtin_bit_cast(uint32_t, u[e]));
+          vt[64 + 4 * m + e][tp] = hi16(__builtin_bit_cast(uint32_t, u[4 + e]));
+        }
+      } else {
+        const bool live = pos < p.T;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vt[4 * m + e][tp] = hi16(live ? __builtin_bit_cast(uint32_t, u[e]) : 0u);
+          vt[64 + 4 * m + e][tp] = hi16(live ? __builtin_bit_cast(uint32_t, u[4 + e]) : 0u);
+        }
       }
     }
   }
