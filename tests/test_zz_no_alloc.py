@@ -45,6 +45,15 @@ def test_qlinear_noalloc_equals_qlinear_two_calls(O, gdn, dev):
     got = gdn.qlinear_noalloc(mats, x)
     torch.cuda.synchronize()
     _same(got, ref, "call 1")
+    # call 1b: 8 layers of the in_proj row count at M = 40 (K = 1024): enough 256-row
+    # workgroups for the kernel whose waves share the operand through LDS
+    log_case("qlinear_noalloc call 1b: in_proj rows x 8 layers, M=40, K=1024 (operand-sharing kernel)")
+    mats1b = _mats(O, gdn, dev, 8, [10240, 6144, 48, 48], 1024, seed=508)
+    x1b = to_dev(O.to_bf16(np.random.default_rng(509).standard_normal((8, 40, 1024)).astype(np.float32)), dev)
+    ref1b = gdn.qlinear(mats1b, x1b, n_layers=8)
+    got1b = gdn.qlinear_noalloc(mats1b, x1b, n_layers=8)
+    torch.cuda.synchronize()
+    _same(got1b, ref1b, "call 1b")
     # call 2: smaller -- M = 5 (one 16-row tile, rows 5..15 are zero padding in the scratch
     # that call 1 filled with data), K = 1024, with the GatedRMSNorm prologue
     log_case("qlinear_noalloc call 2: norm + out_proj, M=5, K=1024, N=300")
