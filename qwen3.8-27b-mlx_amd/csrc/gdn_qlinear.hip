@@ -604,12 +604,12 @@ __device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
 template <int MT>
 __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
   constexpr int NT = kNsTiles, D = kNsAhead, S = D + 1;
-  constexpr int kOp = MT * 4 * 1024;       // a slot's operand: [m tile][group of the step][k step] 1 KB blocks
-  constexpr int kXs = 2 * 64 * 4;          // then the two groups' sums x: [group][64] fp32 (16 MT used)
-  constexpr int kSlot = kOp + kXs;
-  constexpr int kPerStep = MT + 1 + 2 * NT;  // vector-memory instructions per wave and step
+  constexpr int kSlot = MT * 4 * 1024;     // a slot: [m tile][group of the step][k step] 1 KB operand blocks
+  constexpr int kPerStep = MT + 2 * NT;    // vector-memory instructions per wave and step
+  constexpr int kMaxG = 8192 / 64;
   __shared__ __attribute__((aligned(16))) unsigned char ring[S * kSlot];
-  __shared__ __attribute__((aligned(16))) uint16_t sbl[4][2][2][64 * 8];  // [wave][buffer][s, b][row][8 groups]
+  __shared__ __attribute__((aligned(16))) uint16_t sbl[4][2][64 * 8];  // scale words: [wave][buffer][row][8 groups]
+  __shared__ __attribute__((aligned(16))) float xs_all[kMaxG * 16 * MT];  // the sums x: [group][16 MT]
 
   int bid = blockIdx.x;
   if (p.remap) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
@@ -621,6 +621,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
   const int bsrc = (4 * nn + g4) * 4;  // as in qgemm_kernel
   g_u32x2* wr[NT];
   uint16_t* yr[NT];
+  const uint16_t *srow[NT], *brow[NT];  // this lane's output row's scale and bias words
   int ystride[NT];
   bool valid[NT];
 #pragma unroll
@@ -630,19 +631,23 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
     yr[nt] = rp.y;
     ystride[nt] = rp.ystride;
+    srow[nt] = rp.s;
+    brow[nt] = rp.b;
     const int lrow = rbase + 16 * nt + (lane >> 2);
     const RowPtrs rl = row_ptrs(p, layer, lrow < p.R ? lrow : p.R - 1);
     wr[nt] = (g_u32x2*)(rl.w) + (lane & 3);
   }
-  // lane l loads the scale and bias words of the wave's row l
+  // lane l loads the scale words of the wave's row l
   const RowPtrs rsb = row_ptrs(p, layer, min(rbase + lane, p.R - 1));
   const char* s_src = reinterpret_cast<const char*>(rsb.s);
-  const char* b_src = reinterpret_cast<const char*>(rsb.b);
   const char* xa = reinterpret_cast<const char*>(p.xfrag + (size_t)layer * MT * nch * 512) + 16 * lane;
-  // lane l of wave w loads sum l of group 2 j + w % 2 (lanes past 16 MT repeat the last one:
-  // waves w and w + 2 write the same bytes, so every wave issues the same loads and no lane
-  // is masked off -- divergent code here would split the loop into blocks)
-  const char* xsrc = reinterpret_cast<const char*>(p.xsum + (size_t)layer * G * 16 * MT) + 4 * (16 * MT * (wave & 1) + min(lane, 16 * MT - 1));
+  // the layer's sums x, all groups, for the bias products after the loop (one barrier: the
+  // loop issues no load before it)
+  {
+    const f4* src = reinterpret_cast<const f4*>(p.xsum + (size_t)layer * G * 16 * MT);
+    for (int q = threadIdx.x; q < G * 4 * MT; q += kThreads) reinterpret_cast<f4*>(xs_all)[q] = src[q];
+  }
+  __syncthreads();
   const NibbleConsts nk = nibble_consts();
 
   // step j's loads: the wave's block (group 2 j + wave / 2, k step wave % 2) of every m tile
@@ -652,7 +657,6 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     const uint32_t dst = ring_l + sl * kSlot;
 #pragma unroll
     for (int i = 0; i < MT; ++i) dma16(xa + ((size_t)i * nch + 4 * j + wave) * 1024, dst + (4 * i + wave) * 1024);
-    dma4(xsrc + (size_t)j * 2 * 16 * MT * 4, dst + kOp + 256 * (wave & 1));
   };
   struct WStep {
     u32x2 w[2][NT];
@@ -666,11 +670,8 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     }
   };
   // scale and bias words of groups 8 blk .. + 7 into buffer buf
-  const uint32_t sbl_l = lds_addr(&sbl[wave][0][0][0]);
-  auto issue_sb = [&](int blk, int buf) {
-    dma16(s_src + 16 * blk, sbl_l + buf * 2048);
-    dma16(b_src + 16 * blk, sbl_l + buf * 2048 + 1024);
-  };
+  const uint32_t sbl_l = lds_addr(&sbl[wave][0][0]);
+  auto issue_sb = [&](int blk, int buf) { dma16(s_src + 16 * blk, sbl_l + buf * 1024); };
 
   f4 y[MT][NT];
 #pragma unroll
@@ -679,28 +680,20 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     for (int nt = 0; nt < NT; ++nt) y[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int j, const unsigned char* slot, const uint16_t* sbw, const WStep& ws) {
-    // the scale and bias words of the step's two groups, one 4-byte read each per tile
-    uint32_t sw[NT], bw[NT];
+    // the scale words of the step's two groups, one 4-byte read per tile
+    uint32_t sw[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int o = (16 * nt + nn) * 8 + ((2 * j) & 7);
-      sw[nt] = *reinterpret_cast<const uint32_t*>(sbw + o);
-      bw[nt] = *reinterpret_cast<const uint32_t*>(sbw + 64 * 8 + o);
-    }
+    for (int nt = 0; nt < NT; ++nt) sw[nt] = *reinterpret_cast<const uint32_t*>(sbw + (16 * nt + nn) * 8 + ((2 * j) & 7));
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
       bf8 a[MT][2];
-      f4 xs[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int s = 0; s < 2; ++s) a[mt][s] = *reinterpret_cast<const bf8*>(slot + (4 * mt + 2 * gg + s) * 1024 + 16 * lane);
-        xs[mt] = *reinterpret_cast<const f4*>(slot + kOp + 256 * gg + 4 * (16 * mt + 4 * g4));
-      }
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const float sc = __builtin_bit_cast(float, gg ? sw[nt] & 0xFFFF0000u : sw[nt] << 16);
-        const float off = __builtin_bit_cast(float, gg ? bw[nt] & 0xFFFF0000u : bw[nt] << 16) - 128.0f * sc;
         const uint32_t w0 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)ws.w[gg][nt][0]);
         const uint32_t w1 = (uint32_t)__builtin_amdgcn_ds_bpermute(bsrc, (int)ws.w[gg][nt][1]);
         const bf8 b0 = nibbles_bf16(w0, nk), b1 = nibbles_bf16(w1, nk);
@@ -709,7 +702,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
           f4 acc = mfma(a[mt][0], b0, f4{0.f, 0.f, 0.f, 0.f});
           acc = mfma(a[mt][1], b1, acc);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], __builtin_fmaf(off, xs[mt][i], y[mt][nt][i]));
+          for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], y[mt][nt][i]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // a group's products and sums stay together
@@ -729,15 +722,15 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     for (int r = 0; r < 4; ++r) {
       const int j = j0 + r;
       // step j's loads are done once no more than the loads issued after them are in flight:
-      // step j + 1's, and also the scale and bias pair issued at step 4 b after step
-      // 4 b + 2's (in flight at steps 4 b + 1 and 4 b + 2); then every wave's are (the
-      // barrier). The wait and the barrier are one asm statement with a memory clobber, so no
-      // load moves across them.
+      // step j + 1's, and also the scale words issued at step 4 b after step 4 b + 2's (in
+      // flight at steps 4 b + 1 and 4 b + 2); then every wave's are (the barrier). The wait
+      // and the barrier are one asm statement with a memory clobber, so no load moves across
+      // them.
       if (r == 1 || r == 2)
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep + 2) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep + 1) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep) : "memory");
-      compute(j, ring + sl * kSlot, &sbl[wave][(j >> 2) & 1][0][0], W[r & 1]);
+      compute(j, ring + sl * kSlot, &sbl[wave][(j >> 2) & 1][0], W[r & 1]);
       __builtin_amdgcn_sched_barrier(0);
       // refill what step j - 1 read (every wave is past it: the barrier above)
       const int jn = min(j + D, nsteps - 1);
@@ -748,6 +741,67 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated loads, before the LDS goes away
+
+  // The bias term sum_g (b_g - 128 s_g) sum x_g = Yb - 128 Ys, Yb = sum_g b_g sum x_g and
+  // Ys = sum_g s_g sum x_g, on MFMA after the loop (it was two FMAs per element and group):
+  // A = the sums x of 16 operand rows x 32 groups, each split into three bf16 terms (exact to
+  // about 2^-24 of it), B = the rows' bias / scale words of the same groups (bf16, exact);
+  // groups past G are zeros. Lane (g4, r) takes groups 32 ks + 8 g4 .. + 7.
+  {
+    f4 yb[MT][NT], ysc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) yb[mt][nt] = ysc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < (G + 31) / 32; ++ks) {
+      const int g0 = 32 * ks + 8 * g4;
+      const bool live = g0 < G;  // G is a multiple of 16: all eight or none
+      bf8 bb[NT], bs[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        u32x4 vb{}, vs{};
+        if (live) {
+          const u32x2 b0 = *(g_u32x2*)(brow[nt] + g0), b1 = *(g_u32x2*)(brow[nt] + g0 + 4);
+          const u32x2 s0 = *(g_u32x2*)(srow[nt] + g0), s1 = *(g_u32x2*)(srow[nt] + g0 + 4);
+          vb = u32x4{b0[0], b0[1], b1[0], b1[1]};
+          vs = u32x4{s0[0], s0[1], s1[0], s1[1]};
+        }
+        bb[nt] = __builtin_bit_cast(bf8, vb);
+        bs[nt] = __builtin_bit_cast(bf8, vs);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = live ? xs_all[(g0 + i) * 16 * MT + 16 * mt + nn] : 0.0f;
+        bf8 hi, mid, lo;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float h = rbf(v[i]);
+          const float r1 = v[i] - h;
+          const float m1 = rbf(r1);
+          hi[i] = __builtin_bit_cast(__bf16, (uint16_t)(__builtin_bit_cast(uint32_t, h) >> 16));
+          mid[i] = __builtin_bit_cast(__bf16, (uint16_t)(__builtin_bit_cast(uint32_t, m1) >> 16));
+          lo[i] = (__bf16)(r1 - m1);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          yb[mt][nt] = mfma(hi, bb[nt], yb[mt][nt]);
+          yb[mt][nt] = mfma(mid, bb[nt], yb[mt][nt]);
+          yb[mt][nt] = mfma(lo, bb[nt], yb[mt][nt]);
+          ysc[mt][nt] = mfma(hi, bs[nt], ysc[mt][nt]);
+          ysc[mt][nt] = mfma(mid, bs[nt], ysc[mt][nt]);
+          ysc[mt][nt] = mfma(lo, bs[nt], ysc[mt][nt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[mt][nt][i] += __builtin_fmaf(-128.0f, ysc[mt][nt][i], yb[mt][nt][i]);
+  }
 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -901,7 +955,7 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
     sb16 = sb16 && reinterpret_cast<uintptr_t>(a.segs[q].scales) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.segs[q].biases) % 16 == 0;
   const int ns_tiles = (R + kNsRows - 1) / kNsRows;
-  if (gy == 1 && sb16 && (size_t)a.n_layers * ns_tiles >= 512) {
+  if (gy == 1 && MT <= 3 && sb16 && (size_t)a.n_layers * ns_tiles >= 512) {
     p.tiles = ns_tiles;
     p.mgroups = 1;
     const size_t nwg = (size_t)a.n_layers * ns_tiles;
@@ -910,8 +964,7 @@ hipError_t launch_qlinear(const gdn_qlinear_args& a, hipStream_t stream) {
     switch (MT) {
       case 1: hipLaunchKernelGGL(qgemm_ns_kernel<1>, grid, dim3(kThreads), 0, stream, p); break;
       case 2: hipLaunchKernelGGL(qgemm_ns_kernel<2>, grid, dim3(kThreads), 0, stream, p); break;
-      case 3: hipLaunchKernelGGL(qgemm_ns_kernel<3>, grid, dim3(kThreads), 0, stream, p); break;
-      default: hipLaunchKernelGGL(qgemm_ns_kernel<4>, grid, dim3(kThreads), 0, stream, p); break;
+      default: hipLaunchKernelGGL(qgemm_ns_kernel<3>, grid, dim3(kThreads), 0, stream, p); break;
     }
     return hipGetLastError();
   }
