@@ -568,20 +568,23 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(QParams p) {
   }
 }
 
-// MFMA path for calls of many weight rows and few operand rows (one m group, up to 64 rows;
-// 8 layers or more per call): workgroup = 256 weight rows, wave w owns 64 of them (kNsTiles
-// 16-row tiles) over the whole of K, and the four waves share the operand, which passes
-// through an LDS ring once per workgroup (qgemm_kernel reads it from L2 once per 64 rows).
-// A step is two groups. Direct-to-LDS loads (`global_load_lds_dwordx4`: lane l's 16 bytes
-// land at the destination + 16 l, no VGPRs) fill the ring kNsAhead steps ahead: each wave
-// issues one of the step's four 1 KB blocks of every m tile and a quarter of the two
-// groups' sums x, waits for its own loads, and one barrier per step then makes the slot
-// whole for all four. Each wave also loads the scale and bias words of its rows, 8 groups
-// at a time, into its own pair of LDS buffers (read by that wave only: no barrier). The
-// weight words stay in a register ring, loaded and moved into fragment order as in
-// qgemm_kernel. Loads complete in issue order and the waits count them, so every step issues
-// the same loads (past the last step they repeat it). Arithmetic per group as in
-// qgemm_kernel; each wave adds its groups in order and rounds its rows once.
+// MFMA path for calls of many weight rows and few operand rows (one m group of up to 48 rows;
+// 8 layers or more of in_proj per call): workgroup = 256 weight rows, wave w owns 64 of them
+// (kNsTiles 16-row tiles) over the whole of K, and the four waves share the operand, which
+// passes through an LDS ring once per workgroup (qgemm_kernel reads it from L2 once per 64
+// rows). A step is two groups. Direct-to-LDS loads (`global_load_lds_dwordx4`: lane l's 16
+// bytes land at the destination + 16 l, no VGPRs) fill the ring kNsAhead steps ahead: each
+// wave issues one of the step's four 1 KB blocks of every m tile, waits for its own loads,
+// and one barrier per step then makes the slot whole for all four. Each wave also loads the
+// scale words of its rows, 8 groups at a time, into its own pair of LDS buffers (read by that
+// wave only: no barrier). The weight words stay in a register ring, loaded and moved into
+// fragment order as in qgemm_kernel. Loads complete in issue order and the waits count them,
+// so every step issues the same loads (past the last step they repeat it), and no lane is
+// masked off in the loop (a divergent branch there split the loop into blocks, after which
+// the compiler sank a step's FMAs to its end with every MFMA result live). Per group
+// y += s * sum x (128 + q) as in qgemm_kernel, each wave adding its groups in order; the
+// bias term sum_g (b_g - 128 s_g) sum x_g is made after the loop as MFMA products (below),
+// and each row is rounded once.
 constexpr int kNsTiles = 4;
 constexpr int kNsRows = 4 * 16 * kNsTiles;  // weight rows per workgroup
 constexpr int kNsAhead = 2;                 // steps between a load and its use
