@@ -590,18 +590,20 @@ constexpr int kNsRows = 4 * 16 * kNsTiles;  // weight rows per workgroup
 constexpr int kNsAhead = 2;                 // steps between a load and its use
 typedef __attribute__((address_space(3))) void lds_void;
 // Direct-to-LDS loads written as asm: the compiler, which cannot tell which LDS bytes such a
-// load writes, otherwise waits for every one in flight before each later LDS access and
-// each later such load (vmcnt(0)), which would undo the ring. The asm statements have a
-// memory clobber (no memory access moves across them); the kernel waits for them itself.
-// M0 holds the LDS destination; nothing else in the kernel uses M0.
+// load writes, otherwise waits for every one in flight (vmcnt(0)) at points in the loop, which
+// would undo the ring. The asm statements have a memory clobber (no memory access moves
+// across them); the kernel waits for them itself. M0 carries the LDS destination and is
+// restored after the load has been issued (the load takes it at issue), so the compiler's
+// view of M0 is never disturbed.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p);
 }
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
-}
-__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory");
+  uint32_t m0_saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+               : "=&s"(m0_saved)
+               : "v"(src), "s"(lds)
+               : "memory");
 }
 
 template <int MT>
