@@ -625,19 +625,8 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
   const int rbase = (tile * 4 + wave) * 16 * NT;
   const int bsrc = (4 * nn + g4) * 4;  // as in qgemm_kernel
   g_u32x2* wr[NT];
-  uint16_t* yr[NT];
-  const uint16_t *srow[NT], *brow[NT];  // this lane's output row's scale and bias words
-  int ystride[NT];
-  bool valid[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int grow = rbase + 16 * nt + nn;
-    valid[nt] = grow < p.R;
-    const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
-    yr[nt] = rp.y;
-    ystride[nt] = rp.ystride;
-    srow[nt] = rp.s;
-    brow[nt] = rp.b;
     const int lrow = rbase + 16 * nt + (lane >> 2);
     const RowPtrs rl = row_ptrs(p, layer, lrow < p.R ? lrow : p.R - 1);
     wr[nt] = (g_u32x2*)(rl.w) + (lane & 3);
@@ -710,7 +699,6 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
           for (int i = 0; i < 4; ++i) y[mt][nt][i] = __builtin_fmaf(sc, acc[i], y[mt][nt][i]);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);  // a group's products and sums stay together
     }
   };
 
@@ -746,6 +734,22 @@ __global__ __launch_bounds__(kThreads) void qgemm_ns_kernel(QParams p) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated loads, before the LDS goes away
+  // this lane's output rows, their scale and bias words: found here rather than held in
+  // registers through the loop
+  uint16_t* yr[NT];
+  const uint16_t *srow[NT], *brow[NT];
+  int ystride[NT];
+  bool valid[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int grow = rbase + 16 * nt + nn;
+    valid[nt] = grow < p.R;
+    const RowPtrs rp = row_ptrs(p, layer, valid[nt] ? grow : p.R - 1);
+    yr[nt] = rp.y;
+    ystride[nt] = rp.ystride;
+    srow[nt] = rp.s;
+    brow[nt] = rp.b;
+  }
 
   // The bias term sum_g (b_g - 128 s_g) sum x_g = Yb - 128 Ys, Yb = sum_g b_g sum x_g and
   // Ys = sum_g s_g sum x_g, on MFMA after the loop (it was two FMAs per element and group):
