@@ -174,6 +174,7 @@ __device__ __forceinline__ bf8 frag_ilv(const __bf16 (*m)[LD], int row, int k0, 
 struct PrefillParams {
   int B, T, Hk, Hv, rep, C, nC;
   int gate_raw, o_bf16;
+  int q_frag;  // the conv front end writes Q straight into ws_q (the intra kernel then reads no q)
   const uint16_t* x;
   const uint16_t* conv_w;
   const uint16_t* conv_in;
@@ -378,6 +379,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (is_q) dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
   else if (norm) dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
   const size_t pstride = (size_t)p.Hk * kD;
+  // Q: channels 4 m .. + 3 are group m % 4 of 32-channel block m / 8, in the group's low
+  // (m % 8 < 4) or high half
+  auto& qt = *reinterpret_cast<__bf16(*)[kFePos][kD + 8]>(&vtile[wave][0][0]);
+  const int qcol = 32 * (m >> 3) + 8 * (m & 3) + 4 * ((m >> 2) & 1);
   const bool full_block = (pb + 1) * kFePos <= p.T;  // every position of the block is < T
   const float scale_b = rbf(1.0f / sqrtf((float)kD));
   const float eps_b = rbf(1e-6f);
@@ -409,7 +414,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
           y1[e] = rbf(y1[e] * scale_b);
         }
       }
-      if (pos < p.T) {
+      if (is_q && p.q_frag) {
+        // Q to this wave's LDS tile ([position][channel], each 32-channel block in the
+        // fragments' interleaved order: channel 32 kb + 4 g + e at 32 kb + 8 g + e and
+        // 32 kb + 16 + 4 g + e at 32 kb + 8 g + 4 + e), zeros past T
+        const int tp = 8 * (lane >> 4) + t;
+        const bool live = pos < p.T;
+        *reinterpret_cast<bf4*>(&qt[tp][qcol]) = live ? bf4_of_rounded(y0) : bf4{};
+        *reinterpret_cast<bf4*>(&qt[tp][64 + qcol]) = live ? bf4_of_rounded(y1) : bf4{};
+      } else if (pos < p.T) {
         __bf16* o = dst + (size_t)pos * pstride;
         *reinterpret_cast<bf4*>(o + 4 * m) = bf4_of_rounded(y0);
         *reinterpret_cast<bf4*>(o + 64 + 4 * m) = bf4_of_rounded(y1);
@@ -455,6 +468,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       // positions there, and the scan reads V for every position of a chunk)
       if (kh == 0 && pb == pblocks - 1)
         *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + 1) * kFrag + lane * 8) = bf8{};
+    }
+  }
+  if (is_q && p.q_frag) {
+    // Q into ws_q: fragment block 4 (position tile) + 32-channel block of the chunk, lane
+    // 16 g + r holding position r of the tile, channels 4 g .. + 3 and 16 + 4 g .. + 3 of
+    // the block (one 16-byte read of the tile); this block is half a chunk (kFePos = kC / 2)
+    const int kh = pb & 1;
+    __bf16* qf = p.ws_q + (((size_t)b * p.Hk + hh) * p.nC + pb / 2) * kChunkElems + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int pt = i >> 2, kb = i & 3;
+      *reinterpret_cast<bf8*>(qf + ((2 * kh + pt) * 4 + kb) * kFrag) =
+          *reinterpret_cast<const bf8*>(&qt[16 * pt + (lane & 15)][32 * kb + 8 * (lane >> 4)]);
+      // the last chunk's second half when it lies wholly past T: zeros
+      if (kh == 0 && pb == pblocks - 1) *reinterpret_cast<bf8*>(qf + ((2 + pt) * 4 + kb) * kFrag) = bf8{};
     }
   }
   if (p.conv_out && pb == pblocks - 1) {
@@ -574,12 +602,18 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   {
     constexpr int kIt = kC * kD / 8 / kThreads;
     bf8 qv[kIt], kv[kIt];
+    const bool load_q = !PRECISE || !p.q_frag;  // (the front end wrote Q's fragments itself)
+    if (load_q) {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+        qv[it] = *reinterpret_cast<const bf8*>(p.q + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
+      }
+    }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      const size_t gi = (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8;
-      qv[it] = *reinterpret_cast<const bf8*>(p.q + gi);
-      kv[it] = *reinterpret_cast<const bf8*>(p.k + gi);
+      kv[it] = *reinterpret_cast<const bf8*>(p.k + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
     }
     // the first group's (G, beta, e^G), written by the front end's gate workgroups: wave r
     // takes v-head r, lane = position (loaded behind q and k, so their waits come first)
@@ -591,10 +625,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       gb0 = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
       eg0 = p.ws_g[hc * kGStride + 2 * lane];
     }
+    if (load_q) {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+        *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
+      }
+    }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = pos < n ? kv[it] : bf8{};
     }
     if (wave < gs0) {
@@ -620,11 +660,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   {
-    __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
+    if (!PRECISE || !p.q_frag) {
+      __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) {
-      __builtin_nontemporal_store(frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg),
-                                  reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
+      for (int ks = 0; ks < kD / 32; ++ks) {
+        __builtin_nontemporal_store(frag_ilv(s.u.fe.q, 16 * wave + fr, 32 * ks, lg),
+                                    reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
+      }
     }
     if constexpr (PRECISE) {  // K, in the layout of Q, for the scan's K S
       __bf16* wk = p.ws_kk + gc * kChunkElems + lane * 8;
@@ -1609,6 +1651,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.C = 2 * p.Hk * kD + p.Hv * kD;
   p.nC = (p.T + kC - 1) / kC;
   p.gate_raw = a.gate_mode == GDN_GATES_RAW;
+  p.q_frag = a.frontend == GDN_FRONTEND_CONV && a.prefill_precision == GDN_PREFILL_ACCURATE;
   p.o_bf16 = a.o_dtype == GDN_DTYPE_BF16;
   p.x = static_cast<const uint16_t*>(a.x);
   p.conv_w = static_cast<const uint16_t*>(a.conv_weight);
