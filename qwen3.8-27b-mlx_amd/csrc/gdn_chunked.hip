@@ -174,7 +174,7 @@ __device__ __forceinline__ bf8 frag_ilv(const __bf16 (*m)[LD], int row, int k0, 
 struct PrefillParams {
   int B, T, Hk, Hv, rep, C, nC;
   int gate_raw, o_bf16;
-  int q_frag;  // the conv front end writes Q straight into ws_q (the intra kernel then reads no q)
+  int qk_frag;  // the conv front end writes Q and K straight into ws_q and ws_kk (fragment order)
   const uint16_t* x;
   const uint16_t* conv_w;
   const uint16_t* conv_in;
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (is_q) dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
   else if (norm) dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
   const size_t pstride = (size_t)p.Hk * kD;
-  // Q: channels 4 m .. + 3 are group m % 4 of 32-channel block m / 8, in the group's low
+  // Q, K: channels 4 m .. + 3 are group m % 4 of 32-channel block m / 8, in the group's low
   // (m % 8 < 4) or high half
   auto& qt = *reinterpret_cast<__bf16(*)[kFePos][kD + 8]>(&vtile[wave][0][0]);
   const int qcol = 32 * (m >> 3) + 8 * (m & 3) + 4 * ((m >> 2) & 1);
@@ -414,8 +414,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
           y1[e] = rbf(y1[e] * scale_b);
         }
       }
-      if (is_q && p.q_frag) {
-        // Q to this wave's LDS tile ([position][channel], each 32-channel block in the
+      if (p.qk_frag) {
+        // Q or K to this wave's LDS tile ([position][channel], each 32-channel block in the
         // fragments' interleaved order: channel 32 kb + 4 g + e at 32 kb + 8 g + e and
         // 32 kb + 16 + 4 g + e at 32 kb + 8 g + 4 + e), zeros past T
         const int tp = 8 * (lane >> 4) + t;
@@ -470,12 +470,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + 1) * kFrag + lane * 8) = bf8{};
     }
   }
-  if (is_q && p.q_frag) {
-    // Q into ws_q: fragment block 4 (position tile) + 32-channel block of the chunk, lane
-    // 16 g + r holding position r of the tile, channels 4 g .. + 3 and 16 + 4 g .. + 3 of
-    // the block (one 16-byte read of the tile); this block is half a chunk (kFePos = kC / 2)
+  if (norm && p.qk_frag) {
+    // Q into ws_q, K into ws_kk: fragment block 4 (position tile) + 32-channel block of the
+    // chunk, lane 16 g + r holding position r of the tile, channels 4 g .. + 3 and
+    // 16 + 4 g .. + 3 of the block (one 16-byte read of the tile); this block is half a
+    // chunk (kFePos = kC / 2)
     const int kh = pb & 1;
-    __bf16* qf = p.ws_q + (((size_t)b * p.Hk + hh) * p.nC + pb / 2) * kChunkElems + lane * 8;
+    __bf16* qf = (is_q ? p.ws_q : p.ws_kk) + (((size_t)b * p.Hk + (is_q ? hh : hh - p.Hk)) * p.nC + pb / 2) * kChunkElems + lane * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int pt = i >> 2, kb = i & 3;
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   {
     constexpr int kIt = kC * kD / 8 / kThreads;
     bf8 qv[kIt], kv[kIt];
-    const bool load_q = !PRECISE || !p.q_frag;  // (the front end wrote Q's fragments itself)
+    const bool load_q = !PRECISE || !p.qk_frag;  // (the front end wrote Q's fragments itself)
     if (load_q) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
@@ -610,10 +611,20 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         qv[it] = *reinterpret_cast<const bf8*>(p.q + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
       }
     }
+    // K: row-major from the front end or the caller, or (conv front end, accurate form)
+    // the fragments the front end wrote into ws_kk (zeros past T), thread e taking lane
+    // e % 64 of block e / 64
+    const bool k_frag = PRECISE && p.qk_frag;
+    if (k_frag) {
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      kv[it] = *reinterpret_cast<const bf8*>(p.k + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
+      for (int it = 0; it < kIt; ++it)
+        kv[it] = *reinterpret_cast<const bf8*>(p.ws_kk + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
+    } else {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+        kv[it] = *reinterpret_cast<const bf8*>(p.k + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
+      }
     }
     // the first group's (G, beta, e^G), written by the front end's gate workgroups: wave r
     // takes v-head r, lane = position (loaded behind q and k, so their waits come first)
@@ -632,10 +643,22 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       }
     }
+    if (k_frag) {
+      // fragment lane (g, r) of block (position tile pt, 32-channel block kb): position
+      // 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
-      *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = pos < n ? kv[it] : bf8{};
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
+        const int pos = 16 * (blk >> 2) + (fl & 15), d0 = 32 * (blk & 3) + 4 * (fl >> 4);
+        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0]) = __builtin_shufflevector(kv[it], kv[it], 0, 1, 2, 3);
+        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0 + 16]) = __builtin_shufflevector(kv[it], kv[it], 4, 5, 6, 7);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
+        *reinterpret_cast<bf8*>(&s.u.fe.k[pos][d8]) = pos < n ? kv[it] : bf8{};
+      }
     }
     if (wave < gs0) {
       s.G[wave][lane] = gb0.x;
@@ -660,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   {
-    if (!PRECISE || !p.q_frag) {
+    if (!PRECISE || !p.qk_frag) {
       __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -668,7 +691,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                     reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
       }
     }
-    if constexpr (PRECISE) {  // K, in the layout of Q, for the scan's K S
+    if (PRECISE && !p.qk_frag) {  // K, in the layout of Q, for the scan's K S
       __bf16* wk = p.ws_kk + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -1651,7 +1674,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.C = 2 * p.Hk * kD + p.Hv * kD;
   p.nC = (p.T + kC - 1) / kC;
   p.gate_raw = a.gate_mode == GDN_GATES_RAW;
-  p.q_frag = a.frontend == GDN_FRONTEND_CONV && a.prefill_precision == GDN_PREFILL_ACCURATE;
+  p.qk_frag = a.frontend == GDN_FRONTEND_CONV && a.prefill_precision == GDN_PREFILL_ACCURATE;
   p.o_bf16 = a.o_dtype == GDN_DTYPE_BF16;
   p.x = static_cast<const uint16_t*>(a.x);
   p.conv_w = static_cast<const uint16_t*>(a.conv_weight);
