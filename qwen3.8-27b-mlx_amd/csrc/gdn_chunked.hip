@@ -1624,8 +1624,9 @@ struct WorkspaceLayout {
   size_t q, kt, g, vf, fq, fk, gb, m, w, u, us, kk, tp, total;
 };
 
-// conv: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace too (its v
-// goes to vf, which the qkv front end fills from the caller's v).
+// conv, fast form: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace
+// too (its v goes to vf, which the qkv front end fills from the caller's v); in the accurate
+// form it writes Q and K straight into their fragment planes.
 // precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise M, W, U (fp16) and U's scales.
 WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
@@ -1633,7 +1634,7 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
   const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
   const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
-  const size_t fqk = conv ? al((size_t)B * T * Hk * kD * 2) : 0;
+  const size_t fqk = conv && !precise ? al((size_t)B * T * Hk * kD * 2) : 0;
   WorkspaceLayout L{};
   L.q = 0;
   L.kt = L.q + qk;
@@ -1711,8 +1712,9 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {
-    p.q = reinterpret_cast<const __bf16*>(w + L.fq);
-    p.k = reinterpret_cast<const __bf16*>(w + L.fk);
+    // (accurate form: the front end writes Q and K into ws_q and ws_kk, no row-major copy)
+    p.q = p.qk_frag ? nullptr : reinterpret_cast<const __bf16*>(w + L.fq);
+    p.k = p.qk_frag ? nullptr : reinterpret_cast<const __bf16*>(w + L.fk);
     p.v = nullptr;  // the front end writes v straight into ws_vf
   }
 
