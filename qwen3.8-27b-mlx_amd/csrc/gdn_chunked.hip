@@ -15,8 +15,9 @@
 // with the state products at fp32 accuracy (below), so W and U are never formed.
 //
 // Three kernels, one stream:
-//   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position into bf16 q, k
-//                  (B, T, Hk, 128) and v, which goes straight into B-operand fragments in
+//   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position: q and k into the
+//                  A-operand fragment planes of Q and K (accurate form) or bf16 rows
+//                  (B, T, Hk, 128) (fast form), and v straight into B-operand fragments in
 //                  the interleaved k order (with q, k, v given by the caller,
 //                  prefill_vfrag reorders v instead). Extra workgroups of the same launch
 //                  compute the gates and each chunk's cumulative log decay G (one wave per
@@ -25,7 +26,7 @@
 //                  per CU: K K^T (and, fast form, K Q^T) on bf16 MFMA, and for the
 //                  k-head's v-heads A (and M), T = (I + A)^-1 (one wave per v-head, fp32,
 //                  left in LDS), then each wave's T' fragments from T in LDS: stored split
-//                  into bf16 hi + lo (accurate form, with K), or used for U = T'V and
+//                  into bf16 hi + lo (accurate form), or used for U = T'V and
 //                  W = T'diag(e^G)K on bf16 MFMA (fast form; U stored as fp16 scaled by a
 //                  power of two per 16-position tile). Results go to the workspace, already
 //                  in the register order of the MFMA operands that read them.
@@ -578,10 +579,12 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
   finish(3, 0, prod(3, 2, -1, 0, prod(3, 0, 1, 0, zero)));
 }
 
-// q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output.
+// q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output; with the
+// conv front end in the accurate form, K comes from its fragment plane and q is not read
+// (the front end wrote Q's and K's fragments itself).
 // ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
-// dead after the first group). Everything it writes for the scan (Q, K^T, M, U, W: 224 MB at
-// T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
+// dead after the first group). Everything it writes for the scan (fast form: Q, K^T, M, U,
+// W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
 // scan that reads it back. (The front end's outputs, which this kernel reads, stay
 // cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
 template <bool ONE_GROUP, bool PRECISE>
