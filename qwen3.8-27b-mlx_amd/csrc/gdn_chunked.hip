@@ -175,7 +175,7 @@ __device__ __forceinline__ bf8 frag_ilv(const __bf16 (*m)[LD], int row, int k0, 
 struct PrefillParams {
   int B, T, Hk, Hv, rep, C, nC;
   int gate_raw, o_bf16;
-  int qk_frag;  // the conv front end writes Q and K straight into ws_q and ws_kk (fragment order)
+  int qk_frag;  // the conv front end writes Q, K and K^T straight into ws_q, ws_kk, ws_kt
   const uint16_t* x;
   const uint16_t* conv_w;
   const uint16_t* conv_in;
@@ -486,6 +486,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       // the last chunk's second half when it lies wholly past T: zeros
       if (kh == 0 && pb == pblocks - 1) *reinterpret_cast<bf8*>(qf + ((2 + pt) * 4 + kb) * kFrag) = bf8{};
     }
+    if (!is_q) {
+      // K^T into ws_kt: block 2 (16-channel tile a) + half chunk, lane 16 g + r holding
+      // channel 16 a + r at positions 4 g .. + 3 and 16 + 4 g .. + 3 of this block (the B
+      // fragment order of V, read down a column of the tile: the channel's column there is
+      // 32 (a / 2) + 8 (r / 4) + 4 (a % 2) + r % 4)
+      const int r = lane & 15, g = lane >> 4;
+      __bf16* ktf = p.ws_kt + (((size_t)b * p.Hk + (hh - p.Hk)) * p.nC + pb / 2) * kChunkElems + lane * 8;
+#pragma unroll
+      for (int a = 0; a < kD / 16; ++a) {
+        const int col = 32 * (a >> 1) + 8 * (r >> 2) + 4 * (a & 1) + (r & 3);
+        bf8 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = qt[4 * g + i][col];
+          v[4 + i] = qt[16 + 4 * g + i][col];
+        }
+        *reinterpret_cast<bf8*>(ktf + (a * 2 + kh) * kFrag) = v;
+        if (kh == 0 && pb == pblocks - 1) *reinterpret_cast<bf8*>(ktf + (a * 2 + 1) * kFrag) = bf8{};
+      }
+    }
   }
   if (p.conv_out && pb == pblocks - 1) {
     for (int e = lane; e < kConvRows * kD; e += 64) {
@@ -702,17 +722,19 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                     reinterpret_cast<bf8*>(wk + (wave * 4 + ks) * kFrag));
       }
     }
-    const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
+    if (!PRECISE || !p.qk_frag) {  // (else the front end wrote K^T's fragments)
+      const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
-    for (int q8 = 0; q8 < 4; ++q8) {
-      bf8 v;
+      for (int q8 = 0; q8 < 4; ++q8) {
+        bf8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = s.u.fe.k[ph + 8 * q8 + e][dk];
-      *reinterpret_cast<bf8*>(&s.kt[dk][ph + 8 * q8]) = v;
+        for (int e = 0; e < 8; ++e) v[e] = s.u.fe.k[ph + 8 * q8 + e][dk];
+        *reinterpret_cast<bf8*>(&s.kt[dk][ph + 8 * q8]) = v;
+      }
     }
   }
   __syncthreads();
-  {
+  if (!PRECISE || !p.qk_frag) {
     __bf16* wkt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int a2 = 0; a2 < 2; ++a2)
