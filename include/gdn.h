@@ -168,9 +168,9 @@ int gdn_prefill_chunked(const gdn_layer_args* args);
 int gdn_prefill_chunked_timed(const gdn_layer_args* args, float* kernel_ms);
 
 /* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
- * counts, front end (the conv front end also stages its bf16 q, k in the workspace) and
- * prefill_precision (GDN_PREFILL_ACCURATE keeps U in fp32); the other fields are not
- * read. */
+ * counts, front end (with GDN_PREFILL_FAST the conv front end also stages its bf16 q, k
+ * rows in the workspace) and prefill_precision (GDN_PREFILL_ACCURATE keeps K and T' per
+ * chunk, GDN_PREFILL_FAST M, W and U); the other fields are not read. */
 int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {
