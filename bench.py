@@ -227,9 +227,9 @@ def prefill_flops(T: int, C: int = 64):
 
 
 def bench_prefill(torch, gdn, dev, timer, steps: int, warmup: int, T: int = 4096, precision: int = 0):
-    """One layer, B = 1, conv front end; `precision` is gdn_prefill_precision (0, the default
-    fp32-state form, keeps U in fp32 and splits V'' for the state update; 1 is the fast
-    form)."""
+    """One layer, B = 1, conv front end; `precision` is gdn_prefill_precision (0, the default,
+    carries the state products at fp32 accuracy through bf16 hi + lo splits; 1 is the fast
+    form, bf16 operands)."""
     i = make_layer_inputs(torch, dev, 1, 1, T, True, seed=500)
     x = i["x"][0].contiguous()
     o = torch.empty((1, T, HV, D), dtype=torch.bfloat16, device=dev)
