@@ -147,6 +147,23 @@ __device__ __forceinline__ void operand_piece(const QParams& p, int layer, int m
   }
 }
 
+// (a & m) | c: with m and c in VGPRs (opaque values from nibble_consts) the compiler selects
+// one v_and_or_b32 for it -- with literal constants it cannot (a VOP3 takes no literal on
+// this target and at most one SGPR) and emits a separate AND and OR. Written out in C, not
+// as inline asm, so that the compiler also sees the instruction and keeps the wait states
+// an MFMA reading its result needs.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
+struct NibbleConsts {
+  uint32_t mask, bias;  // 0x000F000F, 0x43004300
+};
+__device__ __forceinline__ NibbleConsts nibble_consts() {
+  NibbleConsts k;
+  k.mask = 0x000F000Fu;
+  k.bias = 0x43004300u;
+  asm volatile("" : "+v"(k.mask), "+v"(k.bias));  // (emits nothing: keeps them opaque VGPR values)
+  return k;
+}
+
 template <int J, bool NORM>
 __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -168,6 +185,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   __syncthreads();
 
   // ---- passes of 4 rows per wave ----
+  const NibbleConsts nk = nibble_consts();
   const int lane = tid & 63, m = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int passes = p.passes;
@@ -217,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
       for (int i = 0; i < 4; ++i) {
         const uint32_t wd = wv[j][i];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pr[i][q] = ((wd >> (4 * q)) & 0x000F000Fu) | 0x43004300u;
+        for (int q = 0; q < 4; ++q) pr[i][q] = and_or(wd >> (4 * q), nk.mask, nk.bias);
       }
 #pragma unroll
       for (int mm = 0; mm < GDN_QLINEAR_GEMV_ROWS; ++mm) {
@@ -309,23 +327,6 @@ __global__ __launch_bounds__(kThreads) void qprep_kernel(QParams p, int layers) 
 
 __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// (a & m) | c: with m and c in VGPRs (opaque values from nibble_consts) the compiler selects
-// one v_and_or_b32 for it -- with literal constants it cannot (a VOP3 takes no literal on
-// this target and at most one SGPR) and emits a separate AND and OR. Written out in C, not
-// as inline asm, so that the compiler also sees the instruction and keeps the wait states
-// an MFMA reading its result needs.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
-struct NibbleConsts {
-  uint32_t mask, bias;  // 0x000F000F, 0x43004300
-};
-__device__ __forceinline__ NibbleConsts nibble_consts() {
-  NibbleConsts k;
-  k.mask = 0x000F000Fu;
-  k.bias = 0x43004300u;
-  asm volatile("" : "+v"(k.mask), "+v"(k.bias));  // (emits nothing: keeps them opaque VGPR values)
-  return k;
 }
 
 // A nibble word (values k .. k + 7) as a B fragment: bf16 128 + v, pairs (i, i + 4).
