@@ -167,6 +167,8 @@ __device__ __forceinline__ NibbleConsts nibble_consts() {
 template <int J, bool NORM>
 __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  // each wave's scale and bias words of its current 4 rows: [wave][row][scale, bias][group]
+  __shared__ __attribute__((aligned(16))) uint16_t sbs[4][4][2][8192 / 64];
   const int layer = blockIdx.x / p.tiles;
   const int tile = blockIdx.x % p.tiles;
   const int K = J * 512, nch = K / 32;
@@ -215,21 +217,26 @@ __global__ __launch_bounds__(kThreads) void qlinear_kernel(QParams p) {
     const u32x4* wr = reinterpret_cast<const u32x4*>(wseg + lrow * (K / 8));
     const uint16_t* sr = sseg + lrow * (K / 64);
     const uint16_t* br = bseg + lrow * (K / 64);
+    // the row's scale and bias words, 16 bytes a lane (groups 8 mc .. + 7; lanes past the
+    // row's K / 512 chunks repeat the last), first: they arrive before the weights
+    const int mc = m < J ? m : J - 1;
+    const u32x4 swd = *reinterpret_cast<const u32x4*>(sr + 8 * mc);
+    const u32x4 bwd = *reinterpret_cast<const u32x4*>(br + 8 * mc);
     u32x4 wv[J];
-    uint16_t sv[J], bv[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = m + 16 * j;
-      wv[j] = __builtin_nontemporal_load(wr + c);
-      sv[j] = sr[c >> 1];
-      bv[j] = br[c >> 1];
-    }
+    for (int j = 0; j < J; ++j) wv[j] = __builtin_nontemporal_load(wr + m + 16 * j);
+    // through this wave's LDS rows (written and read by this wave only: no barrier) to the
+    // lanes that use them: piece m + 16 j is in group m / 2 + 8 j
+    uint16_t* srl = &sbs[wave][lane >> 4][0][0];
+    uint16_t* brl = &sbs[wave][lane >> 4][1][0];
+    *reinterpret_cast<u32x4*>(srl + 8 * mc) = swd;
+    *reinterpret_cast<u32x4*>(brl + 8 * mc) = bwd;
     float y[GDN_QLINEAR_GEMV_ROWS] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int c = m + 16 * j;
-      const float sc = bf2f(sv[j]);
-      const float off = bf2f(bv[j]) - 128.0f * sc;
+      const float sc = bf2f(srl[(m >> 1) + 8 * j]);
+      const float off = bf2f(brl[(m >> 1) + 8 * j]) - 128.0f * sc;
       uint32_t pr[4][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
