@@ -11,7 +11,8 @@
 // Mapping: a workgroup stages its operand in LDS, then each wave takes 4 output rows at a
 // time, one per 16-lane DPP row; lane m of a row reads the row's 16-byte pieces m, m + 16,
 // m + 32, ... (each 32 nibbles = half a group), so a load instruction reads 4 x 256
-// contiguous bytes. A nibble v becomes the bf16 value 128 + v with one and-or
+// contiguous bytes; the rows' scale and bias words come 16 bytes a lane, ahead of the
+// weights, and reach the lanes that use them through the wave's LDS rows. A nibble v becomes the bf16 value 128 + v with one and-or
 // ((w >> 4i) & 0x000F000F | 0x43004300 gives nibbles i and i + 4 of the word as two bf16),
 // v_dot2 multiplies pairs by the operand staged in the same pair order, and scale and
 // bias are applied once per half-group: sum x (q s + b) = s * sum x (128 + q) +
