@@ -16,10 +16,10 @@
 //
 // Three kernels, one stream:
 //   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position: q and k into the
-//                  A-operand fragment planes of Q and K (accurate form) or bf16 rows
-//                  (B, T, Hk, 128) (fast form), and v straight into B-operand fragments in
-//                  the interleaved k order (with q, k, v given by the caller,
-//                  prefill_vfrag reorders v instead). Extra workgroups of the same launch
+//                  fragment planes of Q, K and K^T, and v straight into B-operand fragments
+//                  in the interleaved k order (with q, k, v given by the caller,
+//                  prefill_vfrag reorders v instead and the intra kernel makes Q, K and
+//                  K^T). Extra workgroups of the same launch
 //                  compute the gates and each chunk's cumulative log decay G (one wave per
 //                  (v-head, chunk)).
 //   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
@@ -376,10 +376,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   }
   const bool norm = hh < 2 * p.Hk;
   const bool is_q = hh < p.Hk;
-  __bf16* dst = nullptr;
-  if (is_q) dst = const_cast<__bf16*>(p.q) + ((size_t)b * p.T * p.Hk + hh) * kD;
-  else if (norm) dst = const_cast<__bf16*>(p.k) + ((size_t)b * p.T * p.Hk + (hh - p.Hk)) * kD;
-  const size_t pstride = (size_t)p.Hk * kD;
   // Q, K: channels 4 m .. + 3 are group m % 4 of 32-channel block m / 8, in the group's low
   // (m % 8 < 4) or high half
   auto& qt = *reinterpret_cast<__bf16(*)[kFePos][kD + 8]>(&vtile[wave][0][0]);
@@ -415,7 +411,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
           y1[e] = rbf(y1[e] * scale_b);
         }
       }
-      if (p.qk_frag) {
+      {
         // Q or K to this wave's LDS tile ([position][channel], each 32-channel block in the
         // fragments' interleaved order: channel 32 kb + 4 g + e at 32 kb + 8 g + e and
         // 32 kb + 16 + 4 g + e at 32 kb + 8 g + 4 + e), zeros past T
@@ -423,10 +419,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const bool live = pos < p.T;
         *reinterpret_cast<bf4*>(&qt[tp][qcol]) = live ? bf4_of_rounded(y0) : bf4{};
         *reinterpret_cast<bf4*>(&qt[tp][64 + qcol]) = live ? bf4_of_rounded(y1) : bf4{};
-      } else if (pos < p.T) {
-        __bf16* o = dst + (size_t)pos * pstride;
-        *reinterpret_cast<bf4*>(o + 4 * m) = bf4_of_rounded(y0);
-        *reinterpret_cast<bf4*>(o + 64 + 4 * m) = bf4_of_rounded(y1);
       }
     } else {
       // u holds bf16 values: their high halves go to the tile as they are (a 16-bit store of
@@ -471,7 +463,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         *reinterpret_cast<bf8*>(vf + (2 * (dv >> 4) + 1) * kFrag + lane * 8) = bf8{};
     }
   }
-  if (norm && p.qk_frag) {
+  if (norm) {
     // Q into ws_q, K into ws_kk: fragment block 4 (position tile) + 32-channel block of the
     // chunk, lane 16 g + r holding position r of the tile, channels 4 g .. + 3 and
     // 16 + 4 g .. + 3 of the block (one 16-byte read of the tile); this block is half a
@@ -599,9 +591,9 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
   finish(3, 0, prod(3, 2, -1, 0, prod(3, 0, 1, 0, zero)));
 }
 
-// q, k, v are bf16 (B,T,H,128) -- the caller's, or the front-end kernel's output; with the
-// conv front end in the accurate form, K comes from its fragment plane and q is not read
-// (the front end wrote Q's and K's fragments itself).
+// With the conv front end, Q, K and K^T come from the fragment planes it wrote; with q, k, v
+// given they are the caller's bf16 (B,T,H,128) rows, and this kernel writes Q, K^T (and, in
+// the accurate form, K) in fragment order.
 // ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
 // dead after the first group). Everything it writes for the scan (fast form: Q, K^T, M, U,
 // W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
@@ -625,19 +617,30 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
   // zeroed, so all eight loads are in flight together ----
   {
     constexpr int kIt = kC * kD / 8 / kThreads;
-    bf8 qv[kIt], kv[kIt];
-    const bool load_q = !PRECISE || !p.qk_frag;  // (the front end wrote Q's fragments itself)
-    if (load_q) {
+    bf8 qv[kIt], kv[kIt], ktv[kIt];
+    // With the conv front end, Q, K and K^T come from the fragment planes it wrote (zeros
+    // past T), thread e taking lane e % 64 of block e / 64; otherwise q, k are the caller's
+    // rows. The accurate form needs no Q here once the front end wrote its fragments, the
+    // fast form Q (for K Q^T) and K^T (for W) in LDS.
+    const bool frags = p.qk_frag;
+    const bool load_q = !PRECISE || !frags;
+    if (load_q && frags) {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it)
+        qv[it] = *reinterpret_cast<const bf8*>(p.ws_q + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
+    } else if (load_q) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         qv[it] = *reinterpret_cast<const bf8*>(p.q + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
       }
     }
-    // K: row-major from the front end or the caller, or (conv front end, accurate form)
-    // the fragments the front end wrote into ws_kk (zeros past T), thread e taking lane
-    // e % 64 of block e / 64
-    const bool k_frag = PRECISE && p.qk_frag;
+    const bool k_frag = frags;
+    if (!PRECISE && frags) {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it)
+        ktv[it] = *reinterpret_cast<const bf8*>(p.ws_kt + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
+    }
     if (k_frag) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it)
@@ -659,23 +662,39 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
       gb0 = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
       eg0 = p.ws_g[hc * kGStride + 2 * lane];
     }
-    if (load_q) {
+    // fragment lane (g, r) of block (position tile pt, 32-channel block kb) of Q or K:
+    // position 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3; of K^T's
+    // block (16-channel tile a, half chunk h): channel 16 a + r, positions 32 h + 4 g .. + 3
+    // and 32 h + 16 + 4 g .. + 3
+    auto frag_rows = [&](__bf16 (*m)[kD + kPadB], const bf8 (&v)[kIt]) {
+#pragma unroll
+      for (int it = 0; it < kIt; ++it) {
+        const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
+        const int pos = 16 * (blk >> 2) + (fl & 15), d0 = 32 * (blk & 3) + 4 * (fl >> 4);
+        *reinterpret_cast<bf4*>(&m[pos][d0]) = __builtin_shufflevector(v[it], v[it], 0, 1, 2, 3);
+        *reinterpret_cast<bf4*>(&m[pos][d0 + 16]) = __builtin_shufflevector(v[it], v[it], 4, 5, 6, 7);
+      }
+    };
+    if (load_q && frags) {
+      frag_rows(s.u.fe.q, qv);
+    } else if (load_q) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       }
     }
-    if (k_frag) {
-      // fragment lane (g, r) of block (position tile pt, 32-channel block kb): position
-      // 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3
+    if (!PRECISE && frags) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
-        const int pos = 16 * (blk >> 2) + (fl & 15), d0 = 32 * (blk & 3) + 4 * (fl >> 4);
-        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0]) = __builtin_shufflevector(kv[it], kv[it], 0, 1, 2, 3);
-        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0 + 16]) = __builtin_shufflevector(kv[it], kv[it], 4, 5, 6, 7);
+        const int dk = 16 * (blk >> 1) + (fl & 15), p0 = 32 * (blk & 1) + 4 * (fl >> 4);
+        *reinterpret_cast<bf4*>(&s.kt[dk][p0]) = __builtin_shufflevector(ktv[it], ktv[it], 0, 1, 2, 3);
+        *reinterpret_cast<bf4*>(&s.kt[dk][p0 + 16]) = __builtin_shufflevector(ktv[it], ktv[it], 4, 5, 6, 7);
       }
+    }
+    if (k_frag) {
+      frag_rows(s.u.fe.k, kv);
     } else {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
@@ -706,7 +725,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   {
-    if (!PRECISE || !p.qk_frag) {
+    if (!p.qk_frag) {
       __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -722,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                     reinterpret_cast<bf8*>(wk + (wave * 4 + ks) * kFrag));
       }
     }
-    if (!PRECISE || !p.qk_frag) {  // (else the front end wrote K^T's fragments)
+    if (!p.qk_frag) {  // (else the front end wrote K^T's fragments)
       const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
       for (int q8 = 0; q8 < 4; ++q8) {
@@ -734,7 +753,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   __syncthreads();
-  if (!PRECISE || !p.qk_frag) {
+  if (!p.qk_frag) {
     __bf16* wkt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int a2 = 0; a2 < 2; ++a2)
@@ -1646,12 +1665,12 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, g, vf, fq, fk, gb, m, w, u, us, kk, tp, total;
+  size_t q, kt, g, vf, gb, m, w, u, us, kk, tp, total;
 };
 
-// conv, fast form: the conv front end's bf16 q, k (B,T,Hk,128) are staged in the workspace
-// too (its v goes to vf, which the qkv front end fills from the caller's v); in the accurate
-// form it writes Q and K straight into their fragment planes.
+// The conv front end writes Q, K and K^T straight into their fragment planes and v into vf
+// (the qkv front end fills vf from the caller's v; its Q and K^T come from the intra kernel,
+// and in the accurate form its K too).
 // precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise M, W, U (fp16) and U's scales.
 WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
@@ -1659,22 +1678,20 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
   const size_t wm = al((size_t)B * Hv * nC * kChunkElems * 2);
   const size_t gg = al((size_t)B * Hv * nC * kGStride * 4);
-  const size_t fqk = conv && !precise ? al((size_t)B * T * Hk * kD * 2) : 0;
   WorkspaceLayout L{};
   L.q = 0;
   L.kt = L.q + qk;
   L.g = L.kt + qk;
   L.vf = L.g + gg;
-  L.fq = L.vf + wm;
-  L.fk = L.fq + fqk;
-  L.gb = L.fk + fqk;
+  L.gb = L.vf + wm;
   const size_t end = L.gb + gg;
   if (precise) {
     L.kk = end;
     L.tp = L.kk + qk;
     L.total = L.tp + wm;
   } else {
-    L.m = end;
+    L.kk = end;  // (the conv front end's K fragments; not used with q, k, v given)
+    L.m = L.kk + (conv ? qk : 0);
     L.w = L.m + wm;
     L.u = L.w + wm;
     L.us = L.u + wm;
@@ -1700,7 +1717,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.C = 2 * p.Hk * kD + p.Hv * kD;
   p.nC = (p.T + kC - 1) / kC;
   p.gate_raw = a.gate_mode == GDN_GATES_RAW;
-  p.qk_frag = a.frontend == GDN_FRONTEND_CONV && a.prefill_precision == GDN_PREFILL_ACCURATE;
+  p.qk_frag = a.frontend == GDN_FRONTEND_CONV;
   p.o_bf16 = a.o_dtype == GDN_DTYPE_BF16;
   p.x = static_cast<const uint16_t*>(a.x);
   p.conv_w = static_cast<const uint16_t*>(a.conv_weight);
@@ -1724,8 +1741,8 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
+  p.ws_kk = reinterpret_cast<__bf16*>(w + L.kk);
   if (precise) {
-    p.ws_kk = reinterpret_cast<__bf16*>(w + L.kk);
     p.ws_tp = reinterpret_cast<__bf16*>(w + L.tp);
   } else {
     p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
@@ -1737,10 +1754,8 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
   if (conv) {
-    // (accurate form: the front end writes Q and K into ws_q and ws_kk, no row-major copy)
-    p.q = p.qk_frag ? nullptr : reinterpret_cast<const __bf16*>(w + L.fq);
-    p.k = p.qk_frag ? nullptr : reinterpret_cast<const __bf16*>(w + L.fk);
-    p.v = nullptr;  // the front end writes v straight into ws_vf
+    // the front end writes Q, K and K^T into ws_q, ws_kk and ws_kt and v into ws_vf
+    p.q = p.k = p.v = nullptr;
   }
 
   const dim3 block(kThreads);

@@ -122,26 +122,25 @@ def test_run_rejects_bad_arguments(gdn, kw, msg):
 def test_prefill_workspace_size_and_checks(gdn):
     # per chunk: Q, K^T per k-head (bf16 64 x 128); V in fragment order (bf16) per v-head;
     # two pairs of gate factors per position; 256-byte aligned pieces. The default
-    # (accurate) precision adds K per k-head and T' hi/lo per v-head (its conv front end
-    # writes Q and K straight into their planes); the fast one M hi/lo, W and U (fp16) per
-    # v-head, with one scale per 16-position tile, and with the conv front end its bf16 q, k
-    # staged row by row.
+    # (accurate) precision adds K per k-head and T' hi/lo per v-head; the fast one M hi/lo,
+    # W and U (fp16) per v-head, with one scale per 16-position tile, and with the conv front
+    # end (which writes Q, K and K^T straight into their planes) K per k-head.
     n_qkv = gdn.prefill_workspace_size(1, 4096, conv=False)
     assert n_qkv == 3 * 16 * 64 * 8192 * 2 + 2 * 48 * 64 * 8192 * 2 + 2 * 48 * 64 * 128 * 4
     assert gdn.prefill_workspace_size(1, 4096) == n_qkv
-    # a ragged T: whole chunks for the per-chunk pieces, T rows for the fast form's q, k
-    # staging
+    # a ragged T: whole chunks for the per-chunk pieces
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     nc = (100 + 63) // 64
     assert gdn.prefill_workspace_size(2, 100) == (
         3 * al(2 * 16 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 128 * 4))
     assert gdn.PREFILL_ACCURATE == 0   # a zeroed gdn_layer_args gets the accurate form
     assert gdn.prefill_workspace_size(1, 4096, precision=gdn.PREFILL_FAST) == (
-        gdn.prefill_workspace_size(1, 4096) - 16 * 64 * 8192 * 2 + 2 * 48 * 64 * 8192 * 2 + 48 * 64 * 4 * 4
-        + 4096 * (16 + 16) * 128 * 2)
+        gdn.prefill_workspace_size(1, 4096) + 2 * 48 * 64 * 8192 * 2 + 48 * 64 * 4 * 4)
+    assert gdn.prefill_workspace_size(1, 4096, conv=False, precision=gdn.PREFILL_FAST) == (
+        gdn.prefill_workspace_size(1, 4096, precision=gdn.PREFILL_FAST) - 16 * 64 * 8192 * 2)
     assert gdn.prefill_workspace_size(2, 100, precision=gdn.PREFILL_FAST) == (
-        2 * al(2 * 16 * nc * 8192 * 2) + 4 * al(2 * 48 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 128 * 4)
-        + al(2 * 48 * nc * 4 * 4) + 2 * al(2 * 100 * 16 * 128 * 2))
+        3 * al(2 * 16 * nc * 8192 * 2) + 4 * al(2 * 48 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 128 * 4)
+        + al(2 * 48 * nc * 4 * 4))
     with pytest.raises(gdn.GdnError, match="prefill_precision"):
         gdn.prefill_workspace_size(1, 64, precision=2)
     L = gdn.lib()
