@@ -585,7 +585,6 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(RecurrentParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4, j16 = lane & 15;
   const int T = p.T;
-  constexpr int kWin = kTC + kTaps - 1;  // xp rows feeding one pass
   constexpr int kPer = 2 * kD + kTileRows;  // q, k, v values of one step (FE = 0)
   constexpr int kRaw = (kTC * kPer + kThreads - 1) / kThreads;
 
