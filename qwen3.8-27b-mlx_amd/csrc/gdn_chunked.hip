@@ -252,6 +252,19 @@ __device__ __forceinline__ u16x4 xp_vec4(const PrefillParams& p, int b, int pos,
 
 // ============================================================================ intra
 
+// The accurate form with the conv front end needs neither Q nor K^T nor e^G here: its
+// smaller layout (53.8 KB) leaves room for three workgroups per CU (with one group of
+// v-heads per k-head, in 165 VGPRs).
+struct IntraSmemSlim {
+  float G[kGroup][kC];
+  float beta[kGroup][kC];
+  union {
+    struct {
+      __bf16 k[kC][kD + kPadB];
+    } fe;
+    float nat[kGroup][kC][kC + 4];
+  } u;
+};
 struct IntraSmem {
   __bf16 kt[kD][kC + kPadB];  // K^T [dk][pos]
   float G[kGroup][kC];
@@ -599,9 +612,11 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
 // W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
 // scan that reads it back. (The front end's outputs, which this kernel reads, stay
 // cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
-template <bool ONE_GROUP, bool PRECISE>
-__global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) IntraSmem s;
+// FRAGS: the conv front end wrote the fragment planes (p.qk_frag).
+template <bool ONE_GROUP, bool PRECISE, bool FRAGS>
+__global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) void prefill_intra_kernel(PrefillParams p) {
+  typedef typename std::conditional<PRECISE && FRAGS, IntraSmemSlim, IntraSmem>::type Smem;
+  __shared__ __attribute__((aligned(16))) Smem s;
   const int c = blockIdx.x % p.nC;
   const int rest = blockIdx.x / p.nC;
   const int g = rest % p.Hk;
@@ -622,26 +637,26 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     // past T), thread e taking lane e % 64 of block e / 64; otherwise q, k are the caller's
     // rows. The accurate form needs no Q here once the front end wrote its fragments, the
     // fast form Q (for K Q^T) and K^T (for W) in LDS.
-    const bool frags = p.qk_frag;
-    const bool load_q = !PRECISE || !frags;
-    if (load_q && frags) {
+    constexpr bool frags = FRAGS;
+    constexpr bool load_q = !PRECISE || !frags;
+    if constexpr (load_q && frags) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it)
         qv[it] = *reinterpret_cast<const bf8*>(p.ws_q + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
-    } else if (load_q) {
+    } else if constexpr (load_q) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         qv[it] = *reinterpret_cast<const bf8*>(p.q + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
       }
     }
-    const bool k_frag = frags;
-    if (!PRECISE && frags) {
+    constexpr bool k_frag = frags;
+    if constexpr (!PRECISE && frags) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it)
         ktv[it] = *reinterpret_cast<const bf8*>(p.ws_kt + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
     }
-    if (k_frag) {
+    if constexpr (k_frag) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it)
         kv[it] = *reinterpret_cast<const bf8*>(p.ws_kk + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
@@ -660,7 +675,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     if (wave < gs0) {
       const size_t hc = ((size_t)b * p.Hv + g * p.rep + wave) * p.nC + c;
       gb0 = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
-      eg0 = p.ws_g[hc * kGStride + 2 * lane];
+      if constexpr (!PRECISE) eg0 = p.ws_g[hc * kGStride + 2 * lane];
     }
     // fragment lane (g, r) of block (position tile pt, 32-channel block kb) of Q or K:
     // position 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3; of K^T's
@@ -675,16 +690,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         *reinterpret_cast<bf4*>(&m[pos][d0 + 16]) = __builtin_shufflevector(v[it], v[it], 4, 5, 6, 7);
       }
     };
-    if (load_q && frags) {
+    if constexpr (load_q && frags) {
       frag_rows(s.u.fe.q, qv);
-    } else if (load_q) {
+    } else if constexpr (load_q) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       }
     }
-    if (!PRECISE && frags) {
+    if constexpr (!PRECISE && frags) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
@@ -693,7 +708,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         *reinterpret_cast<bf4*>(&s.kt[dk][p0 + 16]) = __builtin_shufflevector(ktv[it], ktv[it], 4, 5, 6, 7);
       }
     }
-    if (k_frag) {
+    if constexpr (k_frag) {
       frag_rows(s.u.fe.k, kv);
     } else {
 #pragma unroll
@@ -705,7 +720,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     if (wave < gs0) {
       s.G[wave][lane] = gb0.x;
       s.beta[wave][lane] = gb0.y;
-      s.eG[wave][lane] = eg0;
+      if constexpr (!PRECISE) s.eG[wave][lane] = eg0;
     }
   }
   __syncthreads();
@@ -725,7 +740,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   {
-    if (!p.qk_frag) {
+    if constexpr (!FRAGS) {
       __bf16* wq = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -733,7 +748,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                     reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
       }
     }
-    if (PRECISE && !p.qk_frag) {  // K, in the layout of Q, for the scan's K S
+    if constexpr (PRECISE && !FRAGS) {  // K, in the layout of Q, for the scan's K S
       __bf16* wk = p.ws_kk + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -741,7 +756,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
                                     reinterpret_cast<bf8*>(wk + (wave * 4 + ks) * kFrag));
       }
     }
-    if (!p.qk_frag) {  // (else the front end wrote K^T's fragments)
+    if constexpr (!FRAGS) {  // (else the front end wrote K^T's fragments)
       const int dk = tid & (kD - 1), ph = (tid >> 7) * 32;
 #pragma unroll
       for (int q8 = 0; q8 < 4; ++q8) {
@@ -753,7 +768,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
     }
   }
   __syncthreads();
-  if (!p.qk_frag) {
+  if constexpr (!FRAGS) {
     __bf16* wkt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int a2 = 0; a2 < 2; ++a2)
@@ -775,7 +790,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_intra_kernel(PrefillParam
         const float2 gb = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
         s.G[wave][lane] = gb.x;
         s.beta[wave][lane] = gb.y;
-        s.eG[wave][lane] = p.ws_g[hc * kGStride + 2 * lane];
+        if constexpr (!PRECISE) s.eG[wave][lane] = p.ws_g[hc * kGStride + 2 * lane];
       }
       __syncthreads();
     }
@@ -1776,13 +1791,14 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
     hipLaunchKernelGGL(prefill_vfrag_kernel, gv, block, 0, stream, p);
   }
   mark(1);
-  if (p.rep <= kGroup) {
-    if (precise) hipLaunchKernelGGL((prefill_intra_kernel<true, true>), g1, block, 0, stream, p);
-    else hipLaunchKernelGGL((prefill_intra_kernel<true, false>), g1, block, 0, stream, p);
-  } else {
-    if (precise) hipLaunchKernelGGL((prefill_intra_kernel<false, true>), g1, block, 0, stream, p);
-    else hipLaunchKernelGGL((prefill_intra_kernel<false, false>), g1, block, 0, stream, p);
-  }
+  // <one group of v-heads per k-head, precision, the front end's fragment planes>
+#define GDN_INTRA(og, pr, fr) hipLaunchKernelGGL((prefill_intra_kernel<og, pr, fr>), g1, block, 0, stream, p)
+  const bool one = p.rep <= kGroup, fr = p.qk_frag != 0;
+  if (one && precise) { if (fr) GDN_INTRA(true, true, true); else GDN_INTRA(true, true, false); }
+  else if (one) { if (fr) GDN_INTRA(true, false, true); else GDN_INTRA(true, false, false); }
+  else if (precise) { if (fr) GDN_INTRA(false, true, true); else GDN_INTRA(false, true, false); }
+  else { if (fr) GDN_INTRA(false, false, true); else GDN_INTRA(false, false, false); }
+#undef GDN_INTRA
   mark(2);
   const dim3 sb(64 * (kScanNt + 2));
   if (p.o_bf16) {
