@@ -608,8 +608,8 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
 // given they are the caller's bf16 (B,T,H,128) rows, and this kernel writes Q, K^T (and, in
 // the accurate form, K) in fragment order.
 // ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
-// dead after the first group). Everything it writes for the scan (fast form: Q, K^T, M, U,
-// W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
+// dead after the first group). Everything it writes for the scan (fast form from the
+// caller's rows: Q, K^T, M, U, W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
 // scan that reads it back. (The front end's outputs, which this kernel reads, stay
 // cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
 // FRAGS: the conv front end wrote the fragment planes (p.qk_frag).
@@ -628,8 +628,9 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
   const int fr = lane & 15, fk = (lane >> 4) * 8, lg = lane >> 4;
   const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
 
-  // ---- q, k of the chunk into LDS (bf16); rows past the end read the last row and are
-  // zeroed, so all eight loads are in flight together ----
+  // ---- Q, K (and, in the fast form from fragment planes, K^T) of the chunk into LDS
+  // (bf16); caller rows past the end read the last row and are zeroed, so all the loads are
+  // in flight together ----
   {
     constexpr int kIt = kC * kD / 8 / kThreads;
     bf8 qv[kIt], kv[kIt], ktv[kIt];
@@ -725,8 +726,9 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
   }
   __syncthreads();
 
-  // ---- K K^T and (fast form) K Q^T on MFMA (wave w: rows j = 16w..; kept in registers), Q
-  // to the workspace, K^T into LDS ----
+  // ---- K K^T and (fast form) K Q^T on MFMA (wave w: rows j = 16w..; kept in registers);
+  // from the caller's rows, also Q (and, accurate form, K) to the workspace and K^T through
+  // LDS to the workspace ----
   f4 gr[4], kq[4];  // lane: (j = 16 wave + 4 lg + e, i = 16 ct + fr): (K K^T)_ji, (Q K^T)_ij
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
