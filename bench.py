@@ -618,7 +618,7 @@ def main() -> int:
                   f"intra {ki['event_us']:.1f} us (MFMA {ki['frac_mfma_normative_event']:.4f} normative, "
                   f"{ki['frac_mfma_executed_event']:.4f} executed), scan {ks['event_us']:.1f} us "
                   f"({ks['frac_mfma_executed_event']:.4f} executed)", flush=True)
-        # the fast form (GDN_PREFILL_FAST: bf16 V'' in the state update, U as fp16) beside it
+        # the fast form (GDN_PREFILL_FAST: bf16 S, T' and V'' in the state products) beside it
         rf = bench_prefill(torch, gdn, dev, timer, steps=max(5, args.steps // 10), warmup=3, precision=1)
         sec["prefill_t4096_fast"] = dict(us_per_call=round(rf["us_per_call"], 2),
                                          tokens_per_s=round(rf["tokens_per_s"], 1),

@@ -84,9 +84,10 @@ typedef enum gdn_prefill_precision {
                                split for K^T V'' -- so the state the next window or decode
                                step starts from is within about 1e-5 (max|a-b|/max|b|;
                                measured 3e-6..8e-6) of the fp32 recurrence whatever the
-                               gates; the smaller workspace */
-  GDN_PREFILL_FAST = 1      /* bf16 operands in the state products and U kept as fp16: the
-                               state ends about 2e-3 from the fp32 recurrence; about 0.9 of
+                               gates */
+  GDN_PREFILL_FAST = 1      /* the same V' with bf16 S, T' and V'' (X alone split), and M V'
+                               on bf16 operands: the state ends about 2e-3 to 4e-3 from the
+                               fp32 recurrence, the outputs within about 6e-3; about 0.85 of
                                the time at T = 4096 */
 } gdn_prefill_precision;
 
@@ -167,10 +168,9 @@ int gdn_prefill_chunked(const gdn_layer_args* args);
  * benchmarks that report each kernel's share of the MFMA peak). */
 int gdn_prefill_chunked_timed(const gdn_layer_args* args, float* kernel_ms);
 
-/* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len, head
- * counts, front end (with GDN_PREFILL_FAST the conv front end also stages its bf16 q, k
- * rows in the workspace) and prefill_precision (GDN_PREFILL_ACCURATE keeps K and T' per
- * chunk, GDN_PREFILL_FAST M, W and U); the other fields are not read. */
+/* Workspace bytes gdn_prefill_chunked needs for these arguments' batch, seq_len and head
+ * counts (per chunk: Q, K, K^T, V, T' and the gate factors; the same for both front ends
+ * and both precisions; prefill_precision is checked); the other fields are not read. */
 int gdn_prefill_workspace_size(const gdn_layer_args* args, size_t* bytes);
 
 typedef struct gdn_commit_args {

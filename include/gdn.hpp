@@ -108,7 +108,7 @@ class DeltaCache {
   // 1024, cpp/src/session.hpp:136) run the chunked form in a workspace allocated here, with
   // `prefill_precision` (gdn_prefill_precision: GDN_PREFILL_ACCURATE, the default, leaves the
   // state the next decode step starts from within about 1e-5 of the fp32 recurrence,
-  // GDN_PREFILL_FAST about 2e-3 in about 0.9 of the time); max_prefill_tokens = 0
+  // GDN_PREFILL_FAST about 2e-3 to 4e-3 in about 0.85 of the time); max_prefill_tokens = 0
   // keeps every block on the exact recurrent kernel.
   DeltaCache(const LayerParams& p, int batch, int max_record_steps, int max_prefill_tokens = 0,
              int prefill_precision = GDN_PREFILL_ACCURATE)

@@ -16,7 +16,7 @@
 
 namespace gdn {
 int recurrent_tile_rows(long long heads);
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv, bool precise);
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv);
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
                                   hipEvent_t* events);
 }  // namespace gdn
@@ -366,9 +366,7 @@ int gdn_prefill_workspace_size(const gdn_layer_args* a, size_t* bytes) {
     return fail(GDN_EINVAL, "gdn_prefill_workspace_size: bad shape");
   if (a->prefill_precision != GDN_PREFILL_FAST && a->prefill_precision != GDN_PREFILL_ACCURATE)
     return fail(GDN_EINVAL, "gdn_prefill_workspace_size: unknown prefill_precision %d", a->prefill_precision);
-  *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads,
-                                        a->frontend == GDN_FRONTEND_CONV,
-                                        a->prefill_precision == GDN_PREFILL_ACCURATE);
+  *bytes = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
   return ok();
 }
 
@@ -386,9 +384,7 @@ int prefill_validate(const gdn_layer_args* a) {
   if (a->frontend == GDN_FRONTEND_QKV && (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16)))
     return fail(GDN_EINVAL, "gdn_prefill_chunked: q, k and v must be 16-byte aligned");
   if (!aligned(a->o, 16)) return fail(GDN_EINVAL, "gdn_prefill_chunked: o must be 16-byte aligned");
-  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads,
-                                                   a->frontend == GDN_FRONTEND_CONV,
-                                                   a->prefill_precision == GDN_PREFILL_ACCURATE);
+  const size_t need = gdn::prefill_workspace_bytes(a->batch, a->seq_len, a->num_k_heads, a->num_v_heads);
   if (a->seq_len > 0) {
     if (!a->workspace || a->workspace_bytes < need)
       return fail(GDN_EINVAL, "gdn_prefill_chunked: workspace of %zu bytes required (got %zu)", need,

@@ -10,9 +10,10 @@
 //   y  = e^G . (Q S) + M V'                              (= MU0 + Qeff S)
 //   S  = e^{G_63} S + K^T (e^{G_63 - G} . V')
 //
-// GDN_PREFILL_FAST runs exactly this. GDN_PREFILL_ACCURATE forms the same V' as
+// Both precisions form V' as
 //   V' = T' (V - e^G . (K S))                            (= U - W S)
-// with the state products at fp32 accuracy (below), so W and U are never formed.
+// so that W and U are never formed; they differ in which products carry their operands
+// as bf16 hi + lo (below).
 //
 // Three kernels, one stream:
 //   prefill_frontend  conv + SiLU (+ l2norm, q scale) of every position: q and k into the
@@ -22,30 +23,28 @@
 //                  K^T). Extra workgroups of the same launch
 //                  compute the gates and each chunk's cumulative log decay G (one wave per
 //                  (v-head, chunk)).
-//   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, two
-//                  per CU: K K^T (and, fast form, K Q^T) on bf16 MFMA, and for the
-//                  k-head's v-heads A (and M), T = (I + A)^-1 (one wave per v-head, fp32,
-//                  left in LDS), then each wave's T' fragments from T in LDS: stored split
-//                  into bf16 hi + lo (accurate form), or used for U = T'V and
-//                  W = T'diag(e^G)K on bf16 MFMA (fast form; U stored as fp16 scaled by a
-//                  power of two per 16-position tile). Results go to the workspace, already
-//                  in the register order of the MFMA operands that read them.
+//   prefill_intra  one workgroup per (batch, k-head, chunk), all chunks in parallel, three
+//                  per CU (two with q, k, v given): K K^T on bf16 MFMA, and for the
+//                  k-head's v-heads A, T = (I + A)^-1 (one wave per v-head, fp32, left in
+//                  LDS), then each wave's T' fragments from T in LDS, stored as bf16 hi
+//                  (and, accurate form, lo) in the register order of the MFMA operands
+//                  that read them.
 //   prefill_scan   one workgroup per (batch, v-head, pair of 16-column Dv tiles), serial
 //                  over the chunks. Each of two state waves keeps its tile's fp32 state
-//                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain (fast: V' =
-//                  U - W S; accurate: K S, X = V - e^G K S, V' = T' X), S = e^G63 S +
-//                  K^T V'' with every operand in registers; two output waves (position
+//                  (Dk 128 x Dv 16) in MFMA accumulators and runs the chain (K S,
+//                  X = V - e^G K S, V' = T' X), S = e^G63 S + K^T V'' with every operand
+//                  in registers; two output waves (position
 //                  tiles {0, 3} and {1, 2} of a chunk) run one chunk behind on the S and V'
 //                  that the state waves leave in a double-buffered LDS mailbox: one barrier
 //                  per chunk. Operands go from the workspace straight into registers two
 //                  chunks ahead of their use, and the output waves touch the lines of the
-//                  chunk four ahead so that they are in L2 when first asked for. Fast form:
-//                  W S, Q S and K^T V'' use bf16 operands, M V' splits both operands into
-//                  bf16 hi + lo (three MFMAs), and M comes from the intra kernel. Accurate
-//                  form: S is split into bf16 hi + lo for K S (K is exact in bf16), X and T'
-//                  for T' X (three MFMAs), V'' for K^T V'' (two MFMAs), so that the state
-//                  follows the fp32 recurrence to about 1e-5 instead of 2e-3, and the
-//                  output waves build M from the chunk's K and Q.
+//                  chunk four ahead so that they are in L2 when first asked for. The
+//                  output waves build M from the chunk's K and Q. Fast form: K S, Q S,
+//                  M V' and K^T V'' use bf16 operands and T' X splits X into bf16 hi + lo
+//                  (two MFMAs). Accurate form: S is also split for K S (K is exact in
+//                  bf16), T' for T' X (three MFMAs), V'' for K^T V'' (two MFMAs), and M
+//                  and V' for M V' (three), so that the state follows the fp32 recurrence
+//                  to about 1e-5 instead of 4e-3.
 //
 // MFMA: v_mfma_f32_16x16x32_bf16. Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16]
 // and C[4(l/16)+i][l%16] (i < 8, 8, 4). LDS matrices are stored so that both operands
@@ -176,6 +175,7 @@ struct PrefillParams {
   int B, T, Hk, Hv, rep, C, nC;
   int gate_raw, o_bf16;
   int qk_frag;  // the conv front end writes Q, K and K^T straight into ws_q, ws_kk, ws_kt
+  int tp_lo;    // T' carried as bf16 hi + lo (GDN_PREFILL_ACCURATE), else hi only
   const uint16_t* x;
   const uint16_t* conv_w;
   const uint16_t* conv_in;
@@ -193,25 +193,17 @@ struct PrefillParams {
   float* state_out;
   void* o;
   // workspace, per chunk
-  // (Q, K^T, W and M in fragment order with the interleaved k order)
+  // (Q, K, K^T and T' in fragment order with the interleaved k order)
   __bf16* ws_q;   // (B, Hk, nC): Q   (64 x 128)
   __bf16* ws_kt;  // (B, Hk, nC): K^T (128 x 64)
-  __bf16* ws_m;   // (B, Hv, nC): M   (64 x 64), hi and lo blocks alternating (the two
-                  // blocks above the diagonal are left unwritten)
-  // GDN_PREFILL_FAST: the chunk's U and W
-  __bf16* ws_w;   // (B, Hv, nC): W   (64 x 128)
-  _Float16* ws_u; // (B, Hv, nC): U (64 x 128) as MFMA result tiles [dv tile][pos tile][lane][4],
-                  // fp16 with each position tile multiplied by a power of two (below)
-  float* ws_us;   // (B, Hv, nC, 4): 1 / that power of two per position tile
-  // GDN_PREFILL_ACCURATE: K and T' instead, so that the scan forms V' = T' (V - e^G K S)
   __bf16* ws_kk;  // (B, Hk, nC): K   (64 x 128), as Q
-  __bf16* ws_tp;  // (B, Hv, nC): T' = (I + A)^-1 diag(beta) (64 x 64) split into bf16 hi + lo,
-                  // laid out as M
+  __bf16* ws_tp;  // (B, Hv, nC): T' = (I + A)^-1 diag(beta) (64 x 64) in 16 x 32 blocks, bf16
+                  // hi and lo blocks alternating (lo written with tp_lo only; the two blocks
+                  // above the diagonal are left unwritten)
   float* ws_g;    // (B, Hv, nC, kGStride): (e^G, e^(G63-G)) per position (e^G63 = e^G at 63)
   float* ws_gb;   // (B, Hv, nC, kGStride): (G, beta) per position
   __bf16* ws_vf;  // (B, Hv, nC): V (64 x 128) as B operand fragments in the interleaved k order
-                  // (the B operand of U = T' V, and two accumulator tiles of the scan's
-                  // V - e^G K S): block 2 (dv / 16) + pos / 32, lane 16 g + dv % 16 with
+                  // (two accumulator tiles of the scan's V - e^G K S): block 2 (dv / 16) + pos / 32, lane 16 g + dv % 16 with
                   // g = (pos % 16) / 4, element (pos % 4) + 4 ((pos % 32) / 16); positions
                   // past T are zeros
 };
@@ -252,7 +244,7 @@ __device__ __forceinline__ u16x4 xp_vec4(const PrefillParams& p, int b, int pos,
 
 // ============================================================================ intra
 
-// The accurate form with the conv front end needs neither Q nor K^T nor e^G here: its
+// With the conv front end's fragment planes the kernel needs neither Q nor K^T in LDS: the
 // smaller layout (53.8 KB) leaves room for three workgroups per CU (with one group of
 // v-heads per k-head, in 165 VGPRs).
 struct IntraSmemSlim {
@@ -269,7 +261,6 @@ struct IntraSmem {
   __bf16 kt[kD][kC + kPadB];  // K^T [dk][pos]
   float G[kGroup][kC];
   float beta[kGroup][kC];
-  float eG[kGroup][kC];  // e^G
   union {
     struct {
       __bf16 q[kC][kD + kPadB];
@@ -604,18 +595,18 @@ __device__ __forceinline__ void invert_blocked(float (*nat)[kC + 4], int lane) {
   finish(3, 0, prod(3, 2, -1, 0, prod(3, 0, 1, 0, zero)));
 }
 
-// With the conv front end, Q, K and K^T come from the fragment planes it wrote; with q, k, v
-// given they are the caller's bf16 (B,T,H,128) rows, and this kernel writes Q, K^T (and, in
-// the accurate form, K) in fragment order.
-// ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T / Q K^T registers are then
-// dead after the first group). Everything it writes for the scan (fast form from the
-// caller's rows: Q, K^T, M, U, W, 224 MB at T = 4096) is stored non-temporally: T = 4096 took 62 -> 54 us here and 110 -> 94 us in the
-// scan that reads it back. (The front end's outputs, which this kernel reads, stay
+// With the conv front end, K comes from the fragment plane it wrote; with q, k, v given they
+// are the caller's bf16 (B,T,H,128) rows, and this kernel writes Q, K and K^T in fragment
+// order.
+// ONE_GROUP: the k-head has at most kGroup v-heads (the K K^T registers are then dead after
+// the first group). Everything it writes for the scan is stored non-temporally (on an
+// earlier form that wrote 224 MB at T = 4096 this took 62 -> 54 us here and 110 -> 94 us in
+// the scan that reads it back). (The front end's outputs, which this kernel reads, stay
 // cached: storing them non-temporally made this kernel slower, 54 -> 67 us.)
 // FRAGS: the conv front end wrote the fragment planes (p.qk_frag).
-template <bool ONE_GROUP, bool PRECISE, bool FRAGS>
-__global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) void prefill_intra_kernel(PrefillParams p) {
-  typedef typename std::conditional<PRECISE && FRAGS, IntraSmemSlim, IntraSmem>::type Smem;
+template <bool ONE_GROUP, bool FRAGS>
+__global__ __launch_bounds__(kThreads, ONE_GROUP && FRAGS ? 3 : 2) void prefill_intra_kernel(PrefillParams p) {
+  typedef typename std::conditional<FRAGS, IntraSmemSlim, IntraSmem>::type Smem;
   __shared__ __attribute__((aligned(16))) Smem s;
   const int c = blockIdx.x % p.nC;
   const int rest = blockIdx.x / p.nC;
@@ -628,36 +619,21 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
   const int fr = lane & 15, fk = (lane >> 4) * 8, lg = lane >> 4;
   const size_t gc = ((size_t)b * p.Hk + g) * p.nC + c;
 
-  // ---- Q, K (and, in the fast form from fragment planes, K^T) of the chunk into LDS
-  // (bf16); caller rows past the end read the last row and are zeroed, so all the loads are
-  // in flight together ----
+  // ---- K (and, from the caller's rows, Q) of the chunk into LDS (bf16); caller rows past
+  // the end read the last row and are zeroed, so all the loads are in flight together ----
   {
     constexpr int kIt = kC * kD / 8 / kThreads;
-    bf8 qv[kIt], kv[kIt], ktv[kIt];
-    // With the conv front end, Q, K and K^T come from the fragment planes it wrote (zeros
-    // past T), thread e taking lane e % 64 of block e / 64; otherwise q, k are the caller's
-    // rows. The accurate form needs no Q here once the front end wrote its fragments, the
-    // fast form Q (for K Q^T) and K^T (for W) in LDS.
-    constexpr bool frags = FRAGS;
-    constexpr bool load_q = !PRECISE || !frags;
-    if constexpr (load_q && frags) {
-#pragma unroll
-      for (int it = 0; it < kIt; ++it)
-        qv[it] = *reinterpret_cast<const bf8*>(p.ws_q + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
-    } else if constexpr (load_q) {
+    bf8 qv[kIt], kv[kIt];
+    // With the conv front end, K comes from the fragment plane it wrote (zeros past T),
+    // thread e taking lane e % 64 of block e / 64; otherwise q, k are the caller's rows.
+    if constexpr (!FRAGS) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         qv[it] = *reinterpret_cast<const bf8*>(p.q + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
       }
     }
-    constexpr bool k_frag = frags;
-    if constexpr (!PRECISE && frags) {
-#pragma unroll
-      for (int it = 0; it < kIt; ++it)
-        ktv[it] = *reinterpret_cast<const bf8*>(p.ws_kt + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
-    }
-    if constexpr (k_frag) {
+    if constexpr (FRAGS) {
 #pragma unroll
       for (int it = 0; it < kIt; ++it)
         kv[it] = *reinterpret_cast<const bf8*>(p.ws_kk + gc * kChunkElems + (size_t)(tid + it * kThreads) * 8);
@@ -668,50 +644,30 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
         kv[it] = *reinterpret_cast<const bf8*>(p.k + (((size_t)b * p.T + t0 + min(pos, n - 1)) * p.Hk + g) * kD + d8);
       }
     }
-    // the first group's (G, beta, e^G), written by the front end's gate workgroups: wave r
-    // takes v-head r, lane = position (loaded behind q and k, so their waits come first)
+    // the first group's (G, beta), written by the front end's gate workgroups: wave r takes
+    // v-head r, lane = position (loaded behind q and k, so their waits come first)
     const int gs0 = min(kGroup, p.rep);
     float2 gb0 = make_float2(0.0f, 0.0f);
-    float eg0 = 0.0f;
     if (wave < gs0) {
       const size_t hc = ((size_t)b * p.Hv + g * p.rep + wave) * p.nC + c;
       gb0 = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
-      if constexpr (!PRECISE) eg0 = p.ws_g[hc * kGStride + 2 * lane];
     }
-    // fragment lane (g, r) of block (position tile pt, 32-channel block kb) of Q or K:
-    // position 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3; of K^T's
-    // block (16-channel tile a, half chunk h): channel 16 a + r, positions 32 h + 4 g .. + 3
-    // and 32 h + 16 + 4 g .. + 3
-    auto frag_rows = [&](__bf16 (*m)[kD + kPadB], const bf8 (&v)[kIt]) {
+    if constexpr (FRAGS) {
+      // fragment lane (g, r) of block (position tile pt, 32-channel block kb) of K: position
+      // 16 pt + r, channels 32 kb + 4 g .. + 3 and 32 kb + 16 + 4 g .. + 3
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
         const int pos = 16 * (blk >> 2) + (fl & 15), d0 = 32 * (blk & 3) + 4 * (fl >> 4);
-        *reinterpret_cast<bf4*>(&m[pos][d0]) = __builtin_shufflevector(v[it], v[it], 0, 1, 2, 3);
-        *reinterpret_cast<bf4*>(&m[pos][d0 + 16]) = __builtin_shufflevector(v[it], v[it], 4, 5, 6, 7);
+        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0]) = __builtin_shufflevector(kv[it], kv[it], 0, 1, 2, 3);
+        *reinterpret_cast<bf4*>(&s.u.fe.k[pos][d0 + 16]) = __builtin_shufflevector(kv[it], kv[it], 4, 5, 6, 7);
       }
-    };
-    if constexpr (load_q && frags) {
-      frag_rows(s.u.fe.q, qv);
-    } else if constexpr (load_q) {
+    } else {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
         *reinterpret_cast<bf8*>(&s.u.fe.q[pos][d8]) = pos < n ? qv[it] : bf8{};
       }
-    }
-    if constexpr (!PRECISE && frags) {
-#pragma unroll
-      for (int it = 0; it < kIt; ++it) {
-        const int e = tid + it * kThreads, blk = e >> 6, fl = e & 63;
-        const int dk = 16 * (blk >> 1) + (fl & 15), p0 = 32 * (blk & 1) + 4 * (fl >> 4);
-        *reinterpret_cast<bf4*>(&s.kt[dk][p0]) = __builtin_shufflevector(ktv[it], ktv[it], 0, 1, 2, 3);
-        *reinterpret_cast<bf4*>(&s.kt[dk][p0 + 16]) = __builtin_shufflevector(ktv[it], ktv[it], 4, 5, 6, 7);
-      }
-    }
-    if constexpr (k_frag) {
-      frag_rows(s.u.fe.k, kv);
-    } else {
 #pragma unroll
       for (int it = 0; it < kIt; ++it) {
         const int e = tid + it * kThreads, pos = e / (kD / 8), d8 = (e % (kD / 8)) * 8;
@@ -721,25 +677,19 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
     if (wave < gs0) {
       s.G[wave][lane] = gb0.x;
       s.beta[wave][lane] = gb0.y;
-      if constexpr (!PRECISE) s.eG[wave][lane] = eg0;
     }
   }
   __syncthreads();
 
-  // ---- K K^T and (fast form) K Q^T on MFMA (wave w: rows j = 16w..; kept in registers);
-  // from the caller's rows, also Q (and, accurate form, K) to the workspace and K^T through
-  // LDS to the workspace ----
-  f4 gr[4], kq[4];  // lane: (j = 16 wave + 4 lg + e, i = 16 ct + fr): (K K^T)_ji, (Q K^T)_ij
+  // ---- K K^T on MFMA (wave w: rows j = 16w..; kept in registers); from the caller's rows,
+  // also Q and K to the workspace and K^T through LDS to the workspace ----
+  f4 gr[4];  // lane: (j = 16 wave + 4 lg + e, i = 16 ct + fr): (K K^T)_ji
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     gr[ct] = f4{0.f, 0.f, 0.f, 0.f};
-    kq[ct] = gr[ct];
 #pragma unroll
-    for (int ks = 0; ks < kD / 32; ++ks) {
-      const bf8 ak = frag(s.u.fe.k, 16 * wave + fr, 32 * ks + fk);
-      gr[ct] = mfma(ak, frag(s.u.fe.k, 16 * ct + fr, 32 * ks + fk), gr[ct]);
-      if constexpr (!PRECISE) kq[ct] = mfma(ak, frag(s.u.fe.q, 16 * ct + fr, 32 * ks + fk), kq[ct]);
-    }
+    for (int ks = 0; ks < kD / 32; ++ks)
+      gr[ct] = mfma(frag(s.u.fe.k, 16 * wave + fr, 32 * ks + fk), frag(s.u.fe.k, 16 * ct + fr, 32 * ks + fk), gr[ct]);
   }
   {
     if constexpr (!FRAGS) {
@@ -750,7 +700,7 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
                                     reinterpret_cast<bf8*>(wq + (wave * 4 + ks) * kFrag));
       }
     }
-    if constexpr (PRECISE && !FRAGS) {  // K, in the layout of Q, for the scan's K S
+    if constexpr (!FRAGS) {  // K, in the layout of Q, for the scan's K S
       __bf16* wk = p.ws_kk + gc * kChunkElems + lane * 8;
 #pragma unroll
       for (int ks = 0; ks < kD / 32; ++ks) {
@@ -786,46 +736,29 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
   const int rep_end = ONE_GROUP ? 1 : p.rep;
   for (int r0 = 0; r0 < rep_end; r0 += kGroup) {
     const int gs = min(kGroup, p.rep - r0);
-    if (!ONE_GROUP && r0 > 0) {  // a later group's (G, beta, e^G) (the first came with q, k)
+    if (!ONE_GROUP && r0 > 0) {  // a later group's (G, beta) (the first came with q, k)
       if (wave < gs) {
         const size_t hc = ((size_t)b * p.Hv + g * p.rep + r0 + wave) * p.nC + c;
         const float2 gb = reinterpret_cast<const float2*>(p.ws_gb + hc * kGStride)[lane];
         s.G[wave][lane] = gb.x;
         s.beta[wave][lane] = gb.y;
-        if constexpr (!PRECISE) s.eG[wave][lane] = p.ws_g[hc * kGStride + 2 * lane];
       }
       __syncthreads();
     }
 
-    // A (into LDS as -A^T) and, in the fast form, M (hi, lo to the workspace; the accurate
-    // form's scan builds M itself) from the registers
+    // A (into LDS as -A^T) from the registers (the scan builds M itself)
     for (int r = 0; r < gs; ++r) {
-      const size_t hc = ((size_t)b * p.Hv + g * p.rep + r0 + r) * p.nC + c;
-      __bf16* wm = PRECISE ? nullptr : p.ws_m + hc * kChunkElems;
       const int j0 = 16 * wave + 4 * lg;
       const f4 Gj = *reinterpret_cast<const f4*>(&s.G[r][j0]);
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         const int i = 16 * ct + fr;
         const float Gi = s.G[r][i], bi = s.beta[r][i];
-        f4 mv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = j0 + e;
           const float dr = j <= i ? fast_exp(Gi - Gj[e]) : 0.0f;
-          mv[e] = dr * kq[ct][e];
           s.u.nat[r][j][i] = j < i ? -((bi * dr) * gr[ct][e]) : 0.0f;
-        }
-        if constexpr (PRECISE) continue;
-        bf4 hi, lo;
-        split_bf4(mv, hi, lo);
-        // M row i, columns j0..j0+3; block (i / 16, j / 32), hi and lo blocks alternating.
-        // Blocks (0, 1) and (1, 1) lie above the diagonal: zero, neither stored nor read.
-        const int off = ilv_off(i, j0, 2);
-        const int blk = off / kFrag, within = off % kFrag;
-        if (ct >= 2 || wave < 2) {
-          __builtin_nontemporal_store(hi, reinterpret_cast<bf4*>(wm + 2 * blk * kFrag + within));
-          __builtin_nontemporal_store(lo, reinterpret_cast<bf4*>(wm + (2 * blk + 1) * kFrag + within));
         }
       }
     }
@@ -857,92 +790,18 @@ __global__ __launch_bounds__(kThreads, ONE_GROUP && PRECISE && FRAGS ? 3 : 2) vo
           tv[4 + e] = x1[e] * b1[e];
         }
       };
-      if constexpr (PRECISE) {
-        // T' split into bf16 hi + lo, blocks (wave, kh) with kh <= wave / 2 (the others are
-        // zero), in the layout of M
-        __bf16* wt = p.ws_tp + hc * kChunkElems + lane * 8;
+      // T' split into bf16 hi + lo (lo stored with tp_lo only), blocks (wave, kh) with
+      // kh <= wave / 2 (the others are zero)
+      __bf16* wt = p.ws_tp + hc * kChunkElems + lane * 8;
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          if (2 * kh > wave) continue;
-          float tv[8];
-          tprime(kh, tv);
-          bf8 th, tl;
-          split_bf8(f4{tv[0], tv[1], tv[2], tv[3]}, f4{tv[4], tv[5], tv[6], tv[7]}, th, tl);
-          __builtin_nontemporal_store(th, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2) * kFrag));
-          __builtin_nontemporal_store(tl, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2 + 1) * kFrag));
-        }
-      } else {
-      // V: the B operand of U, straight from the workspace (a half chunk wholly past T was
-      // never written: zeros)
-      bf8 vb[kD / 16][2];
-      {
-        const __bf16* vf = p.ws_vf + hc * kChunkElems + lane * 8;
-#pragma unroll
-        for (int d = 0; d < kD / 16; ++d)
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
-            vb[d][kh] = 32 * kh < n ? *reinterpret_cast<const bf8*>(vf + (2 * d + kh) * kFrag) : bf8{};
-      }
-      // U = T' V and W^T = K^T (T' e^G)^T: wave w takes position tile w (rows i = 16 w + fr
-      // of T'), all eight dv tiles of U and all eight dk tiles of W; T' split into hi + lo for U
-      {
-        bf8 ah[2], al[2], te[2];
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          float tv[8];
-          tprime(kh, tv);
-          const f4 e0 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 4 * lg]);
-          const f4 e1 = *reinterpret_cast<const f4*>(&s.eG[r][32 * kh + 16 + 4 * lg]);
-          split_bf8(f4{tv[0], tv[1], tv[2], tv[3]}, f4{tv[4], tv[5], tv[6], tv[7]}, ah[kh], al[kh]);
-          te[kh] = stack_bf8(f4{tv[0], tv[1], tv[2], tv[3]} * e0, f4{tv[4], tv[5], tv[6], tv[7]} * e1);
-        }
-        f4 ut[kD / 16];
-#pragma unroll
-        for (int d = 0; d < kD / 16; ++d) {
-          f4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mfma(ah[0], vb[d][0], acc);
-          acc = mfma(al[0], vb[d][0], acc);
-          acc = mfma(ah[1], vb[d][1], acc);
-          acc = mfma(al[1], vb[d][1], acc);
-          ut[d] = acc;
-        }
-        // U stored as fp16 times 2^e, e from the position tile's largest magnitude (so
-        // |U| 2^e < 2^15, inside fp16's range whatever the inputs); 2^-e goes to ws_us
-        uint32_t mx = 0;
-#pragma unroll
-        for (int d = 0; d < kD / 16; ++d)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mx = max(mx, f_bits(ut[d][e]) & 0x7fffffffu);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
-        const int ex = min(100, max(-100, 141 - (int)(mx >> 23)));  // |U| < 2^((mx >> 23) - 126)
-        const float sc = bits_f((uint32_t)(127 + ex) << 23);
-        _Float16* wu = p.ws_u + hc * kChunkElems + lane * 4;
-#pragma unroll
-        for (int d = 0; d < kD / 16; ++d)
-          __builtin_nontemporal_store(__builtin_convertvector(ut[d] * sc, h4),
-                                      reinterpret_cast<h4*>(wu + (d * 4 + wave) * 256));
-        if (lane == 0) p.ws_us[hc * 4 + wave] = bits_f((uint32_t)(127 - ex) << 23);
-        // lane gets W[i = 16 wave + fr][dk = 16 a + 4 lg .. +3]. Tiles a and a + 1 (a even)
-        // fill the two halves of the same 16-byte piece of the fragment order (the
-        // interleaved k order), so each pair is stored as one piece: every store writes 1 KB
-        // of whole lines (8-byte halves written apart were partial-line writes).
-        __bf16* ww = p.ws_w + hc * kChunkElems;
-#pragma unroll
-        for (int a = 0; a < kD / 16; a += 2) {
-          f4 acc[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            acc[h] = f4{0.f, 0.f, 0.f, 0.f};
-            acc[h] = mfma(frag_ilv(s.kt, 16 * (a + h) + fr, 0, lg), te[0], acc[h]);
-            acc[h] = mfma(frag_ilv(s.kt, 16 * (a + h) + fr, 32, lg), te[1], acc[h]);
-          }
-          const bf4 w0 = to_bf4(acc[0]), w1 = to_bf4(acc[1]);
-          const int off = ilv_off(16 * wave + fr, 16 * a + 4 * lg, kD / 32);
-          __builtin_nontemporal_store(__builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7),
-                                      reinterpret_cast<bf8*>(ww + off));
-        }
-      }
+      for (int kh = 0; kh < 2; ++kh) {
+        if (2 * kh > wave) continue;
+        float tv[8];
+        tprime(kh, tv);
+        bf8 th, tl;
+        split_bf8(f4{tv[0], tv[1], tv[2], tv[3]}, f4{tv[4], tv[5], tv[6], tv[7]}, th, tl);
+        __builtin_nontemporal_store(th, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2) * kFrag));
+        if (p.tp_lo) __builtin_nontemporal_store(tl, reinterpret_cast<bf8*>(wt + ((wave * 2 + kh) * 2 + 1) * kFrag));
       }
     }
     __syncthreads();  // the next group rewrites G, beta and the LDS union
@@ -1008,32 +867,20 @@ struct ScanMail {
 
 // A state wave's share of one chunk's operands, in the register order of the MFMAs that
 // read them. The two state waves of a workgroup need all of the chunk's shared operands;
-// each loads half and passes it to the other through LDS (ScanShared).
-// GDN_PREFILL_FAST: W and K^T (state wave i: W position tiles 2i, 2i + 1 and K^T dk tiles
-// 4i .. 4i + 3), with the wave's own U columns and the gates.
-struct StateOpsFast {
-  bf8 w[2][4];   // W   [own pos tile][dk block]   (A of W S)
-  bf8 kt[4][2];  // K^T [own dk tile][pos block]   (A of K^T V'')
-  h4 u[4];       // U [pos tile]: positions 16 pt + 4 lg + e, column fr of the wave's tile,
-                 // fp16 scaled by 1 / us[pt]
-  f4 us;         // the chunk's fp16 U scale factors, one per position tile
-  float2 g;      // (e^G, e^(G63-G)) at position `lane`
-};
-// GDN_PREFILL_ACCURATE: K (position tiles 2i, 2i + 1), T' (state wave 0 the hi parts of its
-// six nonzero blocks, wave 1 the lo parts) and K^T (dk tiles 4i .. 4i + 3), with the wave's
-// own V columns and the gates.
+// each loads half and passes it to the other through LDS (ScanShared): K (position tiles
+// 2i, 2i + 1), T' (state wave 0 the hi parts of its six nonzero blocks, wave 1 the lo
+// parts, which only the accurate form loads) and K^T (dk tiles 4i .. 4i + 3), with the
+// wave's own V columns and the gates.
 constexpr int kTpBlocks = 6;  // T' blocks (pos tile, pos block): (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
 __device__ __forceinline__ constexpr int tp_tile(int bi) { return bi < 2 ? bi : 2 + (bi - 2) / 2; }
 __device__ __forceinline__ constexpr int tp_kb(int bi) { return bi < 2 ? 0 : (bi - 2) % 2; }
-struct StateOpsKtv {
+struct StateOps {
   bf8 kk[2][4];          // K   [own pos tile][dk block]  (A of K S)
   bf8 tp[kTpBlocks];     // T'  [block], hi (wave 0) or lo (wave 1)  (A of T' X)
   bf8 kt[4][2];          // K^T [own dk tile][pos block]  (A of K^T V'')
   bf8 v[2];              // V   [pos block] of the wave's tile (B order: two accumulator tiles)
   float2 g;              // (e^G, e^(G63-G)) at position `lane`
 };
-template <bool PRECISE>
-using StateOps = typename std::conditional<PRECISE, StateOpsKtv, StateOpsFast>::type;
 
 // Output wave `half` makes position tiles half and 3 - half of each chunk: M is lower
 // triangular, so the first tile (rows < 32) has one nonzero 32-column block and the second
@@ -1043,10 +890,10 @@ __device__ __forceinline__ constexpr int out_tile(int half, int i) { return i ==
 // An output wave's operands of one chunk: its two position tiles out_tile(half, 0 / 1).
 struct OutOps {
   bf8 q[2][4];     // Q [pos tile][dk block]          (A of Q S)
-  bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V'); [0][1] is zero, never loaded
-                   // (GDN_PREFILL_FAST; the accurate form builds M from K and Q)
+  bf8 m[2][2][2];  // M [pos tile][pos block][hi, lo] (A of M V', built from K and Q; lo in
+                   // the accurate form only); [0][1] is zero
   float eg;        // e^G at position `lane`
-  float gv;        // G at position `lane` (GDN_PREFILL_ACCURATE)
+  float gv;        // G at position `lane`
   unsigned touch[2];  // the cache-line touches issued with this set (see touch_lines)
 };
 
@@ -1055,69 +902,51 @@ struct OutOps {
 // same time, so a line fetched on demand costs all of them the full memory latency. The
 // output waves therefore touch (one dword per 128-byte line) the lines of the chunk four
 // ahead: the v-head's four workgroups split the four 16 KB matrices between them (group
-// `grp` takes one: W, M, Q, K^T in the fast form, K, T', Q, K^T in the accurate one), and
-// each workgroup touches its own U (or V) columns and the gate pairs.
-template <bool PRECISE>
+// `grp` takes one: K, T', Q, K^T), and each workgroup touches its own V columns and the gate
+// pairs.
 __device__ __forceinline__ void touch_lines(const PrefillParams& p, size_t gc, size_t hc, int grp, int jt, int half,
                                             int lane, unsigned (&t)[2]) {
   const unsigned* base;
   if (half == 0) {
     const int r = grp & 3;
-    const __bf16* m = r == 0 ? (PRECISE ? p.ws_kk + gc * kChunkElems : p.ws_w + hc * kChunkElems)
-                    : r == 1 ? (PRECISE ? p.ws_tp : p.ws_m) + hc * kChunkElems
+    const __bf16* m = r == 0 ? p.ws_kk + gc * kChunkElems
+                    : r == 1 ? p.ws_tp + hc * kChunkElems
                     : r == 2 ? p.ws_q + gc * kChunkElems
                              : p.ws_kt + gc * kChunkElems;
     base = reinterpret_cast<const unsigned*>(m);
     t[0] = base[lane * 32];
     t[1] = base[(64 + lane) * 32];
   } else {
-    if constexpr (PRECISE) {
-      // this workgroup's two dv tiles of V (4 KB, 32 lines) and the (G, beta) pairs
-      const unsigned* vb = reinterpret_cast<const unsigned*>(p.ws_vf + hc * kChunkElems + jt * 2 * kFrag);
-      const unsigned* gb = reinterpret_cast<const unsigned*>(p.ws_gb + hc * kGStride);
-      t[0] = lane < 32 ? vb[lane * 32] : gb[(lane & 3) * 32];
-    } else {
-      // this workgroup's two dv tiles of U: 4 KB, 32 lines
-      base = reinterpret_cast<const unsigned*>(p.ws_u + hc * kChunkElems + jt * 4 * 256);
-      t[0] = base[(lane & 31) * 32];
-    }
+    // this workgroup's two dv tiles of V (4 KB, 32 lines) and the (G, beta) pairs
+    const unsigned* vb = reinterpret_cast<const unsigned*>(p.ws_vf + hc * kChunkElems + jt * 2 * kFrag);
+    const unsigned* gb = reinterpret_cast<const unsigned*>(p.ws_gb + hc * kGStride);
+    t[0] = lane < 32 ? vb[lane * 32] : gb[(lane & 3) * 32];
     t[1] = reinterpret_cast<const unsigned*>(p.ws_g + hc * kGStride)[(lane & 3) * 32];
   }
 }
 
 // Operand loads for chunk c of the (batch, k-head) gc and (batch, v-head) hc: state wave
-// i's half of W with its tile jt's U and the gates (GDN_PREFILL_FAST), or its halves of K
-// and T' with its tile's V and the gates (GDN_PREFILL_ACCURATE); then its half of K^T.
-__device__ __forceinline__ void load_front(const PrefillParams& p, size_t, size_t hc, int jt, int i, int lane,
-                                           StateOpsFast& op) {
-  const __bf16* w = p.ws_w + hc * kChunkElems + lane * 8;
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) op.w[r][ks] = *reinterpret_cast<const bf8*>(w + ((2 * i + r) * 4 + ks) * kFrag);
-  const _Float16* u = p.ws_u + hc * kChunkElems + jt * 4 * 256 + lane * 4;
-#pragma unroll
-  for (int pt = 0; pt < 4; ++pt) op.u[pt] = *reinterpret_cast<const h4*>(u + pt * 256);
-  op.us = *reinterpret_cast<const f4*>(p.ws_us + hc * 4);
-  op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
-}
+// i's halves of K and T' (the accurate form's lo half: wave 1) with its tile's V and the
+// gates; its half of K^T follows separately.
+template <bool SPLIT>
 __device__ __forceinline__ void load_front(const PrefillParams& p, size_t gc, size_t hc, int jt, int i, int lane,
-                                           StateOpsKtv& op) {
+                                           StateOps& op) {
   const __bf16* kk = p.ws_kk + gc * kChunkElems + lane * 8;
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.kk[r][ks] = *reinterpret_cast<const bf8*>(kk + ((2 * i + r) * 4 + ks) * kFrag);
-  const __bf16* tp = p.ws_tp + hc * kChunkElems + lane * 8;
+  if (SPLIT || i == 0) {
+    const __bf16* tp = p.ws_tp + hc * kChunkElems + lane * 8;
 #pragma unroll
-  for (int bi = 0; bi < kTpBlocks; ++bi)
-    op.tp[bi] = *reinterpret_cast<const bf8*>(tp + ((tp_tile(bi) * 2 + tp_kb(bi)) * 2 + i) * kFrag);
+    for (int bi = 0; bi < kTpBlocks; ++bi)
+      op.tp[bi] = *reinterpret_cast<const bf8*>(tp + ((tp_tile(bi) * 2 + tp_kb(bi)) * 2 + i) * kFrag);
+  }
   const __bf16* v = p.ws_vf + hc * kChunkElems + lane * 8;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) op.v[kb] = *reinterpret_cast<const bf8*>(v + (2 * jt + kb) * kFrag);
   op.g = reinterpret_cast<const float2*>(p.ws_g + hc * kGStride)[lane];
 }
-template <bool PRECISE>
 __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_t hc, int half, int lane, OutOps& op) {
   const __bf16* q = p.ws_q + gc * kChunkElems + lane * 8;
 #pragma unroll
@@ -1125,17 +954,9 @@ __device__ __forceinline__ void load_qm(const PrefillParams& p, size_t gc, size_
     const int pt = out_tile(half, i);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) op.q[i][ks] = *reinterpret_cast<const bf8*>(q + (pt * 4 + ks) * kFrag);
-    if constexpr (!PRECISE) {
-      const __bf16* m = p.ws_m + hc * kChunkElems + lane * 8;
-#pragma unroll
-      for (int ks = 0; ks <= i; ++ks)
-#pragma unroll
-        for (int hl = 0; hl < 2; ++hl)
-          op.m[i][ks][hl] = *reinterpret_cast<const bf8*>(m + ((pt * 2 + ks) * 2 + hl) * kFrag);
-    }
   }
   op.eg = p.ws_g[hc * kGStride + 2 * lane];
-  if constexpr (PRECISE) op.gv = p.ws_gb[hc * kGStride + 2 * lane];
+  op.gv = p.ws_gb[hc * kGStride + 2 * lane];
 }
 
 
@@ -1151,33 +972,16 @@ __device__ __forceinline__ void pair_rows(const float2* row, int pt, int lane, f
 
 // The operand halves the two state waves exchange, per lane, in two slots: slot c % 2
 // holds chunk c's, written during chunk c - 1.
-struct ScanSharedFast {
-  bf8 w[2][2][2][4][64];   // [slot][wave][own pos tile][dk block][lane]
-  bf8 kt[2][2][4][2][64];  // [slot][wave][own dk tile][pos block][lane]
-  float2 gt[4][64];        // [wave][position]: the wave's per-position gate pair of its chunk
-};
-struct ScanSharedKtv {
+struct ScanShared {
   bf8 kk[3][2][2][4][64];          // [chunk % 3][wave][own pos tile][dk block][lane] (three
                                    // slots: the output waves read chunk c's K during c + 1)
   bf8 kt[2][2][4][2][64];          // [slot][wave][own dk tile][pos block][lane]
   bf8 tp[2][2][kTpBlocks][64];     // [slot][wave (0: hi, 1: lo)][block][lane]
   float2 gt[4][64];                // [wave][position]: the wave's per-position gate pair
 };
-template <bool PRECISE>
-using ScanShared = typename std::conditional<PRECISE, ScanSharedKtv, ScanSharedFast>::type;
 
-__device__ __forceinline__ void share_out(ScanSharedFast& sh, int slot, int, int i, int lane, const StateOpsFast& nx) {
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sh.w[slot][i][r][ks][lane] = nx.w[r][ks];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) sh.kt[slot][i][r][ks][lane] = nx.kt[r][ks];
-}
-__device__ __forceinline__ void share_out(ScanSharedKtv& sh, int slot, int kslot, int i, int lane,
-                                          const StateOpsKtv& nx) {
+template <bool SPLIT>
+__device__ __forceinline__ void share_out(ScanShared& sh, int slot, int kslot, int i, int lane, const StateOps& nx) {
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -1186,8 +990,10 @@ __device__ __forceinline__ void share_out(ScanSharedKtv& sh, int slot, int kslot
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) sh.kt[slot][i][r][ks][lane] = nx.kt[r][ks];
+  if (SPLIT || i == 0) {
 #pragma unroll
-  for (int bi = 0; bi < kTpBlocks; ++bi) sh.tp[slot][i][bi][lane] = nx.tp[bi];
+    for (int bi = 0; bi < kTpBlocks; ++bi) sh.tp[slot][i][bi][lane] = nx.tp[bi];
+  }
 }
 
 // S as the bf16 B fragments of the four dk blocks (and, with `split`, their remainders);
@@ -1265,70 +1071,18 @@ __device__ __forceinline__ void state_update(const PrefillParams& p, f4 (&S)[kD 
 // slot i. `op` holds this wave's share of chunk c's operands and is reloaded with chunk
 // cn's right after their last product; `nx` (chunk c + 1's share, loaded a chunk ago) is
 // written to the exchange slot of chunk c + 1.
-// GDN_PREFILL_FAST: V' = U - W S with bf16 W and S.
-template <int NT, int i>
-__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedFast& sh,
-                                            f4 (&S)[kD / 16], StateOpsFast& op, const StateOpsFast& nx, size_t gcn,
-                                            size_t hcn, int jt, int slot, int, int lane) {
-  constexpr int o = i ^ 1;
-  // the other wave's halves of this chunk's W and K^T
-  bf8 wo[2][4], kto[4][2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) wo[r][ks] = sh.w[slot][o][r][ks][lane];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
-  bf8 sb[kD / 32], sbl[kD / 32];
-  pack_state<NT, false>(mb, i, lane, S, sb, sbl);
-  sh.gt[i][lane] = op.g;
-  f4 egr[4];
-#pragma unroll
-  for (int pt = 0; pt < 4; ++pt) {
-    f4 unused;
-    pair_rows(sh.gt[i], pt, lane, unused, egr[pt]);
-  }
-  const float gam = sh.gt[i][63].x;
-  // P = W S for the four position tiles (2i, 2i + 1 this wave's, from registers; the others
-  // came through LDS), the four accumulators interleaved so that no MFMA waits for the one
-  // before it
-  f4 P[4];
-#pragma unroll
-  for (int pt = 0; pt < 4; ++pt) P[pt] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < kD / 32; ++ks) {
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-      const bool own = (pt >> 1) == i;  // (compile-time after unrolling)
-      P[pt] = mfma(own ? op.w[pt & 1][ks] : wo[pt & 1][ks], sb[ks], P[pt]);
-    }
-  }
-  f4 vpr[4];
-#pragma unroll
-  for (int pt = 0; pt < 4; ++pt) {
-    vpr[pt] = __builtin_convertvector(op.u[pt], f4) * op.us[pt] - P[pt];
-    mb.vpr[i][pt][lane] = vpr[pt];
-  }
-  // 16 MFMAs and 22 loads (W half 8, U 4, its scales, the gates, K^T half 8)
-  state_update<i, false, 22>(p, S, vpr, egr, gam, kto, op, gcn, lane,
-                             [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
-  share_out(sh, slot ^ 1, 0, i, lane, nx);  // (the slot was last read in chunk c - 1)
-  __syncthreads();  // mail[c % 2] and chunk c + 1's shares are complete; the output waves
-                    // have read mail[(c + 1) % 2]
-}
-
-// GDN_PREFILL_ACCURATE: V' = T' (V - e^G . (K S)) at fp32 accuracy: K is exact in bf16 and
-// S is split into bf16 hi + lo (K S_hi + K S_lo), X = V - e^G . K S is formed in fp32 and
-// split into hi + lo, and T' X = T'_hi X_hi + T'_lo X_hi + T'_hi X_lo (the dropped
-// T'_lo X_lo is 2^-16 relative). With U = T' V and W = T' diag(e^G) K this is U - W S.
-template <int NT, int i>
-__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanSharedKtv& sh,
-                                            f4 (&S)[kD / 16], StateOpsKtv& op, const StateOpsKtv& nx, size_t gcn,
+// V' = T' (V - e^G . (K S)) (with U = T' V and W = T' diag(e^G) K this is U - W S):
+// X = V - e^G . K S is formed in fp32 and split into bf16 hi + lo. SPLIT
+// (GDN_PREFILL_ACCURATE), at fp32 accuracy: K is exact in bf16 and S is split too
+// (K S_hi + K S_lo), and T' X = T'_hi X_hi + T'_lo X_hi + T'_hi X_lo (the dropped T'_lo X_lo
+// is 2^-16 relative). Otherwise (GDN_PREFILL_FAST) K S_hi and T'_hi X_hi + T'_hi X_lo.
+template <int NT, int i, bool SPLIT>
+__device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>& mb, ScanShared& sh,
+                                            f4 (&S)[kD / 16], StateOps& op, const StateOps& nx, size_t gcn,
                                             size_t hcn, int jt, int slot, int kslot, int lane) {
   constexpr int o = i ^ 1;
-  // the other wave's halves of this chunk's K and K^T, and its part of T'
+  // the other wave's halves of this chunk's K and K^T, and its part of T' (wave 1 takes
+  // wave 0's hi parts; wave 0 takes the lo parts of the accurate form)
   bf8 kko[2][4], kto[4][2], tpo[kTpBlocks];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
@@ -1338,16 +1092,18 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) kto[r][ks] = sh.kt[slot][o][r][ks][lane];
+  if (SPLIT || i == 1) {
 #pragma unroll
-  for (int bi = 0; bi < kTpBlocks; ++bi) tpo[bi] = sh.tp[slot][o][bi][lane];
+    for (int bi = 0; bi < kTpBlocks; ++bi) tpo[bi] = sh.tp[slot][o][bi][lane];
+  }
   bf8 sb[kD / 32], sbl[kD / 32];
-  pack_state<NT, true>(mb, i, lane, S, sb, sbl);
+  pack_state<NT, SPLIT>(mb, i, lane, S, sb, sbl);
   sh.gt[i][lane] = op.g;
   f4 eg[4], egr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) pair_rows(sh.gt[i], pt, lane, eg[pt], egr[pt]);
   const float gam = sh.gt[i][63].x;
-  // P = K S_hi + K S_lo for the four position tiles, the accumulators interleaved
+  // P = K S_hi (+ K S_lo) for the four position tiles, the accumulators interleaved
   f4 P[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) P[pt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1358,10 +1114,12 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
       const bool own = (pt >> 1) == i;
       P[pt] = mfma(own ? op.kk[pt & 1][ks] : kko[pt & 1][ks], sb[ks], P[pt]);
     }
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-      const bool own = (pt >> 1) == i;
-      P[pt] = mfma(own ? op.kk[pt & 1][ks] : kko[pt & 1][ks], sbl[ks], P[pt]);
+      for (int pt = 0; pt < 4; ++pt) {
+        const bool own = (pt >> 1) == i;
+        P[pt] = mfma(own ? op.kk[pt & 1][ks] : kko[pt & 1][ks], sbl[ks], P[pt]);
+      }
     }
   }
   // X = V - e^G . K S as two B fragments (position blocks) split into bf16 hi + lo
@@ -1373,14 +1131,15 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
     const f4 x0 = v0 - eg[2 * kb] * P[2 * kb], x1 = v1 - eg[2 * kb + 1] * P[2 * kb + 1];
     split_bf8(x0, x1, xb[kb], xbl[kb]);
   }
-  // V' = T' X over the six nonzero blocks, three products each, in an order that keeps
-  // consecutive MFMAs on different accumulators
+  // V' = T' X over the six nonzero blocks, three products each (two without T'_lo), in an
+  // order that keeps consecutive MFMAs on different accumulators
   f4 vpr[4];
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) vpr[pt] = f4{0.f, 0.f, 0.f, 0.f};
   constexpr int kOrder[kTpBlocks] = {0, 2, 4, 1, 3, 5};
 #pragma unroll
   for (int term = 0; term < 3; ++term) {
+    if (!SPLIT && term == 1) continue;
 #pragma unroll
     for (int j = 0; j < kTpBlocks; ++j) {
       const int bi = kOrder[j], pt = tp_tile(bi), kb = tp_kb(bi);
@@ -1391,10 +1150,11 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
   }
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) mb.vpr[i][pt][lane] = vpr[pt];
-  // 32 MFMAs and 25 loads (K half 8, T' part 6, V 2, the gates, K^T half 8)
-  state_update<i, true, 25>(p, S, vpr, egr, gam, kto, op, gcn, lane,
-                            [&] { load_front(p, gcn, hcn, jt, i, lane, op); });
-  share_out(sh, slot ^ 1, kslot == 2 ? 0 : kslot + 1, i, lane, nx);
+  // 32 (16) MFMAs and 25 loads (K half 8, T' part 6 -- none for the fast form's wave 1 --,
+  // V 2, the gates, K^T half 8)
+  state_update<i, SPLIT, (SPLIT || i == 0) ? 25 : 19>(p, S, vpr, egr, gam, kto, op, gcn, lane,
+                                                      [&] { load_front<SPLIT>(p, gcn, hcn, jt, i, lane, op); });
+  share_out<SPLIT>(sh, slot ^ 1, kslot == 2 ? 0 : kslot + 1, i, lane, nx);
   __syncthreads();
 }
 
@@ -1403,8 +1163,8 @@ __device__ __forceinline__ void state_chunk(const PrefillParams& p, ScanMail<NT>
 // in the order the loop reissues them so that the loop is entered with the same loads in
 // flight as at its back edge. Barriers: one after chunk 0's shares are exchanged, one per
 // chunk, one at the end, as the output waves.
-template <int NT, int i, bool PRECISE>
-__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared<PRECISE>& sh,
+template <int NT, int i, bool SPLIT>
+__device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail<NT> (&mail)[2], ScanShared& sh,
                                                 int b, int h, int g, int jt, int lane) {
   const int fr = lane & 15, lg = lane >> 4;
   const size_t gc0 = ((size_t)b * p.Hk + g) * p.nC;
@@ -1422,8 +1182,8 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
   }
 
   const int last = p.nC - 1;
-  StateOps<PRECISE> A, B;
-  auto load_kt = [&](size_t gc, StateOps<PRECISE>& op) {
+  StateOps A, B;
+  auto load_kt = [&](size_t gc, StateOps& op) {
     const __bf16* kt = p.ws_kt + gc * kChunkElems + lane * 8;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -1431,24 +1191,24 @@ __device__ __forceinline__ void scan_state_wave(const PrefillParams& p, ScanMail
       for (int ks = 0; ks < 2; ++ks) op.kt[r][ks] = *reinterpret_cast<const bf8*>(kt + ((4 * i + r) * 2 + ks) * kFrag);
   };
   __builtin_amdgcn_sched_barrier(0);
-  load_front(p, gc0, hc0, jt, i, lane, A);
+  load_front<SPLIT>(p, gc0, hc0, jt, i, lane, A);
   __builtin_amdgcn_sched_barrier(0);
   load_kt(gc0, A);
   __builtin_amdgcn_sched_barrier(0);
-  load_front(p, gc0 + min(1, last), hc0 + min(1, last), jt, i, lane, B);
+  load_front<SPLIT>(p, gc0 + min(1, last), hc0 + min(1, last), jt, i, lane, B);
   __builtin_amdgcn_sched_barrier(0);
   load_kt(gc0 + min(1, last), B);
   __builtin_amdgcn_sched_barrier(0);
-  share_out(sh, 0, 0, i, lane, A);
+  share_out<SPLIT>(sh, 0, 0, i, lane, A);
   __syncthreads();
   int c = 0, kslot = 0;  // kslot = c % 3 (the accurate form's three K slots)
   for (; c + 2 <= p.nC; c += 2) {
-    state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, kslot, lane);
+    state_chunk<NT, i, SPLIT>(p, mail[0], sh, S, A, B, gc0 + min(c + 2, last), hc0 + min(c + 2, last), jt, 0, kslot, lane);
     kslot = kslot == 2 ? 0 : kslot + 1;
-    state_chunk<NT, i>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, kslot, lane);
+    state_chunk<NT, i, SPLIT>(p, mail[1], sh, S, B, A, gc0 + min(c + 3, last), hc0 + min(c + 3, last), jt, 1, kslot, lane);
     kslot = kslot == 2 ? 0 : kslot + 1;
   }
-  if (c < p.nC) state_chunk<NT, i>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, kslot, lane);
+  if (c < p.nC) state_chunk<NT, i, SPLIT>(p, mail[0], sh, S, A, B, gc0 + last, hc0 + last, jt, 0, kslot, lane);
   __syncthreads();
 
   if (p.state_out) {
@@ -1484,41 +1244,40 @@ __device__ __forceinline__ void store_tile(const PrefillParams& p, const OutTile
 }
 
 // Output wave `half` (position tiles out_tile(half, 0 / 1) of each chunk), one chunk behind
-// the state wave (chunk c after its barrier c): y = e^G . (Q S) + M V' (V' split into bf16
-// hi + lo) from mail[c % 2] into the tile, after the previous chunk's outputs have been
+// the state wave (chunk c after its barrier c): y = e^G . (Q S) + M V' (with SPLIT, M and V'
+// split into bf16 hi + lo) from mail[c % 2] into the tile, after the previous chunk's outputs have been
 // stored from it (the stores are issued before the reloads, so a wait for a reloaded
 // operand never has to count stores that may not have been issued). `op` is reloaded with
 // chunk cn's operands and touches the lines of chunk c + 4 (gc4, hc4). The touches issued
 // with this set two chunks ago have long arrived: they are folded into `tacc` only so that
 // they stay live.
-template <int NT, bool OBF16, bool PRECISE>
-__device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb,
-                                             ScanShared<PRECISE>& sh,
+template <int NT, bool OBF16, bool SPLIT>
+__device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanMail<NT>& mb, ScanShared& sh,
                                              OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                              OutOps& op, size_t gcn, size_t hcn, size_t gc4, size_t hc4, int b, int h,
                                              int jt, int half, int c, int kslot, int lane, unsigned& tacc) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   const int fr = lane & 15, lg = lane >> 4;
   if (c > 0) store_tile<NT, OT>(p, tile, b, h, jt, half, c - 1, lane);
-  // Accurate form: every wave starts its step with LDS reads (the state waves their partner's
-  // operand halves, on the chain; these waves K and the mail, ~28 KB each), and the state
-  // waves are the critical ones, so these start ~190 cycles later and leave the LDS to the
-  // exchange first (T = 4096: scan 120 -> 117 us in an A/B run; a longer pause, ~380 cycles,
-  // gained nothing). The fast form's output waves are as busy as its state waves: no pause.
-  if constexpr (PRECISE) __builtin_amdgcn_s_sleep(3);
+  // Every wave starts its step with LDS reads (the state waves their partner's operand
+  // halves, on the chain; these waves K and the mail, ~28 KB each), and the state waves are
+  // the critical ones, so these start ~190 cycles later and leave the LDS to the exchange
+  // first (accurate form, T = 4096: scan 120 -> 117 us in an A/B run; a longer pause, ~380
+  // cycles, gained nothing).
+  __builtin_amdgcn_s_sleep(3);
   tacc ^= op.touch[0] ^ op.touch[1];
   // (e^G, G) per position through this wave's gate row
   float2* grow = sh.gt[NT + half];
-  grow[lane] = make_float2(op.eg, PRECISE ? op.gv : 0.0f);
+  grow[lane] = make_float2(op.eg, op.gv);
   f4 eg[2], gr[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) pair_rows(grow, out_tile(half, i), lane, eg[i], gr[i]);
-  if constexpr (PRECISE) {
+  {
     // M = e^(G_i - G_j) (Q K^T)_ij (j <= i) of this wave's position tiles, from the chunk's K
-    // (the state waves' K slot, still unchanged) and Q, as the intra kernel makes it for the
-    // fast form: tile (j tile, i tile) of K Q^T as an accumulator (rows j), decayed, split
-    // into bf16 hi + lo; two stacked j tiles are the A fragment of M's rows i over one
-    // 32-position block of j in the interleaved k order.
+    // (the state waves' K slot, still unchanged) and Q: tile (j tile, i tile) of K Q^T as an
+    // accumulator (rows j), decayed (and, with SPLIT, split into bf16 hi + lo); two stacked j
+    // tiles are the A fragment of M's rows i over one 32-position block of j in the
+    // interleaved k order.
     // (half is a compile-time constant here: the tiles below the diagonal are known, and
     // their MFMAs, all K fragments read first, interleave)
     constexpr int kJt = 4;
@@ -1566,7 +1325,8 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
             mt[hh][e] = jt2 <= pt && j <= 16 * pt + fr ? fast_exp(gi - gj[jt2][e]) * acc[i][jt2][e] : 0.0f;
           }
         }
-        split_bf8(mt[0], mt[1], op.m[i][kb][0], op.m[i][kb][1]);
+        if constexpr (SPLIT) split_bf8(mt[0], mt[1], op.m[i][kb][0], op.m[i][kb][1]);
+        else op.m[i][kb][0] = stack_bf8(mt[0], mt[1]);
       }
     }
   }
@@ -1581,7 +1341,8 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
     bf8 vh[2], vl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      split_bf8(vpr[2 * ks], vpr[2 * ks + 1], vh[ks], vl[ks]);
+      if constexpr (SPLIT) split_bf8(vpr[2 * ks], vpr[2 * ks + 1], vh[ks], vl[ks]);
+      else vh[ks] = stack_bf8(vpr[2 * ks], vpr[2 * ks + 1]);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -1592,8 +1353,10 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
 #pragma unroll
       for (int ks = 0; ks <= i; ++ks) {  // (M's block (tile 0 or 1, columns 32..63) is zero)
         acc = mfma(op.m[i][ks][0], vh[ks], acc);
-        acc = mfma(op.m[i][ks][1], vh[ks], acc);
-        acc = mfma(op.m[i][ks][0], vl[ks], acc);
+        if constexpr (SPLIT) {
+          acc = mfma(op.m[i][ks][1], vh[ks], acc);
+          acc = mfma(op.m[i][ks][0], vl[ks], acc);
+        }
       }
       const f4 y = eg[i] * qs + acc;
 #pragma unroll
@@ -1601,15 +1364,14 @@ __device__ __forceinline__ void output_chunk(const PrefillParams& p, const ScanM
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  load_qm<PRECISE>(p, gcn, hcn, half, lane, op);
-  touch_lines<PRECISE>(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
+  load_qm(p, gcn, hcn, half, lane, op);
+  touch_lines(p, gc4, hc4, jt / NT, jt, half, lane, op.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // done with mail[c % 2]; mail[(c + 1) % 2] is complete
 }
 
-template <int NT, bool OBF16, bool PRECISE, int HALF>
-__device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2],
-                                                 ScanShared<PRECISE>& sh,
+template <int NT, bool OBF16, bool SPLIT, int HALF>
+__device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const ScanMail<NT> (&mail)[2], ScanShared& sh,
                                                  OutTile<NT, typename std::conditional<OBF16, __bf16, float>::type>& tile,
                                                  int b, int h, int g, int jt, int lane) {
   constexpr int half = HALF;
@@ -1621,25 +1383,25 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
   unsigned tacc = 0;
   OutOps A, B;
   __builtin_amdgcn_sched_barrier(0);
-  load_qm<PRECISE>(p, gc0, hc0, half, lane, A);
-  touch_lines<PRECISE>(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
+  load_qm(p, gc0, hc0, half, lane, A);
+  touch_lines(p, gc0 + min(2, last), hc0 + min(2, last), grp, jt, half, lane, A.touch);
   __builtin_amdgcn_sched_barrier(0);
-  load_qm<PRECISE>(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
-  touch_lines<PRECISE>(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
+  load_qm(p, gc0 + min(1, last), hc0 + min(1, last), half, lane, B);
+  touch_lines(p, gc0 + min(3, last), hc0 + min(3, last), grp, jt, half, lane, B.touch);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // the state waves' exchange of chunk 0's shares
   __syncthreads();  // chunk 0's mail
   int c = 0, kslot = 0;  // kslot = c % 3
   for (; c + 2 <= p.nC; c += 2) {
-    output_chunk<NT, OBF16, PRECISE>(p, mail[0], sh, tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
+    output_chunk<NT, OBF16, SPLIT>(p, mail[0], sh, tile, A, gc0 + min(c + 2, last), hc0 + min(c + 2, last),
                             gc0 + min(c + 4, last), hc0 + min(c + 4, last), b, h, jt, half, c, kslot, lane, tacc);
     kslot = kslot == 2 ? 0 : kslot + 1;
-    output_chunk<NT, OBF16, PRECISE>(p, mail[1], sh, tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
+    output_chunk<NT, OBF16, SPLIT>(p, mail[1], sh, tile, B, gc0 + min(c + 3, last), hc0 + min(c + 3, last),
                             gc0 + min(c + 5, last), hc0 + min(c + 5, last), b, h, jt, half, c + 1, kslot, lane, tacc);
     kslot = kslot == 2 ? 0 : kslot + 1;
   }
   if (c < p.nC)
-    output_chunk<NT, OBF16, PRECISE>(p, mail[0], sh, tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half,
+    output_chunk<NT, OBF16, SPLIT>(p, mail[0], sh, tile, A, gc0 + last, hc0 + last, gc0 + last, hc0 + last, b, h, jt, half,
                             c, kslot, lane, tacc);
   store_tile<NT, OT>(p, tile, b, h, jt, half, p.nC - 1, lane);
   // (never true: T >= 1; it keeps the touches from being dropped as unused)
@@ -1649,13 +1411,14 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
 // Workgroup = (batch, v-head, NT 16-column Dv tiles): waves 0 .. NT-1 carry the state of
 // one tile each, waves NT and NT + 1 make the outputs of position tiles {0, 3} and {1, 2}
 // of each chunk for all NT tiles. All waves pass nC + 2 barriers.
-template <int NT, bool OBF16, bool PRECISE>
+// SPLIT: GDN_PREFILL_ACCURATE's hi + lo operands.
+template <int NT, bool OBF16, bool SPLIT>
 __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
   static_assert(NT == 2, "two state waves exchange halves of W and K^T");
   __shared__ __attribute__((aligned(16))) ScanMail<NT> mail[2];
   __shared__ __attribute__((aligned(16))) OutTile<NT, OT> tiles[2];
-  __shared__ __attribute__((aligned(16))) ScanShared<PRECISE> shared_ops;
+  __shared__ __attribute__((aligned(16))) ScanShared shared_ops;
   // Workgroups are dispatched to the 8 XCDs round robin (bid % 8); renumber them so that
   // each XCD gets a contiguous range of (batch, v-head, tiles) -- whole v-heads, and whole
   // k-head groups when the count divides -- and the chunk operands those waves share are
@@ -1671,25 +1434,25 @@ __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillPara
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave == 0) {
-    scan_state_wave<NT, 0, PRECISE>(p, mail, shared_ops, b, h, g, jt, lane);
+    scan_state_wave<NT, 0, SPLIT>(p, mail, shared_ops, b, h, g, jt, lane);
   } else if (wave == 1) {
-    scan_state_wave<NT, 1, PRECISE>(p, mail, shared_ops, b, h, g, jt + 1, lane);
+    scan_state_wave<NT, 1, SPLIT>(p, mail, shared_ops, b, h, g, jt + 1, lane);
   } else if (wave == NT) {
-    scan_output_wave<NT, OBF16, PRECISE, 0>(p, mail, shared_ops, tiles[0], b, h, g, jt, lane);
+    scan_output_wave<NT, OBF16, SPLIT, 0>(p, mail, shared_ops, tiles[0], b, h, g, jt, lane);
   } else {
-    scan_output_wave<NT, OBF16, PRECISE, 1>(p, mail, shared_ops, tiles[1], b, h, g, jt, lane);
+    scan_output_wave<NT, OBF16, SPLIT, 1>(p, mail, shared_ops, tiles[1], b, h, g, jt, lane);
   }
 }
 
 struct WorkspaceLayout {
-  size_t q, kt, g, vf, gb, m, w, u, us, kk, tp, total;
+  size_t q, kt, g, vf, gb, kk, tp, total;
 };
 
 // The conv front end writes Q, K and K^T straight into their fragment planes and v into vf
-// (the qkv front end fills vf from the caller's v; its Q and K^T come from the intra kernel,
-// and in the accurate form its K too).
-// precise (GDN_PREFILL_ACCURATE): K and T' per chunk; otherwise M, W, U (fp16) and U's scales.
-WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool precise) {
+// (the qkv front end fills vf from the caller's v; its Q, K and K^T come from the intra
+// kernel). Per chunk also T' (hi + lo; the fast form leaves the lo blocks unused). The
+// same layout serves both precisions and both front ends.
+WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv) {
   const size_t nC = (size_t)(T + kC - 1) / kC;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t qk = al((size_t)B * Hk * nC * kChunkElems * 2);
@@ -1701,26 +1464,16 @@ WorkspaceLayout workspace_layout(int B, int T, int Hk, int Hv, bool conv, bool p
   L.g = L.kt + qk;
   L.vf = L.g + gg;
   L.gb = L.vf + wm;
-  const size_t end = L.gb + gg;
-  if (precise) {
-    L.kk = end;
-    L.tp = L.kk + qk;
-    L.total = L.tp + wm;
-  } else {
-    L.kk = end;  // (the conv front end's K fragments; not used with q, k, v given)
-    L.m = L.kk + (conv ? qk : 0);
-    L.w = L.m + wm;
-    L.u = L.w + wm;
-    L.us = L.u + wm;
-    L.total = L.us + al((size_t)B * Hv * nC * 4 * 4);
-  }
+  L.kk = L.gb + gg;
+  L.tp = L.kk + qk;
+  L.total = L.tp + wm;
   return L;
 }
 
 }  // namespace
 
-size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv, bool conv, bool precise) {
-  return workspace_layout(B, T, Hk, Hv, conv, precise).total;
+size_t prefill_workspace_bytes(int B, int T, int Hk, int Hv) {
+  return workspace_layout(B, T, Hk, Hv).total;
 }
 
 hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipStream_t stream,
@@ -1735,6 +1488,7 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.nC = (p.T + kC - 1) / kC;
   p.gate_raw = a.gate_mode == GDN_GATES_RAW;
   p.qk_frag = a.frontend == GDN_FRONTEND_CONV;
+  p.tp_lo = a.prefill_precision == GDN_PREFILL_ACCURATE;
   p.o_bf16 = a.o_dtype == GDN_DTYPE_BF16;
   p.x = static_cast<const uint16_t*>(a.x);
   p.conv_w = static_cast<const uint16_t*>(a.conv_weight);
@@ -1753,20 +1507,12 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
   p.state_out = a.state_out;
   p.o = a.o;
   const bool conv = a.frontend == GDN_FRONTEND_CONV;
-  const bool precise = a.prefill_precision == GDN_PREFILL_ACCURATE;
-  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv, conv, precise);
+  const WorkspaceLayout L = workspace_layout(p.B, p.T, p.Hk, p.Hv);
   char* w = static_cast<char*>(workspace);
   p.ws_q = reinterpret_cast<__bf16*>(w + L.q);
   p.ws_kt = reinterpret_cast<__bf16*>(w + L.kt);
   p.ws_kk = reinterpret_cast<__bf16*>(w + L.kk);
-  if (precise) {
-    p.ws_tp = reinterpret_cast<__bf16*>(w + L.tp);
-  } else {
-    p.ws_m = reinterpret_cast<__bf16*>(w + L.m);
-    p.ws_w = reinterpret_cast<__bf16*>(w + L.w);
-    p.ws_u = reinterpret_cast<_Float16*>(w + L.u);
-    p.ws_us = reinterpret_cast<float*>(w + L.us);
-  }
+  p.ws_tp = reinterpret_cast<__bf16*>(w + L.tp);
   p.ws_gb = reinterpret_cast<float*>(w + L.gb);
   p.ws_g = reinterpret_cast<float*>(w + L.g);
   p.ws_vf = reinterpret_cast<__bf16*>(w + L.vf);
@@ -1793,21 +1539,19 @@ hipError_t launch_chunked_prefill(const gdn_layer_args& a, void* workspace, hipS
     hipLaunchKernelGGL(prefill_vfrag_kernel, gv, block, 0, stream, p);
   }
   mark(1);
-  // <one group of v-heads per k-head, precision, the front end's fragment planes>
-#define GDN_INTRA(og, pr, fr) hipLaunchKernelGGL((prefill_intra_kernel<og, pr, fr>), g1, block, 0, stream, p)
+  // <one group of v-heads per k-head, the front end's fragment planes>
+#define GDN_INTRA(og, fr) hipLaunchKernelGGL((prefill_intra_kernel<og, fr>), g1, block, 0, stream, p)
   const bool one = p.rep <= kGroup, fr = p.qk_frag != 0;
-  if (one && precise) { if (fr) GDN_INTRA(true, true, true); else GDN_INTRA(true, true, false); }
-  else if (one) { if (fr) GDN_INTRA(true, false, true); else GDN_INTRA(true, false, false); }
-  else if (precise) { if (fr) GDN_INTRA(false, true, true); else GDN_INTRA(false, true, false); }
-  else { if (fr) GDN_INTRA(false, false, true); else GDN_INTRA(false, false, false); }
+  if (one) { if (fr) GDN_INTRA(true, true); else GDN_INTRA(true, false); }
+  else { if (fr) GDN_INTRA(false, true); else GDN_INTRA(false, false); }
 #undef GDN_INTRA
   mark(2);
   const dim3 sb(64 * (kScanNt + 2));
   if (p.o_bf16) {
-    if (precise) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true, true>), g2, sb, 0, stream, p);
+    if (p.tp_lo) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true, true>), g2, sb, 0, stream, p);
     else hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, true, false>), g2, sb, 0, stream, p);
   } else {
-    if (precise) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false, true>), g2, sb, 0, stream, p);
+    if (p.tp_lo) hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false, true>), g2, sb, 0, stream, p);
     else hipLaunchKernelGGL((prefill_scan_kernel<kScanNt, false, false>), g2, sb, 0, stream, p);
   }
   mark(3);

@@ -332,8 +332,9 @@ def layer(*, x=None, q=None, k=None, v=None, a, b, A_log, dt_bias, state=None,
     products at fp32 accuracy (V' = T' (V - e^G K S) with S, X = V - e^G K S and T' split
     into bf16 hi + lo, V'' split in K^T V''), as the reference's fp32 Metal kernel for every
     window (cpp/src/model.cpp:619-624): the state ends within about 1e-5 (relative) of the
-    fp32 recurrence whatever the gates. PREFILL_FAST (bf16 operands, U as fp16) leaves it
-    about 2e-3 off in about 0.9 of the time. The recurrent kernel is within about 1e-7.
+    fp32 recurrence whatever the gates. PREFILL_FAST (bf16 operands, X alone split) leaves
+    it about 2e-3 to 4e-3 off in about 0.85 of the time. The recurrent kernel is within about
+    1e-7.
     Later decode steps continue from that state."""
     import torch
     src = x if x is not None else q

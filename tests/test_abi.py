@@ -120,11 +120,9 @@ def test_run_rejects_bad_arguments(gdn, kw, msg):
 
 
 def test_prefill_workspace_size_and_checks(gdn):
-    # per chunk: Q, K^T per k-head (bf16 64 x 128); V in fragment order (bf16) per v-head;
-    # two pairs of gate factors per position; 256-byte aligned pieces. The default
-    # (accurate) precision adds K per k-head and T' hi/lo per v-head; the fast one M hi/lo,
-    # W and U (fp16) per v-head, with one scale per 16-position tile, and with the conv front
-    # end (which writes Q, K and K^T straight into their planes) K per k-head.
+    # per chunk: Q, K and K^T per k-head (bf16 64 x 128); V in fragment order (bf16) and T'
+    # hi/lo per v-head; two pairs of gate factors per position; 256-byte aligned pieces. The
+    # same for both precisions (the fast one leaves the T' lo blocks unused) and front ends.
     n_qkv = gdn.prefill_workspace_size(1, 4096, conv=False)
     assert n_qkv == 3 * 16 * 64 * 8192 * 2 + 2 * 48 * 64 * 8192 * 2 + 2 * 48 * 64 * 128 * 4
     assert gdn.prefill_workspace_size(1, 4096) == n_qkv
@@ -134,13 +132,10 @@ def test_prefill_workspace_size_and_checks(gdn):
     assert gdn.prefill_workspace_size(2, 100) == (
         3 * al(2 * 16 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 128 * 4))
     assert gdn.PREFILL_ACCURATE == 0   # a zeroed gdn_layer_args gets the accurate form
-    assert gdn.prefill_workspace_size(1, 4096, precision=gdn.PREFILL_FAST) == (
-        gdn.prefill_workspace_size(1, 4096) + 2 * 48 * 64 * 8192 * 2 + 48 * 64 * 4 * 4)
-    assert gdn.prefill_workspace_size(1, 4096, conv=False, precision=gdn.PREFILL_FAST) == (
-        gdn.prefill_workspace_size(1, 4096, precision=gdn.PREFILL_FAST) - 16 * 64 * 8192 * 2)
-    assert gdn.prefill_workspace_size(2, 100, precision=gdn.PREFILL_FAST) == (
-        3 * al(2 * 16 * nc * 8192 * 2) + 4 * al(2 * 48 * nc * 8192 * 2) + 2 * al(2 * 48 * nc * 128 * 4)
-        + al(2 * 48 * nc * 4 * 4))
+    for conv in (True, False):
+        for T in (4096, 100, 1):
+            assert gdn.prefill_workspace_size(2, T, conv=conv, precision=gdn.PREFILL_FAST) == (
+                gdn.prefill_workspace_size(2, T, conv=conv))
     with pytest.raises(gdn.GdnError, match="prefill_precision"):
         gdn.prefill_workspace_size(1, 64, precision=2)
     L = gdn.lib()

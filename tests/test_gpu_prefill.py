@@ -5,8 +5,9 @@ token-by-token recurrence -- the reference's own criterion for its chunked form
 Tolerance: outputs within 1e-2 of the token-by-token result in the reference's measure
 max|a-b|/max|b| (the task statement's bound for chunked prefill); the bf16 output rounding
 (up to 2^-8 relative) is inside that budget. The final fp32 state, which later decode steps
-continue from, is held to 5e-3: about twice what the chunked form's bf16 products give at
-T = 4096 (2.1e-3), so that a loss of precision shows.
+continue from, is held to 8e-3 in the fast form: about twice the largest its bf16 state
+products give over these cases (4.0e-3), so that a loss of precision shows; the accurate
+form to 2e-5.
 """
 from __future__ import annotations
 
@@ -18,7 +19,7 @@ from _util import bf16_to_f32, log_case, to_dev, to_np
 pytestmark = pytest.mark.gpu
 
 PREFILL_TOL = 1e-2
-STATE_TOL = 5e-3
+STATE_TOL = 8e-3
 # GDN_PREFILL_ACCURATE (V' = T' (V - e^G K S) with S, X = V - e^G K S, T' and V'' split into
 # bf16 hi + lo: the state products at fp32 accuracy): measured 3e-6 to 8e-6 at every tested
 # length, carried state and gate regime
@@ -200,7 +201,7 @@ def test_prefill_1024_then_decode_16(O, gdn, dev, precision):
 
 # (T, carried state, state bound): windows of one, two and several chunks from a carried state
 # (B = 2, state ~N(0, 0.05)), where a short last chunk keeps the carried state's roundings in
-# W S unless S and W are split, and the benchmark shape
+# K S unless S is split, and the benchmark shape
 ACC_CASES = [(1, True, STATE_TOL_ACC), (65, True, STATE_TOL_ACC), (200, True, STATE_TOL_ACC),
              (4096, False, STATE_TOL_ACC)]
 
@@ -208,7 +209,7 @@ ACC_CASES = [(1, True, STATE_TOL_ACC), (65, True, STATE_TOL_ACC), (200, True, ST
 @pytest.mark.parametrize("T,carried,stol", ACC_CASES)
 def test_prefill_accurate(O, gdn, dev, T, carried, stol):
     """GDN_PREFILL_ACCURATE against the token-by-token recurrence: the final state within the
-    case's bound (U kept in fp32, V'' split into bf16 hi + lo for the state update), fp32
+    case's bound (S, X, T' and V'' split into bf16 hi + lo in the state products), fp32
     outputs within the chunked bound. Conv front end; with a carried state and conv state
     (B = 2, state ~N(0, 0.05)), or the benchmark shape at 4096."""
     log_case(f"prefill accurate T={T} carried={carried}")
@@ -224,8 +225,8 @@ def test_prefill_accurate(O, gdn, dev, T, carried, stol):
 def test_prefill_accurate_slow_gates(O, gdn, dev):
     """Gates near 1 (A_log = -4: alpha in 0.93 .. 0.9997), where a chunk does not forget its
     incoming state, so every bf16 rounding in the state products persists: GDN_PREFILL_FAST
-    ends about 2e-3 from the recurrence, GDN_PREFILL_ACCURATE (S and W split in W S, V''
-    split in K^T V'') within its fp32-level bound."""
+    ends about 3e-3 from the recurrence, GDN_PREFILL_ACCURATE (S split in K S, T' in T' X,
+    V'' in K^T V'') within its fp32-level bound."""
     log_case("prefill T=1024 slow gates, both precisions")
     inp = O.make_inputs(config=4, layer=21, B=1, L=1024, conv=True, conv_state=False, zero_state=True)
     inp.A_log = np.full_like(inp.A_log, -4.0)
