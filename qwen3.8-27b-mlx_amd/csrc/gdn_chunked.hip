@@ -1415,7 +1415,7 @@ __device__ __forceinline__ void scan_output_wave(const PrefillParams& p, const S
 template <int NT, bool OBF16, bool SPLIT>
 __global__ __launch_bounds__(64 * (NT + 2)) void prefill_scan_kernel(PrefillParams p) {
   typedef typename std::conditional<OBF16, __bf16, float>::type OT;
-  static_assert(NT == 2, "two state waves exchange halves of W and K^T");
+  static_assert(NT == 2, "two state waves exchange halves of K, K^T and T'");
   __shared__ __attribute__((aligned(16))) ScanMail<NT> mail[2];
   __shared__ __attribute__((aligned(16))) OutTile<NT, OT> tiles[2];
   __shared__ __attribute__((aligned(16))) ScanShared shared_ops;
